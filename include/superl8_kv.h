@@ -1,0 +1,142 @@
+/*
+ * superl8_kv.h -- C ABI of the MI355X (gfx950) quantized paged KV-cache path.
+ *
+ * Drop-in boundary for the kernels that jajmangold/superl8-serve reaches through
+ * the external `superl8` Python package.  Every entry point takes plain device
+ * pointers, element strides and sizes, runs on the HIP stream passed in
+ * `stream` (a hipStream_t; NULL = the default stream), never synchronizes,
+ * never allocates device memory, and returns an S8KV_* status code.  On a
+ * non-zero status `s8kv_last_error()` returns a message for the calling thread.
+ *
+ * Cache layout (superl8serve/engine/kv_cache.py:484-512), one layer per call:
+ *   k_cache, v_cache : int8    [num_blocks, num_kv_heads, block_size, head_dim]
+ *   k_scale, v_scale : float32 [num_blocks, num_kv_heads, block_size]
+ *   v_packed (k8v3)  : int32   [num_blocks, num_kv_heads, block_size, head_dim*3/32]
+ *   v_norm   (k8v3)  : float32 [num_blocks, num_kv_heads, block_size, head_dim/128]
+ *   v_codebook(k8v3) : float32 [8]
+ * A flat slot s addresses block s / block_size, offset s % block_size
+ * (kv_cache.py:570-585).  block_size must be a power of two >= 4 and
+ * head_dim one of 32, 64, 128, 256 (k8v3: 128 or 256, lloyd_block 128).
+ */
+#ifndef SUPERL8_KV_H_
+#define SUPERL8_KV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S8KV_OK 0
+#define S8KV_ERR_INVALID (-1)     /* bad shape, stride, size or pointer */
+#define S8KV_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim 96) */
+#define S8KV_ERR_LAUNCH (-3)      /* the HIP runtime rejected a launch */
+#define S8KV_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int s8kv_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* s8kv_last_error(void);
+
+/*
+ * Paged int8 append: quantize-on-write of fp16 K/V into the int8 cache.
+ * Replaces superl8.quantize_kv_write_paged(k, v, k_cache, k_scale, v_cache,
+ * v_scale, slot_mapping) called at kv_cache.py:1073-1081 (prefill / varlen),
+ * kv_cache.py:1108-1116 (decode / verify) and kv_cache.py:288-296 (compaction).
+ *
+ * k, v: fp16 [num_tokens, num_kv_heads, head_dim]; element strides for the
+ * token and head axes, head_dim contiguous.  K is Hadamard-rotated then
+ * per-(token, head) symmetric RTN int8 with an fp32 scale (kv_cache.py:587-604);
+ * V is RTN without rotation.  Tokens whose slot is negative are skipped.
+ */
+int s8kv_append_int8(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
+                     int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h,
+                     const int32_t* slot_mapping, int8_t* k_cache, float* k_scale, int8_t* v_cache,
+                     float* v_scale, int64_t num_blocks, int block_size, void* stream);
+
+/*
+ * Paged K8V3 append: K as s8kv_append_int8; V through the 3-bit Lloyd-Max codec
+ * (per-128-element L2 norm, nearest codebook entry, bit-plane packing).
+ * Replaces the two-step Python write PagedKVCache._write_k_int8 +
+ * _write_v_lloydmax3 (kv_cache.py:587-626) reached from write_prefill_varlen /
+ * write_decode_static (kv_cache.py:1068-1071, 1103-1106).
+ */
+int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
+                     int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h,
+                     const int32_t* slot_mapping, int8_t* k_cache, float* k_scale, int32_t* v_packed,
+                     float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                     int block_size, void* stream);
+
+/*
+ * Bytes of scratch device memory the decode entry points need for this
+ * geometry (0 when no split of the context is used).  Depends only on its
+ * arguments, so a caller can size the workspace once per graph bucket.
+ */
+int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                   int max_context_len);
+
+/*
+ * Ragged-batch GQA decode attention over the int8 paged cache.
+ * Replaces superl8.attn_paged_decode_cached(q, k_cache, k_scale, v_cache,
+ * v_scale, block_table, context_lens, block_size, *, max_context_len, scale)
+ * called at kv_cache.py:1190-1201 (and S times per chain-verify step,
+ * gqa_attention.py:259-291).
+ *
+ * q: fp16 [batch, num_q_heads, head_dim] with element strides q_stride_b,
+ * q_stride_h (head_dim contiguous; a [B,Hq,1,D] transpose view qualifies).
+ * block_table: int32 [batch, >= ceil(max_context_len/block_size)] with row
+ * stride block_table_stride; row b is read only for its first
+ * ceil(context_lens[b]/block_size) entries.  context_lens: int32 [batch].
+ * max_context_len >= max(context_lens) sizes the context split; a row whose
+ * context_lens entry exceeds it is truncated to max_context_len tokens.
+ * out: fp16 [batch, num_q_heads, head_dim] contiguous.
+ * Row b, head h attends tokens [0, context_lens[b]) of KV head
+ * h / (num_q_heads / num_kv_heads) with softmax scale `scale`, applying the
+ * Hadamard rotation to q (K is stored rotated).
+ */
+int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                     const int8_t* v_cache, const float* v_scale, int64_t num_blocks, int block_size,
+                     const int32_t* block_table, int64_t block_table_stride, const int32_t* context_lens,
+                     int max_context_len, float scale, void* out, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Decode attention over the K8V3 cache (int8 K, 3-bit Lloyd-Max V dequantized
+ * in-kernel).  Replaces superl8.attn_paged_decode_k8v3(q, k_cache, k_scale,
+ * v_packed, v_norm, v_codebook, block_table, context_lens, block_size, *,
+ * max_context_len, scale) called at kv_cache.py:1170-1182.  Arguments as
+ * s8kv_decode_int8; head_dim 128 or 256 and lloyd_block 128 (the reference's
+ * own gate, kv_cache.py:691-701).
+ */
+int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                     const int32_t* v_packed, const float* v_norm, const float* v_codebook, int lloyd_block,
+                     int64_t num_blocks, int block_size, const int32_t* block_table,
+                     int64_t block_table_stride, const int32_t* context_lens, int max_context_len, float scale,
+                     void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Copy whole physical blocks across every layer of up to 8 cache tensors
+ * (copy-on-write of a shared prefix block; compaction of the pool).
+ * The reference has no block copy: prefix sharing is refcounted
+ * (kv_cache.py:751-755) and compaction re-quantizes token by token
+ * (kv_cache.py:199-313).  This entry point is the byte-exact replacement used
+ * behind the build's copy-on-write and compaction.
+ *
+ * tensor_ptrs[i]: base of tensor i, laid out [num_layers][num_blocks][...];
+ * block_bytes[i]: bytes of one block of one layer (a multiple of 16);
+ * layer_stride_bytes[i]: bytes between consecutive layers.
+ * src_blocks, dst_blocks: device int32 [num_pairs]; the two sets must be
+ * disjoint.  Copies t[layer][dst[p]] = t[layer][src[p]] for all layers.
+ */
+int s8kv_copy_blocks(int num_tensors, void* const* tensor_ptrs, const int64_t* block_bytes,
+                     const int64_t* layer_stride_bytes, int num_layers, int64_t num_blocks,
+                     const int32_t* src_blocks, const int32_t* dst_blocks, int num_pairs, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUPERL8_KV_H_ */

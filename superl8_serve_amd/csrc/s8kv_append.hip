@@ -1,0 +1,290 @@
+// Paged KV append: quantize-on-write of fp16 K/V into the int8 and K8V3 layouts.
+//
+// One wave64 handles one (token, kv-head) row: it reads D fp16 K and V values,
+// rotates K with a fixed-order fp32 Walsh-Hadamard transform, quantizes, and
+// scatters the bytes to storage row (block*Hkv + h)*bs + offset.  Lane l holds
+// elements l, l+64, l+128, ... so that every global access of the wave is one
+// contiguous span.
+#include "s8kv_device.h"
+#include "s8kv_host.h"
+
+namespace s8kv {
+
+constexpr int kAppendWaves = 4;  // waves per workgroup
+
+template <int D>
+struct RowLayout {
+  static constexpr int E = D >= 64 ? D / 64 : 1;    // elements per lane
+  static constexpr int ACTIVE = D >= 64 ? 64 : D;   // lanes holding data
+};
+
+// Fixed-order fp32 Walsh-Hadamard transform of one D-row spread over the wave:
+// stages h = 1, 2, ..., D/2; the pair (i, i+h) with bit h of i clear becomes
+// (x[i] + x[i+h], x[i] - x[i+h]).
+template <int D>
+__device__ __forceinline__ void fwht_row(float (&x)[RowLayout<D>::E], int lane) {
+  constexpr int E = RowLayout<D>::E;
+#pragma unroll
+  for (int h = 1; h < D && h < 64; h <<= 1) {
+    const bool upper = (lane & h) != 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      float p = shfl_xor_f(x[j], h);
+      x[j] = upper ? (p - x[j]) : (x[j] + p);
+    }
+  }
+#pragma unroll
+  for (int hs = 1; hs < E; hs <<= 1) {  // h = 64*hs, in-lane
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      if ((j & hs) == 0) {
+        float a = x[j], b = x[j + hs];
+        x[j] = a + b;
+        x[j + hs] = a - b;
+      }
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void load_row_f16(const _Float16* p, float (&x)[RowLayout<D>::E], int lane) {
+  constexpr int E = RowLayout<D>::E;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    int e = lane + 64 * j;
+    x[j] = (lane < RowLayout<D>::ACTIVE) ? (float)p[e] : 0.0f;
+  }
+}
+
+// Per-row RTN int8 of the wave's row; writes D bytes at `byte_off` and the scale.
+template <int D>
+__device__ __forceinline__ void rtn_store_row(const float (&y)[RowLayout<D>::E], int lane, rsrc_t qbuf,
+                                              uint32_t byte_off, rsrc_t sbuf, uint32_t scale_off) {
+  constexpr int E = RowLayout<D>::E;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(y[j]));
+  amax = wave_max(amax);
+  const float scale = amax / 127.0f;
+  if (lane < RowLayout<D>::ACTIVE) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      int q = rtn_i8(y[j], scale);
+      bstore8((uint8_t)(int8_t)q, qbuf, byte_off + lane + 64 * j);
+    }
+  }
+  if (lane == 0) bstore32(__builtin_bit_cast(uint32_t, scale), sbuf, scale_off);
+}
+
+struct AppendArgs {
+  const _Float16* k;
+  const _Float16* v;
+  int64_t num_tokens;
+  int num_kv_heads;
+  int64_t k_stride_t, k_stride_h, v_stride_t, v_stride_h;
+  const int32_t* slot_mapping;
+  void* k_cache;
+  void* k_scale;
+  void* v_cache;   // int8 V (int8 layout) or int32 packed V (k8v3)
+  void* v_scale;   // fp32 V scale (int8) or fp32 V norms (k8v3)
+  const float* v_codebook;
+  uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
+  int64_t num_blocks;
+  int block_size_log2;
+  float rot_norm;  // float32(1/sqrt(D))
+};
+
+template <int D, bool K8V3>
+__global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a) {
+  constexpr int E = RowLayout<D>::E;
+  const int lane = threadIdx.x & 63;
+  const int64_t row_id = (int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6);
+  const int64_t total = a.num_tokens * a.num_kv_heads;
+  if (row_id >= total) return;
+  const int64_t t = row_id / a.num_kv_heads;
+  const int h = (int)(row_id - t * a.num_kv_heads);
+  const int32_t slot = a.slot_mapping[t];
+  if (slot < 0) return;
+  const int bs = 1 << a.block_size_log2;
+  const uint32_t blk = (uint32_t)slot >> a.block_size_log2;
+  if ((int64_t)blk >= a.num_blocks) return;  // slot outside the pool
+  const uint32_t off = (uint32_t)slot & (uint32_t)(bs - 1);
+  const uint32_t row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) + off;
+
+  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
+  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
+
+  // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
+  float x[E];
+  load_row_f16<D>(a.k + t * a.k_stride_t + h * a.k_stride_h, x, lane);
+  fwht_row<D>(x, lane);
+#pragma unroll
+  for (int j = 0; j < E; ++j) x[j] = (float)(_Float16)materialize(x[j] * a.rot_norm);
+  rtn_store_row<D>(x, lane, kc, row * (uint32_t)D, ks, row * 4u);
+
+  // ---- V ----
+  load_row_f16<D>(a.v + t * a.v_stride_t + h * a.v_stride_h, x, lane);
+  if constexpr (!K8V3) {
+    rtn_store_row<D>(x, lane, vc, row * (uint32_t)D, vs, row * 4u);
+  } else {
+    static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
+    constexpr int NB = D / 128;   // Lloyd-Max blocks per row (lloyd_block = 128)
+    constexpr int WORDS = D / 32 * 3;
+    float cb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
+    float norm[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      // Block nb holds elements 128nb + {lane, lane+64}: fold the halves, then
+      // butterflies 32..1 -- the order the CPU restatement uses.
+      float s = x[2 * nb] * x[2 * nb] + x[2 * nb + 1] * x[2 * nb + 1];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) s = s + shfl_xor_f(s, m);
+      norm[nb] = __builtin_sqrtf(s);
+    }
+    uint32_t codes[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const float nrm = norm[j / 2];
+      const float u = nrm > 0.0f ? x[j] / nrm : 0.0f;
+      float best = fabsf(u - cb[0]);
+      uint32_t c = 0;
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        float d = fabsf(u - cb[i]);
+        if (d < best) {
+          best = d;
+          c = (uint32_t)i;
+        }
+      }
+      codes[j] = c;
+    }
+    // Bit-plane packing: element group g (32 elements) -> words 3g+b, bit i of
+    // word 3g+b = bit b of the code of element 32g+i.  Slot j of lanes 0..31
+    // is group 2j, of lanes 32..63 group 2j+1.
+    uint32_t words[WORDS];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        uint64_t m = __ballot((codes[j] >> b) & 1u);
+        words[3 * (2 * j) + b] = (uint32_t)m;
+        words[3 * (2 * j + 1) + b] = (uint32_t)(m >> 32);
+      }
+    }
+    if (lane < WORDS) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < WORDS; ++i) w = (lane == i) ? words[i] : w;
+      bstore32(w, vc, row * (uint32_t)(WORDS * 4) + lane * 4u);
+    }
+    if (lane < NB) {
+      float nv = norm[0];
+#pragma unroll
+      for (int nb = 1; nb < NB; ++nb) nv = (lane == nb) ? norm[nb] : nv;
+      bstore32(__builtin_bit_cast(uint32_t, nv), vs, row * (uint32_t)(NB * 4) + lane * 4u);
+    }
+  }
+}
+
+template <bool K8V3>
+static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) {
+  const int64_t rows = a.num_tokens * a.num_kv_heads;
+  if (rows == 0) return S8KV_OK;
+  const int64_t grid = (rows + kAppendWaves - 1) / kAppendWaves;
+  S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);
+  dim3 g((unsigned)grid), b(64 * kAppendWaves);
+  switch (head_dim) {
+    case 32:
+      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<32, false>), g, b, 0, stream, a); break; }
+      return S8KV_ERR_UNSUPPORTED;
+    case 64:
+      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<64, false>), g, b, 0, stream, a); break; }
+      return S8KV_ERR_UNSUPPORTED;
+    case 128: hipLaunchKernelGGL((append_kernel<128, K8V3>), g, b, 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((append_kernel<256, K8V3>), g, b, 0, stream, a); break;
+    default: return S8KV_ERR_UNSUPPORTED;
+  }
+  return check_launch(K8V3 ? "s8kv_append_k8v3" : "s8kv_append_int8");
+}
+
+static int common_append_checks(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
+                                const int32_t* slot_mapping, int64_t num_blocks, int block_size) {
+  S8KV_REQUIRE(num_tokens >= 0, S8KV_ERR_INVALID, "append: num_tokens < 0");
+  S8KV_REQUIRE(num_kv_heads > 0, S8KV_ERR_INVALID, "append: num_kv_heads must be > 0");
+  S8KV_REQUIRE(head_dim_ok(head_dim), S8KV_ERR_UNSUPPORTED, "append: head_dim %d not in {32,64,128,256}", head_dim);
+  S8KV_REQUIRE(is_pow2(block_size) && block_size >= 4, S8KV_ERR_UNSUPPORTED,
+               "append: block_size %d must be a power of two >= 4", block_size);
+  S8KV_REQUIRE(num_blocks > 0, S8KV_ERR_INVALID, "append: num_blocks must be > 0");
+  S8KV_REQUIRE(num_tokens == 0 || (k && v && slot_mapping), S8KV_ERR_INVALID, "append: null input pointer");
+  return S8KV_OK;
+}
+
+}  // namespace s8kv
+
+using namespace s8kv;
+
+extern "C" int s8kv_append_int8(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
+                                int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h,
+                                const int32_t* slot_mapping, int8_t* k_cache, float* k_scale, int8_t* v_cache,
+                                float* v_scale, int64_t num_blocks, int block_size, void* stream) {
+  int rc = common_append_checks(k, v, num_tokens, num_kv_heads, head_dim, slot_mapping, num_blocks, block_size);
+  if (rc) return rc;
+  const int64_t rows = num_blocks * num_kv_heads * block_size;
+  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "append: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE(k_cache && k_scale && v_cache && v_scale, S8KV_ERR_INVALID, "append: null cache pointer");
+  AppendArgs a{};
+  a.k = (const _Float16*)k;
+  a.v = (const _Float16*)v;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.k_stride_t = k_stride_t; a.k_stride_h = k_stride_h;
+  a.v_stride_t = v_stride_t; a.v_stride_h = v_stride_h;
+  a.slot_mapping = slot_mapping;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
+  a.kc_bytes = (uint32_t)(rows * head_dim);
+  a.vc_bytes = (uint32_t)(rows * head_dim);
+  a.ks_bytes = (uint32_t)(rows * 4);
+  a.vs_bytes = (uint32_t)(rows * 4);
+  a.num_blocks = num_blocks;
+  a.block_size_log2 = log2i(block_size);
+  a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  return launch_append<false>(a, head_dim, (hipStream_t)stream);
+}
+
+extern "C" int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
+                                int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h,
+                                const int32_t* slot_mapping, int8_t* k_cache, float* k_scale, int32_t* v_packed,
+                                float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                int block_size, void* stream) {
+  int rc = common_append_checks(k, v, num_tokens, num_kv_heads, head_dim, slot_mapping, num_blocks, block_size);
+  if (rc) return rc;
+  S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
+               "append_k8v3: head_dim %d not in {128, 256}", head_dim);
+  S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "append_k8v3: lloyd_block %d != 128", lloyd_block);
+  S8KV_REQUIRE(k_cache && k_scale && v_packed && v_norm && v_codebook, S8KV_ERR_INVALID,
+               "append_k8v3: null cache pointer");
+  const int64_t rows = num_blocks * num_kv_heads * block_size;
+  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "append_k8v3: per-layer cache exceeds 4 GiB");
+  AppendArgs a{};
+  a.k = (const _Float16*)k;
+  a.v = (const _Float16*)v;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.k_stride_t = k_stride_t; a.k_stride_h = k_stride_h;
+  a.v_stride_t = v_stride_t; a.v_stride_h = v_stride_h;
+  a.slot_mapping = slot_mapping;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_packed; a.v_scale = v_norm;
+  a.v_codebook = v_codebook;
+  a.kc_bytes = (uint32_t)(rows * head_dim);
+  a.ks_bytes = (uint32_t)(rows * 4);
+  a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
+  a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
+  a.num_blocks = num_blocks;
+  a.block_size_log2 = log2i(block_size);
+  a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  return launch_append<true>(a, head_dim, (hipStream_t)stream);
+}

@@ -1,0 +1,594 @@
+// Ragged-batch GQA decode attention over the paged int8 / K8V3 cache.
+//
+// Work decomposition: one workgroup (4 waves) per (sequence b, kv head h,
+// context split).  Each wave walks 32-token tiles of its split (tiles w, w+4,
+// ... of the split) and keeps an online softmax for the G = Hq/Hkv query heads
+// that share the KV head, so every KV byte is read once for all G heads.
+//
+// Per 32-token tile a wave does:
+//   QK  : S[token][head] on MFMA 16x16x32 f16.  A = K rows (int8 -> fp16 is
+//         exact) loaded straight from HBM in MFMA operand layout; B = the
+//         rotated, pre-scaled q split into fp16 hi + lo parts (two MFMAs), so
+//         scores carry ~22 bits of q precision.
+//   softmax: lane (head c = lane%16, group g = lane/16) owns tokens
+//         {4g..4g+3} and {16+4g..16+4g+3} of the tile; the running max is
+//         shared across the 4 groups with two lane shuffles.
+//   PV  : O^T[dim][head] on MFMA 16x16x32 f16.  B = P^T taken from the lane's
+//         own softmax values (times the per-token V scale / norm, split into
+//         fp16 hi + lo) -- no shuffle; A = V^T read from an LDS copy of the tile with the gfx950
+//         transpose read ds_read_b64_tr_b8 (int8) / ds_read_b64_tr_b16 (K8V3
+//         dequantized to fp16 in LDS).
+// The 4 waves of a workgroup merge in LDS; a context split > 1 writes
+// (max, sum, acc) partials that s8kv_merge_kernel combines.
+#include <stdlib.h>
+
+#include "s8kv_device.h"
+#include "s8kv_host.h"
+
+namespace s8kv {
+
+constexpr int kDecWaves = 4;
+constexpr int kTile = 32;
+constexpr float kNegInf = -__builtin_inff();
+
+template <int D, bool K8V3>
+struct DecCfg {
+  static constexpr int KCH = D / 4;          // K bytes per lane per token row
+  static constexpr int NQK = D / 32;         // QK MFMAs per 16-token subtile
+  static constexpr int NPV = D / 16;         // PV MFMAs per tile (16 dims each)
+  static constexpr int NB = K8V3 ? D / 128 : 1;  // per-token V scales: 1 (int8) or Lloyd-Max blocks (K8V3)
+  static constexpr int NG = D / 32;          // 32-dim code groups per row (K8V3)
+  static constexpr int WORDS = NG * 3;       // packed words per row (K8V3)
+  // LDS row pitch of the staged V tile: int8 rows padded by 16 B, fp16 rows by
+  // 32 B, so the 8 (int8) / 4 (fp16) rows one transpose read touches fall in
+  // distinct banks.
+  static constexpr int VROW = K8V3 ? (2 * D + 32) : (D + 16);
+  static constexpr int VSTAGE = kTile * VROW;                 // bytes per wave
+  static constexpr int QROT = 16 * D * 4;                     // q staging
+  static constexpr int MERGE = kDecWaves * (16 * D + 32) * 4; // cross-wave merge
+  static constexpr int SMEM_A = kDecWaves * VSTAGE;
+  static constexpr int SMEM = (SMEM_A > QROT ? (SMEM_A > MERGE ? SMEM_A : MERGE) : (QROT > MERGE ? QROT : MERGE));
+};
+
+struct DecodeArgs {
+  const _Float16* q;
+  int64_t q_stride_b, q_stride_h;
+  int num_q_heads, num_kv_heads, group;
+  const void* k_cache;
+  const void* k_scale;
+  const void* v_cache;   // int8 V or int32 packed V
+  const void* v_scale;   // fp32 V scale or fp32 V norms
+  const float* v_codebook;
+  uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* context_lens;
+  int bs_log2;
+  int max_context_len;  // every row is clamped to it (block-table rows hold this many tokens)
+  int split_tokens;
+  int n_splits;
+  float qscale;    // softmax scale * log2(e) * 1/sqrt(D) (rotation norm)
+  _Float16* out;
+  float* ws_ml;    // [B][n_splits][Hq][2]
+  float* ws_acc;   // [B][n_splits][Hq][D]
+};
+
+// Position of tile token tt (0..31) in the LDS-staged V tile: lane group g's
+// eight transpose-read rows (tokens 4g..4g+3 and 16+4g..16+4g+3) are
+// consecutive rows 8g..8g+7.
+__device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
+
+__device__ __forceinline__ uint32_t storage_row(const DecodeArgs& a, const int32_t* bt_row, int tok, int h) {
+  const uint32_t blk = (uint32_t)bt_row[tok >> a.bs_log2];
+  return ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.bs_log2) + ((uint32_t)tok & ((1u << a.bs_log2) - 1u));
+}
+
+template <int KCH>
+__device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4]) {
+  if constexpr (KCH == 8) {
+    u32x2_t v = bload64(r, off);
+    dst[0] = v.x; dst[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < KCH / 16; ++i) {
+      u32x4_t v = bload128(r, off + 16 * i);
+      dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
+    }
+  }
+}
+
+// fp16 lookup of 4 three-bit codes held as bytes of `sel` through the byte
+// tables (lo/hi bytes of the 8 fp16 codebook entries).
+__device__ __forceinline__ u32x2_t cb_lookup4(uint32_t sel, uint32_t lo03, uint32_t lo47, uint32_t hi03, uint32_t hi47) {
+  uint32_t lo = __builtin_amdgcn_perm(lo47, lo03, sel);
+  uint32_t hi = __builtin_amdgcn_perm(hi47, hi03, sel);
+  u32x2_t r;
+  r.x = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  r.y = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  return r;
+}
+
+template <int D, bool K8V3>
+__global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a) {
+  using C = DecCfg<D, K8V3>;
+  __shared__ __attribute__((aligned(16))) char smem[C::SMEM];
+
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int L = min(a.context_lens[b], a.max_context_len);
+  const int t0 = split * a.split_tokens;
+  const int G = a.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  if (L <= 0) {  // empty row: defined as zeros
+    if (split == 0) {
+      for (int i = tid; i < G * D; i += 64 * kDecWaves)
+        a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
+    }
+    return;
+  }
+  if (t0 >= L) return;
+  const int t1 = min(L, t0 + a.split_tokens);
+  const int n_split_b = (L + a.split_tokens - 1) / a.split_tokens;
+
+  // ---- q: load G heads, fp32 Walsh-Hadamard in LDS, split into fp16 hi/lo ----
+  float* qrot = reinterpret_cast<float*>(smem);
+  for (int i = tid; i < G * D; i += 64 * kDecWaves) {
+    const int cc = i / D, d = i - cc * D;
+    qrot[i] = (float)a.q[(int64_t)b * a.q_stride_b + (int64_t)(h * G + cc) * a.q_stride_h + d];
+  }
+  __syncthreads();
+  for (int hs = 1; hs < D; hs <<= 1) {
+    for (int p = tid; p < G * (D / 2); p += 64 * kDecWaves) {
+      const int cc = p / (D / 2), j = p - cc * (D / 2);
+      const int i = (j / hs) * 2 * hs + (j % hs);
+      float* r = qrot + cc * D;
+      const float x0 = r[i], x1 = r[i + hs];
+      r[i] = x0 + x1;
+      r[i + hs] = x0 - x1;
+    }
+    __syncthreads();
+  }
+  half8_t qhi[C::NQK], qlo[C::NQK];
+#pragma unroll
+  for (int m = 0; m < C::NQK; ++m) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dim = g * C::KCH + 8 * m + e;
+      const float val = (c < G) ? qrot[c * D + dim] * a.qscale : 0.0f;
+      const _Float16 hi = (_Float16)val;
+      qhi[m][e] = hi;
+      qlo[m][e] = (_Float16)(val - (float)hi);
+    }
+  }
+  __syncthreads();  // qrot is reused as V staging below
+
+  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
+  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
+  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+  char* vstage = smem + wave * C::VSTAGE;
+
+  // K8V3 codebook byte tables (fp16 of the fp32 codebook).
+  uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
+  if constexpr (K8V3) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
+      const uint32_t lo = hb & 0xFFu, hi = hb >> 8;
+      if (i < 4) { tlo03 |= lo << (8 * i); thi03 |= hi << (8 * i); }
+      else { tlo47 |= lo << (8 * (i - 4)); thi47 |= hi << (8 * (i - 4)); }
+    }
+  }
+
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+  float4_t acc[C::NPV];
+#pragma unroll
+  for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int tb = t0 + kTile * wave; tb < t1; tb += kTile * kDecWaves) {
+    const int last = L - 1;
+    // ---- K rows in MFMA A layout: lane (c, g) holds token tb+16s+c, bytes [g*KCH, (g+1)*KCH) ----
+    uint32_t kreg[2][C::KCH / 4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int tok = min(tb + 16 * s + c, last);
+      const uint32_t row = storage_row(a, bt_row, tok, h);
+      load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), kreg[s]);
+    }
+    // ---- per-token scales of the lane's 8 tokens (4 consecutive per subtile) ----
+    float4_t ksc[2];
+    float4_t vsc[2][C::NB];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int tok = min(tb + 16 * s + 4 * g, last & ~3);
+      const uint32_t row = storage_row(a, bt_row, tok, h);
+      ksc[s] = bloadf4(ks, row * 4u);
+      if constexpr (!K8V3) {
+        vsc[s][0] = bloadf4(vs, row * 4u);
+      } else {
+        if constexpr (C::NB == 1) {
+          vsc[s][0] = bloadf4(vs, row * 4u);
+        } else {
+          float4_t n0 = bloadf4(vs, row * 8u), n1 = bloadf4(vs, row * 8u + 16u);
+          // norms of 4 tokens x 2 blocks laid out [tok][nb]
+          vsc[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
+          vsc[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
+        }
+      }
+    }
+    // ---- V tile -> LDS ----
+    if constexpr (!K8V3) {
+      constexpr int LPR = D / 16;          // lanes per row (16 B each)
+      constexpr int RPI = 64 / LPR;        // rows per load instruction
+#pragma unroll
+      for (int j = 0; j < kTile / RPI; ++j) {
+        const int tt = j * RPI + lane / LPR;
+        const int col = (lane % LPR) * 16;
+        const int tok = min(tb + tt, last);
+        const uint32_t row = storage_row(a, bt_row, tok, h);
+        u32x4_t v = bload128(vc, row * (uint32_t)D + (uint32_t)col);
+        *reinterpret_cast<u32x4_t*>(vstage + lds_row_of(tt) * C::VROW + col) = v;
+      }
+    } else {
+      // 32 tokens x NG code groups; each job expands 3 bit-plane words into 32 fp16.
+#pragma unroll
+      for (int jb = 0; jb < (kTile * C::NG) / 64; ++jb) {
+        const int job = jb * 64 + lane;
+        const int tt = job / C::NG, gi = job % C::NG;
+        const int tok = min(tb + tt, last);
+        const uint32_t row = storage_row(a, bt_row, tok, h);
+        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)(gi * 12);
+        const uint32_t w0 = bload32(vc, base), w1 = bload32(vc, base + 4), w2 = bload32(vc, base + 8);
+        char* dst = vstage + lds_row_of(tt) * C::VROW + gi * 64;
+#pragma unroll
+        for (int q4 = 0; q4 < 8; q4 += 2) {
+          u32x4_t o;
+          {
+            const int i = 4 * q4;
+            const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
+            u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+            o.x = r.x; o.y = r.y;
+          }
+          {
+            const int i = 4 * q4 + 4;
+            const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
+            u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+            o.z = r.x; o.w = r.y;
+          }
+          *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
+        }
+      }
+    }
+
+    // ---- QK ----
+    float4_t sc[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < C::NQK; ++m) {
+        const half8_t ka = i8x8_to_f16(u32x2_t{kreg[s][2 * m], kreg[s][2 * m + 1]});
+        cacc = mfma16x16x32(ka, qhi[m], cacc);
+        cacc = mfma16x16x32(ka, qlo[m], cacc);
+      }
+      sc[s] = cacc;
+    }
+
+    // ---- online softmax (log2 domain; q carries scale*log2e) ----
+    float p[2][4];
+    bool valid[2][4];
+    float mt = kNegInf;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tb + 16 * s + 4 * g + i;
+        valid[s][i] = tok < t1;
+        const float x = sc[s][i] * ksc[s][i];
+        p[s][i] = valid[s][i] ? x : kNegInf;
+        mt = fmaxf(mt, p[s][i]);
+      }
+    }
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const bool any = m_new != kNegInf;
+    const float alpha = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    float psum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = (valid[s][i] && any) ? __builtin_amdgcn_exp2f(p[s][i] - m_new) : 0.0f;
+        p[s][i] = e;
+        psum += e;
+      }
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
+
+    // ---- PV ----
+    // P' = p * (V scale | Lloyd-Max norm) split into fp16 hi + lo: a single
+    // fp16 rounding of the weights costs up to 2^-11 relative per term, which
+    // outputs formed by cancellation of large outlier-channel terms amplify.
+    half8_t pbh[C::NB], pbl[C::NB];
+#pragma unroll
+    for (int nb = 0; nb < C::NB; ++nb) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w = valid[s][i] ? p[s][i] * vsc[s][nb][i] : 0.0f;
+          const _Float16 wh = (_Float16)w;
+          pbh[nb][4 * s + i] = wh;
+          pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) {
+      half8_t va;
+      if constexpr (!K8V3) {
+        const int off = (8 * g + ((lane >> 1) & 7)) * C::VROW + 16 * n + 8 * (lane & 1);
+        i32x2_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((S8KV_LDS i32x2_t*)(vstage + off));
+        va = i8x8_to_f16(__builtin_bit_cast(u32x2_t, t));
+      } else {
+        const int r0 = 8 * g + ((lane >> 2) & 3);
+        const int colb = (16 * n + 4 * (lane & 3)) * 2;
+        i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + r0 * C::VROW + colb));
+        i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + (r0 + 4) * C::VROW + colb));
+        half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
+        va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+      }
+      const int nb = C::NB == 1 ? 0 : (16 * n) / 128;
+      acc[n] = mfma16x16x32(va, pbh[nb], acc[n]);
+      acc[n] = mfma16x16x32(va, pbl[nb], acc[n]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- merge the 4 waves of the workgroup ----
+  float l_tot = l_run;
+  l_tot += shfl_xor_f(l_tot, 16);
+  l_tot += shfl_xor_f(l_tot, 32);
+  __syncthreads();  // every wave is done with its V staging
+  float* mrg = reinterpret_cast<float*>(smem);
+  float* w_acc = mrg + wave * (16 * D + 32);  // [16 heads][D] then m[16], l[16]
+  if (c < G) {
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w_acc[c * D + 16 * n + 4 * g + r] = acc[n][r];
+    }
+    if (g == 0) {
+      w_acc[16 * D + c] = m_run;
+      w_acc[16 * D + 16 + c] = l_tot;
+    }
+  }
+  __syncthreads();
+  // every thread combines some (head, dim) outputs
+  for (int i = tid; i < G * D; i += 64 * kDecWaves) {
+    const int cc = i / D, d = i - cc * D;
+    float mw[kDecWaves];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      mw[w] = mrg[w * (16 * D + 32) + 16 * D + cc];
+      M = fmaxf(M, mw[w]);
+    }
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      const float* wa = mrg + w * (16 * D + 32);
+      const float f = (mw[w] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+      num += f * wa[cc * D + d];
+      den += f * wa[16 * D + 16 + cc];
+    }
+    const int hq = h * G + cc;
+    if (n_split_b == 1) {
+      a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
+    } else {
+      const int64_t pi = ((int64_t)b * a.n_splits + split) * a.num_q_heads + hq;
+      a.ws_acc[pi * D + d] = num;
+      if (d == 0) {
+        a.ws_ml[pi * 2] = M;
+        a.ws_ml[pi * 2 + 1] = den;
+      }
+    }
+  }
+}
+
+// Combine the context splits of one (row, q head): one wave per output row.
+template <int D>
+__global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int L = min(a.context_lens[b], a.max_context_len);
+  if (L <= 0) return;
+  const int n = (L + a.split_tokens - 1) / a.split_tokens;
+  if (n <= 1) return;
+  const int lane = threadIdx.x;
+  const int64_t base = (int64_t)b * a.n_splits;
+  float M = kNegInf;
+  for (int s = 0; s < n; ++s) M = fmaxf(M, a.ws_ml[((base + s) * a.num_q_heads + hq) * 2]);
+  constexpr int E = D >= 64 ? D / 64 : 1;
+  float num[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) num[j] = 0.0f;
+  float den = 0.0f;
+  for (int s = 0; s < n; ++s) {
+    const int64_t pi = (base + s) * a.num_q_heads + hq;
+    const float ms = a.ws_ml[pi * 2];
+    const float f = (ms == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    den += f * a.ws_ml[pi * 2 + 1];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) num[j] += f * a.ws_acc[pi * D + d];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num[j] / den : 0.0f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+struct SplitPlan {
+  int split_tokens;
+  int n_splits;
+};
+
+// Tiles per wave so that a batch of rows with mean length ~max/2 yields about
+// 8 waves per SIMD (256 CUs x 4 SIMDs).  S8KV_DECODE_TILES_PER_WAVE overrides.
+static SplitPlan plan_split(int batch, int num_kv_heads, int max_context_len) {
+  int tpw = 0;
+  if (const char* env = getenv("S8KV_DECODE_TILES_PER_WAVE")) tpw = atoi(env);
+  if (tpw <= 0) {
+    const int64_t est_tiles = (int64_t)batch * num_kv_heads * ((max_context_len / 2 + kTile - 1) / kTile);
+    const int64_t target_waves = 8192;
+    int64_t t = est_tiles / target_waves;
+    tpw = 1;
+    while (tpw * 2 <= t && tpw < 64) tpw *= 2;
+  }
+  SplitPlan p;
+  p.split_tokens = tpw * kTile * kDecWaves;
+  const int mc = max_context_len > 0 ? max_context_len : 1;
+  p.n_splits = (mc + p.split_tokens - 1) / p.split_tokens;
+  return p;
+}
+
+template <int D, bool K8V3>
+static int launch_decode(DecodeArgs& a, int batch, hipStream_t stream) {
+  dim3 grid(a.n_splits, a.num_kv_heads, batch);
+  hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), 0, stream, a);
+  int rc = check_launch("s8kv_decode");
+  if (rc) return rc;
+  if (a.n_splits > 1) {
+    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_q_heads, batch), dim3(64), 0, stream, a);
+    rc = check_launch("s8kv_decode(merge)");
+  }
+  return rc;
+}
+
+static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                         int64_t num_blocks, int block_size, int max_context_len, float scale, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  S8KV_REQUIRE(batch >= 0, S8KV_ERR_INVALID, "decode: batch < 0");
+  if (batch == 0) return S8KV_OK;
+  S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
+               "decode: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
+  S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "decode: more than 16 q heads per kv head");
+  S8KV_REQUIRE(head_dim_ok(head_dim), S8KV_ERR_UNSUPPORTED, "decode: head_dim %d not in {32,64,128,256}", head_dim);
+  S8KV_REQUIRE(!k8v3 || head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
+               "decode_k8v3: head_dim %d not in {128, 256}", head_dim);
+  S8KV_REQUIRE(is_pow2(block_size) && block_size >= 4, S8KV_ERR_UNSUPPORTED,
+               "decode: block_size %d must be a power of two >= 4", block_size);
+  S8KV_REQUIRE(num_blocks > 0, S8KV_ERR_INVALID, "decode: num_blocks must be > 0");
+  S8KV_REQUIRE(max_context_len >= 0, S8KV_ERR_INVALID, "decode: max_context_len < 0");
+  S8KV_REQUIRE(a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.block_table && a.context_lens && a.out,
+               S8KV_ERR_INVALID, "decode: null pointer argument");
+  const int64_t rows = num_blocks * num_kv_heads * block_size;
+  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "decode: per-layer cache exceeds 4 GiB");
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.kc_bytes = (uint32_t)(rows * head_dim);
+  a.ks_bytes = (uint32_t)(rows * 4);
+  if (k8v3) {
+    a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
+    a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
+  } else {
+    a.vc_bytes = (uint32_t)(rows * head_dim);
+    a.vs_bytes = (uint32_t)(rows * 4);
+  }
+  a.bs_log2 = log2i(block_size);
+  a.max_context_len = max_context_len;
+  SplitPlan p = plan_split(batch, num_kv_heads, max_context_len);
+  a.split_tokens = p.split_tokens;
+  a.n_splits = p.n_splits;
+  a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
+  const int64_t need = s8kv_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, max_context_len);
+  if (need > 0) {
+    S8KV_REQUIRE(workspace != nullptr && workspace_bytes >= need, S8KV_ERR_WORKSPACE,
+                 "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes);
+    a.ws_ml = reinterpret_cast<float*>(workspace);
+    a.ws_acc = a.ws_ml + (int64_t)batch * p.n_splits * num_q_heads * 2;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (head_dim) {
+    case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false>(a, batch, s);
+    case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false>(a, batch, s);
+    case 128: return k8v3 ? launch_decode<128, true>(a, batch, s) : launch_decode<128, false>(a, batch, s);
+    case 256: return k8v3 ? launch_decode<256, true>(a, batch, s) : launch_decode<256, false>(a, batch, s);
+  }
+  return S8KV_ERR_UNSUPPORTED;
+}
+
+}  // namespace s8kv
+
+using namespace s8kv;
+
+extern "C" int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                              int max_context_len) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
+  SplitPlan p = plan_split(batch, num_kv_heads, max_context_len);
+  if (p.n_splits <= 1) return 0;
+  return (int64_t)batch * p.n_splits * num_q_heads * (head_dim + 2) * 4;
+}
+
+extern "C" int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                                const int8_t* v_cache, const float* v_scale, int64_t num_blocks, int block_size,
+                                const int32_t* block_table, int64_t block_table_stride, const int32_t* context_lens,
+                                int max_context_len, float scale, void* out, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  return decode_common(a, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size, max_context_len,
+                       scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                                const int32_t* v_packed, const float* v_norm, const float* v_codebook, int lloyd_block,
+                                int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                float scale, void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "decode_k8v3: lloyd_block %d != 128", lloyd_block);
+  S8KV_REQUIRE(v_codebook != nullptr, S8KV_ERR_INVALID, "decode_k8v3: null codebook");
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_packed; a.v_scale = v_norm;
+  a.v_codebook = v_codebook;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  return decode_common(a, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size, max_context_len,
+                       scale, workspace, workspace_bytes, stream);
+}

@@ -1,0 +1,124 @@
+// Device-side helpers shared by the quantized paged-KV kernels (gfx950, wave64).
+//
+// Numerics that must be bit-identical to the CPU restatement of the reference
+// (K rotation, RTN int8, Lloyd-Max V codec) are implemented here with a fixed
+// operation order; see the comments on each helper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace s8kv {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+#define S8KV_LDS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// Buffer resources: every bulk cache access goes through a buffer descriptor
+// whose num_records is the tensor's byte size, so an index that escapes the
+// tensor reads zeros instead of faulting.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ float4_t bloadf4(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void bstore128(u32x4_t v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore32(uint32_t v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore8(uint8_t v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers (wave64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  int lane = __lane_id();
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// int8 -> fp16 conversion for MFMA operands (exact: |x| <= 128 fits fp16).
+// Bytes are biased to unsigned (x ^ 0x80 = x + 128), placed in the mantissa of
+// the fp16 constant 1024 (0x6400) with v_perm_b32, then 1152 is subtracted
+// with one packed fp16 add per pair.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ half8_t i8x8_to_f16(u32x2_t x) {
+  const uint32_t magic = 0x64646464u;
+  uint32_t a = x.x ^ 0x80808080u;
+  uint32_t b = x.y ^ 0x80808080u;
+  u32x4_t w;
+  w.x = __builtin_amdgcn_perm(magic, a, 0x04010400u);
+  w.y = __builtin_amdgcn_perm(magic, a, 0x04030402u);
+  w.z = __builtin_amdgcn_perm(magic, b, 0x04010400u);
+  w.w = __builtin_amdgcn_perm(magic, b, 0x04030402u);
+  half8_t h = __builtin_bit_cast(half8_t, w);
+  const half8_t bias = {-1152.0f16, -1152.0f16, -1152.0f16, -1152.0f16,
+                        -1152.0f16, -1152.0f16, -1152.0f16, -1152.0f16};
+  return h + bias;
+}
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Quantization helpers (must match the CPU restatement bit for bit)
+// ---------------------------------------------------------------------------
+
+// Materialize an fp32 value: stops the compiler from fusing the operation that
+// produced it into a following fp16 conversion (v_fma_mix*), which would round
+// once from the exact product instead of rounding to fp32 first.
+__device__ __forceinline__ float materialize(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Round-half-even to int, clamped to [-127, 127].  `y` and `scale` are fp32;
+// the division is IEEE correctly rounded (HIP's default fp32 divide).
+__device__ __forceinline__ int rtn_i8(float y, float scale) {
+  if (!(scale > 0.0f)) return 0;
+  float q = __builtin_rintf(y / scale);
+  q = fminf(127.0f, fmaxf(-127.0f, q));
+  return (int)q;
+}
+
+// Spread the low 4 bits of x into bit 0 of each byte.
+__device__ __forceinline__ uint32_t spread4(uint32_t x) {
+  return ((x & 0xFu) * 0x00204081u) & 0x01010101u;
+}
+
+}  // namespace s8kv

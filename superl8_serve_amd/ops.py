@@ -1,0 +1,288 @@
+"""Torch-facing ops with the signatures the reference's cache code calls on the
+``superl8`` module (SURVEY boundary; call sites in
+``superl8serve/engine/kv_cache.py``).
+
+Each op checks shapes/dtypes on the host, turns tensors into pointers and
+element strides, and launches the gfx950 kernels of ``libsuperl8_kv.so`` on
+torch's current stream.  Outputs and scratch come from the torch caching
+allocator; nothing synchronizes, so every op can be captured in a HIP graph.
+CPU tensors are rejected: there is no host implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "quantize_kv_write_paged",
+    "quantize_kv_write_paged_k8v3",
+    "attn_paged_decode_cached",
+    "attn_paged_decode_k8v3",
+    "decode_workspace_bytes",
+    "copy_blocks",
+]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond: bool, msg: str, exc=ValueError) -> None:
+    if not cond:
+        raise exc(msg)
+
+
+def _on_gpu(name: str, t: torch.Tensor, dtype: torch.dtype | None = None, device=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (the paged-KV ops run only on the HIP device)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _cache_geometry(k_cache: torch.Tensor) -> tuple[int, int, int, int]:
+    _require(k_cache.dim() == 4, f"k_cache must be [num_blocks, num_kv_heads, block_size, head_dim], got {tuple(k_cache.shape)}")
+    _require(k_cache.is_contiguous(), "k_cache must be contiguous")
+    n, hkv, bs, d = k_cache.shape
+    return n, hkv, bs, d
+
+
+def _tokens_view(x: torch.Tensor, name: str, hkv: int, d: int) -> torch.Tensor:
+    _require(x.dim() == 3 and x.shape[1] == hkv and x.shape[2] == d,
+             f"{name} must be [num_tokens, {hkv}, {d}], got {tuple(x.shape)}")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    return x
+
+
+def quantize_kv_write_paged(k, v, k_cache, k_scale, v_cache, v_scale, slot_mapping) -> None:
+    """Quantize-on-write of fp16 K/V ``[T, Hkv, D]`` into the int8 paged cache
+    (``superl8.quantize_kv_write_paged`` at kv_cache.py:1073-1081, 1108-1116,
+    288-296).  K is Hadamard-rotated then RTN int8 with an fp32 per-(token,
+    head) scale; V is RTN int8.  ``slot_mapping``: int32 ``[T]`` flat slots."""
+    _on_gpu("k", k, torch.float16)
+    dev = k.device
+    _on_gpu("v", v, torch.float16, dev)
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _on_gpu("slot_mapping", slot_mapping, torch.int32, dev)
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs] contiguous")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs] contiguous")
+    k = _tokens_view(k, "k", hkv, d)
+    v = _tokens_view(v, "v", hkv, d)
+    t = k.shape[0]
+    _require(v.shape[0] == t, "k and v token counts differ")
+    _require(slot_mapping.dim() == 1 and slot_mapping.shape[0] == t, f"slot_mapping must be [{t}]")
+    if t == 0:
+        return
+    slot_mapping = slot_mapping.contiguous()
+    lib = _lib.load()
+    rc = lib.s8kv_append_int8(
+        k.data_ptr(), v.data_ptr(), t, hkv, d,
+        k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        slot_mapping.data_ptr(), k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(),
+        n, bs, _stream(k),
+    )
+    _lib.check(rc, "quantize_kv_write_paged")
+
+
+def quantize_kv_write_paged_k8v3(k, v, k_cache, k_scale, v_packed, v_norm, v_codebook, slot_mapping,
+                                 lloyd_block: int = 128) -> None:
+    """Fused K8V3 append: K as ``quantize_kv_write_paged``; V through the 3-bit
+    Lloyd-Max codec into ``v_packed`` (int32 ``[N, Hkv, bs, D*3/32]``) and
+    ``v_norm`` (fp32 ``[N, Hkv, bs, D/128]``).  Replaces the reference's
+    ``_write_k_int8`` + ``_write_v_lloydmax3`` (kv_cache.py:587-626)."""
+    _on_gpu("k", k, torch.float16)
+    dev = k.device
+    _on_gpu("v", v, torch.float16, dev)
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_packed", v_packed, torch.int32, dev)
+    _on_gpu("v_norm", v_norm, torch.float32, dev)
+    _on_gpu("v_codebook", v_codebook, torch.float32, dev)
+    _on_gpu("slot_mapping", slot_mapping, torch.int32, dev)
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs] contiguous")
+    _require(tuple(v_packed.shape) == (n, hkv, bs, d * 3 // 32) and v_packed.is_contiguous(),
+             "v_packed must be [N, Hkv, bs, D*3/32] contiguous")
+    _require(tuple(v_norm.shape) == (n, hkv, bs, d // lloyd_block) and v_norm.is_contiguous(),
+             "v_norm must be [N, Hkv, bs, D/lloyd_block] contiguous")
+    _require(v_codebook.numel() == 8 and v_codebook.is_contiguous(), "v_codebook must hold 8 contiguous entries")
+    k = _tokens_view(k, "k", hkv, d)
+    v = _tokens_view(v, "v", hkv, d)
+    t = k.shape[0]
+    _require(v.shape[0] == t and slot_mapping.dim() == 1 and slot_mapping.shape[0] == t, "token counts differ")
+    if t == 0:
+        return
+    slot_mapping = slot_mapping.contiguous()
+    lib = _lib.load()
+    rc = lib.s8kv_append_k8v3(
+        k.data_ptr(), v.data_ptr(), t, hkv, d,
+        k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        slot_mapping.data_ptr(), k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
+        v_codebook.data_ptr(), lloyd_block, n, bs, _stream(k),
+    )
+    _lib.check(rc, "quantize_kv_write_paged_k8v3")
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_context_len: int) -> int:
+    """Scratch bytes the decode ops allocate for this geometry."""
+    return int(_lib.load().s8kv_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, max_context_len))
+
+
+def _decode_prep(q, k_cache, block_table, context_lens, block_size, max_context_len):
+    _on_gpu("q", q, torch.float16)
+    dev = q.device
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("block_table", block_table, torch.int32, dev)
+    _on_gpu("context_lens", context_lens, torch.int32, dev)
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(int(block_size) == bs, f"block_size {block_size} does not match the cache ({bs})")
+    squeeze = False
+    if q.dim() == 4:
+        _require(q.shape[2] == 1, f"decode q must be [B, Hq, 1, D], got {tuple(q.shape)}")
+        q3 = q[:, :, 0, :]
+    else:
+        _require(q.dim() == 3, f"decode q must be [B, Hq, 1, D] or [B, Hq, D], got {tuple(q.shape)}")
+        q3 = q
+        squeeze = True
+    _require(q3.shape[2] == d, f"q head_dim {q3.shape[2]} != cache head_dim {d}")
+    if q3.stride(2) != 1:
+        q3 = q3.contiguous()
+    b, hq = q3.shape[0], q3.shape[1]
+    _require(block_table.dim() == 2 and block_table.shape[0] == b, f"block_table must be [{b}, max_blocks]")
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    _require(context_lens.dim() == 1 and context_lens.shape[0] == b, f"context_lens must be [{b}]")
+    context_lens = context_lens.contiguous()
+    max_context_len = int(max_context_len)
+    _require(max_context_len >= 0, "max_context_len must be >= 0")
+    _require(max_context_len <= block_table.shape[1] * bs,
+             f"max_context_len {max_context_len} exceeds the block table capacity {block_table.shape[1] * bs}")
+    out = torch.empty((b, hq, 1, d) if not squeeze else (b, hq, d), dtype=torch.float16, device=dev)
+    ws_bytes = decode_workspace_bytes(b, hq, hkv, d, max_context_len)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    return q3, block_table, context_lens, out, ws, ws_bytes, (n, hkv, bs, d, b, hq), max_context_len
+
+
+def attn_paged_decode_cached(q, k_cache, k_scale, v_cache, v_scale, block_table, context_lens, block_size, *,
+                             max_context_len, scale):
+    """Ragged-batch GQA decode over the int8 paged cache
+    (``superl8.attn_paged_decode_cached``, kv_cache.py:1190-1201).
+
+    ``q``: fp16 ``[B, Hq, 1, D]`` (a transpose view is fine).  Returns fp16
+    ``[B, Hq, 1, D]``.  ``max_context_len`` only sizes the context split; every
+    row is gated by its own ``context_lens`` entry."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_int8(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+        bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_cached")
+    return out
+
+
+def attn_paged_decode_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, context_lens, block_size,
+                           *, max_context_len, scale):
+    """Decode over the K8V3 cache with the 3-bit V dequantized in-kernel
+    (``superl8.attn_paged_decode_k8v3``, kv_cache.py:1170-1182; positional
+    order pinned by tests/test_k8v3_cache.py:179-186)."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_packed", v_packed, torch.int32, dev)
+    _on_gpu("v_norm", v_norm, torch.float32, dev)
+    _on_gpu("v_codebook", v_codebook, torch.float32, dev)
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_packed.shape) == (n, hkv, bs, d * 3 // 32) and v_packed.is_contiguous(),
+             "v_packed must be [N, Hkv, bs, D*3/32]")
+    lloyd_block = d // v_norm.shape[-1] if v_norm.dim() == 4 and v_norm.shape[-1] > 0 else 0
+    _require(tuple(v_norm.shape[:3]) == (n, hkv, bs) and v_norm.is_contiguous(), "v_norm must be [N, Hkv, bs, D/128]")
+    _require(v_codebook.numel() == 8 and v_codebook.is_contiguous(), "v_codebook must hold 8 contiguous entries")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_k8v3(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
+        lloyd_block, n, bs, bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_k8v3")
+    return out
+
+
+def copy_blocks(tensors: Sequence[torch.Tensor], src: Sequence[int] | torch.Tensor,
+                dst: Sequence[int] | torch.Tensor) -> None:
+    """Byte copy ``t[:, dst[i]] = t[:, src[i]]`` for every cache tensor
+    ``t`` laid out ``[num_layers, num_blocks, ...]`` (copy-on-write and pool
+    compaction).  ``src``/``dst`` are host integer sequences (validated here:
+    in range, equal length, disjoint) or int32 device tensors."""
+    _require(1 <= len(tensors) <= 8, "copy_blocks takes 1..8 tensors")
+    t0 = tensors[0]
+    _on_gpu("tensors[0]", t0)
+    dev = t0.device
+    nl, nb = t0.shape[0], t0.shape[1]
+    ptrs, bbytes, lstrides = [], [], []
+    for i, t in enumerate(tensors):
+        _on_gpu(f"tensors[{i}]", t, None, dev)
+        _require(t.is_contiguous(), f"tensors[{i}] must be contiguous")
+        _require(t.shape[0] == nl and t.shape[1] == nb, f"tensors[{i}] must be [{nl}, {nb}, ...]")
+        per_block = t[0, 0].numel() * t.element_size()
+        ptrs.append(t.data_ptr())
+        bbytes.append(per_block)
+        lstrides.append(t.stride(0) * t.element_size())
+    if isinstance(src, torch.Tensor) or isinstance(dst, torch.Tensor):
+        _require(isinstance(src, torch.Tensor) and isinstance(dst, torch.Tensor), "src and dst must both be tensors")
+        _on_gpu("src", src, torch.int32, dev)
+        _on_gpu("dst", dst, torch.int32, dev)
+        src_t, dst_t = src.contiguous(), dst.contiguous()
+        _require(src_t.numel() == dst_t.numel(), "src and dst differ in length")
+    else:
+        src_l, dst_l = [int(x) for x in src], [int(x) for x in dst]
+        _require(len(src_l) == len(dst_l), "src and dst differ in length")
+        _require(all(0 <= x < nb for x in src_l + dst_l), f"block ids must be in [0, {nb})")
+        _require(not (set(src_l) & set(dst_l)), "source and destination blocks overlap")
+        _require(len(set(dst_l)) == len(dst_l), "destination blocks repeat")
+        if not src_l:
+            return
+        src_t = torch.tensor(src_l, dtype=torch.int32).to(dev, non_blocking=True)
+        dst_t = torch.tensor(dst_l, dtype=torch.int32).to(dev, non_blocking=True)
+    npairs = src_t.numel()
+    if npairs == 0:
+        return
+    n = len(tensors)
+    arr_p = (ctypes.c_void_p * n)(*ptrs)
+    arr_b = (ctypes.c_int64 * n)(*bbytes)
+    arr_s = (ctypes.c_int64 * n)(*lstrides)
+    rc = _lib.load().s8kv_copy_blocks(n, arr_p, arr_b, arr_s, nl, nb, src_t.data_ptr(), dst_t.data_ptr(), npairs,
+                                      _stream(t0))
+    _lib.check(rc, "copy_blocks")
