@@ -1,7 +1,7 @@
 // Ragged-batch GQA decode attention over the paged int8 / K8V3 cache.
 //
-// Work decomposition: one workgroup (4 waves) per (sequence b, kv head h,
-// context split).  Each wave walks 32-token tiles of its split (tiles w, w+4,
+// Work decomposition: one workgroup (4 waves) per (kv head h, sequence b,
+// context split), in that grid order (XCD balance, see the kernel).  Each wave walks 32-token tiles of its split (tiles w, w+4,
 // ... of the split) and keeps an online softmax for the G = Hq/Hkv query heads
 // that share the KV head, so every KV byte is read once for all G heads.
 //
@@ -18,8 +18,12 @@
 //         fp16 hi + lo) -- no shuffle; A = V^T read from an LDS copy of the tile with the gfx950
 //         transpose read ds_read_b64_tr_b8 (int8) / ds_read_b64_tr_b16 (K8V3
 //         dequantized to fp16 in LDS).
-// The 4 waves of a workgroup merge in LDS; a context split > 1 writes
-// (max, sum, acc) partials that s8kv_merge_kernel combines.
+// The 4 waves of a workgroup merge in LDS.  With more than one context split
+// per row every workgroup writes (max, sum, acc) partials to the workspace and
+// merge_kernel combines them.  (Combining them in the last-arriving workgroup
+// needs agent-scope release/acquire fences, which on this multi-XCD part
+// write back and invalidate the whole L2 per workgroup -- far costlier than a
+// second launch.)
 #include <stdlib.h>
 
 #include "s8kv_device.h"
@@ -30,6 +34,8 @@ namespace s8kv {
 constexpr int kDecWaves = 4;
 constexpr int kTile = 32;
 constexpr float kNegInf = -__builtin_inff();
+constexpr int kMaxSplitTokens = 2048;                     // bounds the staged block ids
+constexpr int kMaxSplitBlocks = kMaxSplitTokens / 4 + 2;  // block_size >= 4
 
 template <int D, bool K8V3>
 struct DecCfg {
@@ -44,10 +50,11 @@ struct DecCfg {
   // distinct banks.
   static constexpr int VROW = K8V3 ? (2 * D + 32) : (D + 16);
   static constexpr int VSTAGE = kTile * VROW;                 // bytes per wave
-  static constexpr int QROT = 16 * D * 4;                     // q staging
   static constexpr int MERGE = kDecWaves * (16 * D + 32) * 4; // cross-wave merge
+  static constexpr int VLOADS = K8V3 ? (kTile * NG) / 64 : (kTile * D / 16) / 64;  // V loads per lane per tile
   static constexpr int SMEM_A = kDecWaves * VSTAGE;
-  static constexpr int SMEM = (SMEM_A > QROT ? (SMEM_A > MERGE ? SMEM_A : MERGE) : (QROT > MERGE ? QROT : MERGE));
+  static constexpr int SMEM_MAIN = SMEM_A > MERGE ? SMEM_A : MERGE;
+  static constexpr int SMEM = SMEM_MAIN + kMaxSplitBlocks * 4;  // + block ids of the split
 };
 
 struct DecodeArgs {
@@ -78,10 +85,6 @@ struct DecodeArgs {
 // consecutive rows 8g..8g+7.
 __device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-__device__ __forceinline__ uint32_t storage_row(const DecodeArgs& a, const int32_t* bt_row, int tok, int h) {
-  const uint32_t blk = (uint32_t)bt_row[tok >> a.bs_log2];
-  return ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.bs_log2) + ((uint32_t)tok & ((1u << a.bs_log2) - 1u));
-}
 
 template <int KCH>
 __device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4]) {
@@ -108,14 +111,31 @@ __device__ __forceinline__ u32x2_t cb_lookup4(uint32_t sel, uint32_t lo03, uint3
   return r;
 }
 
+// Split the workgroup's tiles over its waves and stream them with a one-tile
+// software pipeline: the next tile's K/V loads are issued right after this
+// tile's QK MFMAs, its scales after this tile's softmax.
+template <int D, bool K8V3>
+struct TileIO {
+  using C = DecCfg<D, K8V3>;
+  uint32_t k[2][C::KCH / 4];        // K rows, MFMA A layout
+  u32x4_t v[C::VLOADS];             // int8: 16-byte V chunks; K8V3: packed words (x,y,z used)
+  float4_t ks[2];
+  float4_t vs[2][C::NB];
+};
+
 template <int D, bool K8V3>
 __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
   __shared__ __attribute__((aligned(16))) char smem[C::SMEM];
+  int* bt_lds = reinterpret_cast<int*>(smem + C::SMEM_MAIN);
 
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id, so the KV
+  // head varies fastest and the context split slowest: every XCD then gets
+  // an equal share of (row, head) pairs, whereas split-fastest ordering would
+  // send all first splits (present for every row) to one XCD.
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
   const int L = min(a.context_lens[b], a.max_context_len);
   const int t0 = split * a.split_tokens;
   const int G = a.group;
@@ -135,45 +155,70 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
   if (t0 >= L) return;
   const int t1 = min(L, t0 + a.split_tokens);
   const int n_split_b = (L + a.split_tokens - 1) / a.split_tokens;
+  const int last = L - 1;
+  const int bs_log2 = a.bs_log2;
+  const int fb = t0 >> bs_log2;  // first block of the split
 
-  // ---- q: load G heads, fp32 Walsh-Hadamard in LDS, split into fp16 hi/lo ----
-  float* qrot = reinterpret_cast<float*>(smem);
-  for (int i = tid; i < G * D; i += 64 * kDecWaves) {
-    const int cc = i / D, d = i - cc * D;
-    qrot[i] = (float)a.q[(int64_t)b * a.q_stride_b + (int64_t)(h * G + cc) * a.q_stride_h + d];
-  }
-  __syncthreads();
-  for (int hs = 1; hs < D; hs <<= 1) {
-    for (int p = tid; p < G * (D / 2); p += 64 * kDecWaves) {
-      const int cc = p / (D / 2), j = p - cc * (D / 2);
-      const int i = (j / hs) * 2 * hs + (j % hs);
-      float* r = qrot + cc * D;
-      const float x0 = r[i], x1 = r[i + hs];
-      r[i] = x0 + x1;
-      r[i + hs] = x0 - x1;
-    }
-    __syncthreads();
-  }
+  // ---- block ids of the split -> LDS ----
+  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+  const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
+  for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
+
+  // ---- q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
+  // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32) ----
   half8_t qhi[C::NQK], qlo[C::NQK];
+  {
+    float x[C::KCH];
+    const _Float16* qp =
+        a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + (c < G ? c : 0)) * a.q_stride_h + g * C::KCH;
 #pragma unroll
-  for (int m = 0; m < C::NQK; ++m) {
+    for (int i = 0; i < C::KCH; ++i) x[i] = (c < G) ? (float)qp[i] : 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int dim = g * C::KCH + 8 * m + e;
-      const float val = (c < G) ? qrot[c * D + dim] * a.qscale : 0.0f;
-      const _Float16 hi = (_Float16)val;
-      qhi[m][e] = hi;
-      qlo[m][e] = (_Float16)(val - (float)hi);
+    for (int hs = 1; hs < C::KCH; hs <<= 1) {
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        if ((i & hs) == 0) {
+          const float x0 = x[i], x1 = x[i + hs];
+          x[i] = x0 + x1;
+          x[i + hs] = x0 - x1;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) {
+      const bool upper = (lane & m) != 0;
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        const float p = shfl_xor_f(x[i], m);
+        x[i] = upper ? (p - x[i]) : (x[i] + p);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < C::NQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float val = x[8 * m + e] * a.qscale;
+        const _Float16 hi = (_Float16)val;
+        qhi[m][e] = hi;
+        qlo[m][e] = (_Float16)(val - (float)hi);
+      }
     }
   }
-  __syncthreads();  // qrot is reused as V staging below
+  __syncthreads();  // block ids visible
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
   const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
-  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
   char* vstage = smem + wave * C::VSTAGE;
+  const uint32_t hkv = (uint32_t)a.num_kv_heads;
+  const uint32_t bsm = (1u << bs_log2) - 1u;
+
+  // storage row of token `tok` (already clamped to the row's last token)
+  auto row_of = [&](int tok) -> uint32_t {
+    const uint32_t blk = (uint32_t)bt_lds[(tok >> bs_log2) - fb];
+    return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tok & bsm);
+  };
 
   // K8V3 codebook byte tables (fp16 of the fp32 codebook).
   uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
@@ -187,66 +232,80 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
     }
   }
 
+  TileIO<D, K8V3> io;
+  auto issue_kv = [&](int tb) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t row = row_of(min(tb + 16 * s + c, last));
+      load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
+    }
+    if constexpr (!K8V3) {
+      constexpr int LPR = D / 16;    // lanes per V row (16 B each)
+      constexpr int RPI = 64 / LPR;  // rows per load instruction
+#pragma unroll
+      for (int j = 0; j < C::VLOADS; ++j) {
+        const int tt = j * RPI + lane / LPR;
+        const uint32_t row = row_of(min(tb + tt, last));
+        io.v[j] = bload128(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::VLOADS; ++j) {
+        const int job = j * 64 + lane;
+        const int tt = job / C::NG, gi = job % C::NG;
+        const uint32_t row = row_of(min(tb + tt, last));
+        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)(gi * 12);
+        io.v[j].x = bload32(vc, base);
+        io.v[j].y = bload32(vc, base + 4);
+        io.v[j].z = bload32(vc, base + 8);
+      }
+    }
+  };
+  auto issue_scales = [&](int tb) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
+      io.ks[s] = bloadf4(ks, row * 4u);
+      if constexpr (C::NB == 1) {
+        io.vs[s][0] = bloadf4(vs, row * 4u);
+      } else {
+        const float4_t n0 = bloadf4(vs, row * 8u), n1 = bloadf4(vs, row * 8u + 16u);
+        io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
+        io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
+      }
+    }
+  };
+
   float m_run = kNegInf;
   float l_run = 0.0f;
   float4_t acc[C::NPV];
 #pragma unroll
   for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int tb = t0 + kTile * wave; tb < t1; tb += kTile * kDecWaves) {
-    const int last = L - 1;
-    // ---- K rows in MFMA A layout: lane (c, g) holds token tb+16s+c, bytes [g*KCH, (g+1)*KCH) ----
-    uint32_t kreg[2][C::KCH / 4];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int tok = min(tb + 16 * s + c, last);
-      const uint32_t row = storage_row(a, bt_row, tok, h);
-      load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), kreg[s]);
-    }
-    // ---- per-token scales of the lane's 8 tokens (4 consecutive per subtile) ----
-    float4_t ksc[2];
-    float4_t vsc[2][C::NB];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int tok = min(tb + 16 * s + 4 * g, last & ~3);
-      const uint32_t row = storage_row(a, bt_row, tok, h);
-      ksc[s] = bloadf4(ks, row * 4u);
-      if constexpr (!K8V3) {
-        vsc[s][0] = bloadf4(vs, row * 4u);
-      } else {
-        if constexpr (C::NB == 1) {
-          vsc[s][0] = bloadf4(vs, row * 4u);
-        } else {
-          float4_t n0 = bloadf4(vs, row * 8u), n1 = bloadf4(vs, row * 8u + 16u);
-          // norms of 4 tokens x 2 blocks laid out [tok][nb]
-          vsc[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
-          vsc[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
-        }
-      }
-    }
-    // ---- V tile -> LDS ----
+  int tb = t0 + kTile * wave;
+  if (tb < t1) {
+    issue_kv(tb);
+    issue_scales(tb);
+  }
+  while (tb < t1) {
+    const int tn = tb + kTile * kDecWaves;
+    const bool more = tn < t1;
+
+    // ---- 1. V tile -> LDS (int8 rows, or K8V3 codes expanded to fp16 rows) ----
     if constexpr (!K8V3) {
-      constexpr int LPR = D / 16;          // lanes per row (16 B each)
-      constexpr int RPI = 64 / LPR;        // rows per load instruction
+      constexpr int LPR = D / 16;
+      constexpr int RPI = 64 / LPR;
 #pragma unroll
-      for (int j = 0; j < kTile / RPI; ++j) {
+      for (int j = 0; j < C::VLOADS; ++j) {
         const int tt = j * RPI + lane / LPR;
-        const int col = (lane % LPR) * 16;
-        const int tok = min(tb + tt, last);
-        const uint32_t row = storage_row(a, bt_row, tok, h);
-        u32x4_t v = bload128(vc, row * (uint32_t)D + (uint32_t)col);
-        *reinterpret_cast<u32x4_t*>(vstage + lds_row_of(tt) * C::VROW + col) = v;
+        *reinterpret_cast<u32x4_t*>(vstage + lds_row_of(tt) * C::VROW + (lane % LPR) * 16) = io.v[j];
       }
     } else {
-      // 32 tokens x NG code groups; each job expands 3 bit-plane words into 32 fp16.
 #pragma unroll
-      for (int jb = 0; jb < (kTile * C::NG) / 64; ++jb) {
-        const int job = jb * 64 + lane;
+      for (int j = 0; j < C::VLOADS; ++j) {
+        const int job = j * 64 + lane;
         const int tt = job / C::NG, gi = job % C::NG;
-        const int tok = min(tb + tt, last);
-        const uint32_t row = storage_row(a, bt_row, tok, h);
-        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)(gi * 12);
-        const uint32_t w0 = bload32(vc, base), w1 = bload32(vc, base + 4), w2 = bload32(vc, base + 8);
+        const uint32_t w0 = io.v[j].x, w1 = io.v[j].y, w2 = io.v[j].z;
         char* dst = vstage + lds_row_of(tt) * C::VROW + gi * 64;
 #pragma unroll
         for (int q4 = 0; q4 < 8; q4 += 2) {
@@ -254,13 +313,13 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
           {
             const int i = 4 * q4;
             const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-            u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+            const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
             o.x = r.x; o.y = r.y;
           }
           {
             const int i = 4 * q4 + 4;
             const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-            u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+            const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
             o.z = r.x; o.w = r.y;
           }
           *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
@@ -268,21 +327,24 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       }
     }
 
-    // ---- QK ----
+    // ---- 2. QK ----
     float4_t sc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < C::NQK; ++m) {
-        const half8_t ka = i8x8_to_f16(u32x2_t{kreg[s][2 * m], kreg[s][2 * m + 1]});
+        const half8_t ka = i8x8_to_f16(u32x2_t{io.k[s][2 * m], io.k[s][2 * m + 1]});
         cacc = mfma16x16x32(ka, qhi[m], cacc);
         cacc = mfma16x16x32(ka, qlo[m], cacc);
       }
       sc[s] = cacc;
     }
 
-    // ---- online softmax (log2 domain; q carries scale*log2e) ----
+    // ---- 3. prefetch next tile's K and V ----
+    if (more) issue_kv(tn);
+
+    // ---- 4. online softmax (log2 domain; q carries scale*log2e) ----
     float p[2][4];
     bool valid[2][4];
     float mt = kNegInf;
@@ -290,9 +352,8 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tok = tb + 16 * s + 4 * g + i;
-        valid[s][i] = tok < t1;
-        const float x = sc[s][i] * ksc[s][i];
+        valid[s][i] = (tb + 16 * s + 4 * g + i) < t1;
+        const float x = sc[s][i] * io.ks[s][i];
         p[s][i] = valid[s][i] ? x : kNegInf;
         mt = fmaxf(mt, p[s][i]);
       }
@@ -317,10 +378,9 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
 
-    // ---- PV ----
-    // P' = p * (V scale | Lloyd-Max norm) split into fp16 hi + lo: a single
-    // fp16 rounding of the weights costs up to 2^-11 relative per term, which
-    // outputs formed by cancellation of large outlier-channel terms amplify.
+    // ---- 5. P' = p * (V scale | Lloyd-Max norm) as fp16 hi + lo ----
+    // A single fp16 rounding of the weights costs up to 2^-11 relative per
+    // term, which outputs formed by cancellation of large terms amplify.
     half8_t pbh[C::NB], pbl[C::NB];
 #pragma unroll
     for (int nb = 0; nb < C::NB; ++nb) {
@@ -328,43 +388,49 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float w = valid[s][i] ? p[s][i] * vsc[s][nb][i] : 0.0f;
+          const float w = valid[s][i] ? p[s][i] * io.vs[s][nb][i] : 0.0f;
           const _Float16 wh = (_Float16)w;
           pbh[nb][4 * s + i] = wh;
           pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
         }
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+    // ---- 6. prefetch next tile's scales ----
+    if (more) issue_scales(tn);
+
+    // ---- 7. PV: A = V^T through LDS transpose reads, B = P'^T ----
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) {
       half8_t va;
       if constexpr (!K8V3) {
         const int off = (8 * g + ((lane >> 1) & 7)) * C::VROW + 16 * n + 8 * (lane & 1);
-        i32x2_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((S8KV_LDS i32x2_t*)(vstage + off));
+        const i32x2_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((S8KV_LDS i32x2_t*)(vstage + off));
         va = i8x8_to_f16(__builtin_bit_cast(u32x2_t, t));
       } else {
         const int r0 = 8 * g + ((lane >> 2) & 3);
         const int colb = (16 * n + 4 * (lane & 3)) * 2;
-        i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + r0 * C::VROW + colb));
-        i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + (r0 + 4) * C::VROW + colb));
-        half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
+        const i16x4_t lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + r0 * C::VROW + colb));
+        const i16x4_t hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + (r0 + 4) * C::VROW + colb));
+        const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
         va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
       }
       const int nb = C::NB == 1 ? 0 : (16 * n) / 128;
       acc[n] = mfma16x16x32(va, pbh[nb], acc[n]);
       acc[n] = mfma16x16x32(va, pbl[nb], acc[n]);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    tb = tn;
   }
 
-  // ---- merge the 4 waves of the workgroup ----
+  // ---- merge the waves of the workgroup in LDS ----
   float l_tot = l_run;
   l_tot += shfl_xor_f(l_tot, 16);
   l_tot += shfl_xor_f(l_tot, 32);
   __syncthreads();  // every wave is done with its V staging
   float* mrg = reinterpret_cast<float*>(smem);
-  float* w_acc = mrg + wave * (16 * D + 32);  // [16 heads][D] then m[16], l[16]
+  float* w_acc = mrg + wave * (16 * D + 32);  // [16 heads][D], then m[16], l[16]
   if (c < G) {
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) {
@@ -377,21 +443,18 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
     }
   }
   __syncthreads();
-  // every thread combines some (head, dim) outputs
+  const int64_t part0 = (int64_t)b * a.n_splits;
   for (int i = tid; i < G * D; i += 64 * kDecWaves) {
     const int cc = i / D, d = i - cc * D;
-    float mw[kDecWaves];
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) {
-      mw[w] = mrg[w * (16 * D + 32) + 16 * D + cc];
-      M = fmaxf(M, mw[w]);
-    }
+    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, mrg[w * (16 * D + 32) + 16 * D + cc]);
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) {
       const float* wa = mrg + w * (16 * D + 32);
-      const float f = (mw[w] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+      const float mw = wa[16 * D + cc];
+      const float f = (mw == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       num += f * wa[cc * D + d];
       den += f * wa[16 * D + 16 + cc];
     }
@@ -399,7 +462,7 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
     if (n_split_b == 1) {
       a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
     } else {
-      const int64_t pi = ((int64_t)b * a.n_splits + split) * a.num_q_heads + hq;
+      const int64_t pi = (part0 + split) * a.num_q_heads + hq;
       a.ws_acc[pi * D + d] = num;
       if (d == 0) {
         a.ws_ml[pi * 2] = M;
@@ -409,39 +472,32 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
   }
 }
 
-// Combine the context splits of one (row, q head): one wave per output row.
+// Combine the context splits of (row b, kv head h): one workgroup per pair,
+// each thread producing outputs (head, dim) of the G query heads.
 template <int D>
-__global__ __launch_bounds__(64) void merge_kernel(DecodeArgs a) {
-  const int hq = blockIdx.x;
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+  const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int L = min(a.context_lens[b], a.max_context_len);
   if (L <= 0) return;
   const int n = (L + a.split_tokens - 1) / a.split_tokens;
   if (n <= 1) return;
-  const int lane = threadIdx.x;
-  const int64_t base = (int64_t)b * a.n_splits;
-  float M = kNegInf;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, a.ws_ml[((base + s) * a.num_q_heads + hq) * 2]);
-  constexpr int E = D >= 64 ? D / 64 : 1;
-  float num[E];
-#pragma unroll
-  for (int j = 0; j < E; ++j) num[j] = 0.0f;
-  float den = 0.0f;
-  for (int s = 0; s < n; ++s) {
-    const int64_t pi = (base + s) * a.num_q_heads + hq;
-    const float ms = a.ws_ml[pi * 2];
-    const float f = (ms == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    den += f * a.ws_ml[pi * 2 + 1];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) num[j] += f * a.ws_acc[pi * D + d];
+  const int G = a.group;
+  const int64_t part0 = (int64_t)b * a.n_splits;
+  for (int i = threadIdx.x; i < G * D; i += 256) {
+    const int cc = i / D, d = i - cc * D;
+    const int hq = h * G + cc;
+    float M = kNegInf;
+    for (int sp = 0; sp < n; ++sp) M = fmaxf(M, a.ws_ml[((part0 + sp) * a.num_q_heads + hq) * 2]);
+    float num = 0.0f, den = 0.0f;
+    for (int sp = 0; sp < n; ++sp) {
+      const int64_t pi = (part0 + sp) * a.num_q_heads + hq;
+      const float ms = a.ws_ml[pi * 2];
+      const float f = (ms == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+      den += f * a.ws_ml[pi * 2 + 1];
+      num += f * a.ws_acc[pi * D + d];
     }
-  }
-#pragma unroll
-  for (int j = 0; j < E; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num[j] / den : 0.0f);
+    a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
   }
 }
 
@@ -466,6 +522,7 @@ static SplitPlan plan_split(int batch, int num_kv_heads, int max_context_len) {
     tpw = 1;
     while (tpw * 2 <= t && tpw < 64) tpw *= 2;
   }
+  while (tpw > 1 && tpw * kTile * kDecWaves > kMaxSplitTokens) tpw >>= 1;
   SplitPlan p;
   p.split_tokens = tpw * kTile * kDecWaves;
   const int mc = max_context_len > 0 ? max_context_len : 1;
@@ -475,12 +532,11 @@ static SplitPlan plan_split(int batch, int num_kv_heads, int max_context_len) {
 
 template <int D, bool K8V3>
 static int launch_decode(DecodeArgs& a, int batch, hipStream_t stream) {
-  dim3 grid(a.n_splits, a.num_kv_heads, batch);
+  dim3 grid(a.num_kv_heads, batch, a.n_splits);
   hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), 0, stream, a);
   int rc = check_launch("s8kv_decode");
-  if (rc) return rc;
-  if (a.n_splits > 1) {
-    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_q_heads, batch), dim3(64), 0, stream, a);
+  if (rc == S8KV_OK && a.n_splits > 1) {
+    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_kv_heads, batch), dim3(256), 0, stream, a);
     rc = check_launch("s8kv_decode(merge)");
   }
   return rc;

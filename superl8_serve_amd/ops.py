@@ -173,7 +173,7 @@ def _decode_prep(q, k_cache, block_table, context_lens, block_size, max_context_
              f"max_context_len {max_context_len} exceeds the block table capacity {block_table.shape[1] * bs}")
     out = torch.empty((b, hq, 1, d) if not squeeze else (b, hq, d), dtype=torch.float16, device=dev)
     ws_bytes = decode_workspace_bytes(b, hq, hkv, d, max_context_len)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     return q3, block_table, context_lens, out, ws, ws_bytes, (n, hkv, bs, d, b, hq), max_context_len
 
 
