@@ -26,6 +26,8 @@
 // second launch.)
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "s8kv_device.h"
 #include "s8kv_host.h"
 
@@ -34,6 +36,7 @@ namespace s8kv {
 constexpr int kDecWaves = 4;
 constexpr int kTile = 32;
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kMaxSlack = 8.0f;  // lazy softmax max: rescale only past this (log2 units)
 constexpr int kMaxSplitTokens = 2048;                     // bounds the staged block ids
 constexpr int kMaxSplitBlocks = kMaxSplitTokens / 4 + 2;  // block_size >= 4
 
@@ -50,11 +53,8 @@ struct DecCfg {
   // distinct banks.
   static constexpr int VROW = K8V3 ? (2 * D + 32) : (D + 16);
   static constexpr int VSTAGE = kTile * VROW;                 // bytes per wave
-  static constexpr int MERGE = kDecWaves * (16 * D + 32) * 4; // cross-wave merge
   static constexpr int VLOADS = K8V3 ? (kTile * NG) / 64 : (kTile * D / 16) / 64;  // V loads per lane per tile
   static constexpr int SMEM_A = kDecWaves * VSTAGE;
-  static constexpr int SMEM_MAIN = SMEM_A > MERGE ? SMEM_A : MERGE;
-  static constexpr int SMEM = SMEM_MAIN + kMaxSplitBlocks * 4;  // + block ids of the split
 };
 
 struct DecodeArgs {
@@ -72,6 +72,8 @@ struct DecodeArgs {
   const int32_t* context_lens;
   int bs_log2;
   int max_context_len;  // every row is clamped to it (block-table rows hold this many tokens)
+  int smem_main;        // LDS bytes before the staged block ids (V staging, then the merge)
+  int q_vec;            // q rows are 16-byte aligned: load them with 16-byte loads
   int split_tokens;
   int n_splits;
   float qscale;    // softmax scale * log2(e) * 1/sqrt(D) (rotation norm)
@@ -87,14 +89,14 @@ __device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) 
 
 
 template <int KCH>
-__device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4]) {
+__device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4], uint32_t soff = 0) {
   if constexpr (KCH == 8) {
-    u32x2_t v = bload64(r, off);
+    u32x2_t v = bload64(r, off, soff);
     dst[0] = v.x; dst[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < KCH / 16; ++i) {
-      u32x4_t v = bload128(r, off + 16 * i);
+      u32x4_t v = bload128(r, off + 16 * i, soff);
       dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
     }
   }
@@ -126,8 +128,9 @@ struct TileIO {
 template <int D, bool K8V3>
 __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
-  __shared__ __attribute__((aligned(16))) char smem[C::SMEM];
-  int* bt_lds = reinterpret_cast<int*>(smem + C::SMEM_MAIN);
+  // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids]
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
 
   // Workgroups are dealt to the 8 XCDs round-robin by linear id, so the KV
   // head varies fastest and the context split slowest: every XCD then gets
@@ -159,52 +162,8 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
   const int bs_log2 = a.bs_log2;
   const int fb = t0 >> bs_log2;  // first block of the split
 
-  // ---- block ids of the split -> LDS ----
   const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
-  const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
-  for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
-
-  // ---- q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
-  // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32) ----
-  half8_t qhi[C::NQK], qlo[C::NQK];
-  {
-    float x[C::KCH];
-    const _Float16* qp =
-        a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + (c < G ? c : 0)) * a.q_stride_h + g * C::KCH;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) x[i] = (c < G) ? (float)qp[i] : 0.0f;
-#pragma unroll
-    for (int hs = 1; hs < C::KCH; hs <<= 1) {
-#pragma unroll
-      for (int i = 0; i < C::KCH; ++i) {
-        if ((i & hs) == 0) {
-          const float x0 = x[i], x1 = x[i + hs];
-          x[i] = x0 + x1;
-          x[i + hs] = x0 - x1;
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 16; m <= 32; m <<= 1) {
-      const bool upper = (lane & m) != 0;
-#pragma unroll
-      for (int i = 0; i < C::KCH; ++i) {
-        const float p = shfl_xor_f(x[i], m);
-        x[i] = upper ? (p - x[i]) : (x[i] + p);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < C::NQK; ++m) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float val = x[8 * m + e] * a.qscale;
-        const _Float16 hi = (_Float16)val;
-        qhi[m][e] = hi;
-        qlo[m][e] = (_Float16)(val - (float)hi);
-      }
-    }
-  }
-  __syncthreads();  // block ids visible
+  half8_t qhi[C::NQK], qlo[C::NQK];  // rotated, pre-scaled q (filled after the first loads issue)
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
@@ -233,43 +192,77 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
   }
 
   TileIO<D, K8V3> io;
-  auto issue_kv = [&](int tb) {
+  // A 32-token tile never crosses a block when block_size >= 32: the tile's
+  // first storage row is then wave-uniform and rides in the buffer loads'
+  // scalar offset, while each lane's vector offset is a loop constant.
+  const bool tile_in_block = bs_log2 >= 5;
+  constexpr int LPR = D / 16;    // int8 V: lanes per 16-byte-chunked row
+  constexpr int RPI = 64 / LPR;  // int8 V: rows per load instruction
+  auto tile_row0 = [&](int tb) -> uint32_t {
+    const uint32_t blk = (uint32_t)bt_lds[(tb >> bs_log2) - fb];
+    return __builtin_amdgcn_readfirstlane(((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tb & bsm));
+  };
+  auto issue_kv = [&](int tb, uint32_t r0) {
+    if (tile_in_block) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        load_kchunk<C::KCH>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
+      if constexpr (!K8V3) {
+#pragma unroll
+        for (int j = 0; j < C::VLOADS; ++j)
+          io.v[j] = bload128(vc, (uint32_t)((j * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
+      } else {
+#pragma unroll
+        for (int j = 0; j < C::VLOADS; ++j) {
+          const int job = j * 64 + lane;
+          const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
+          const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
+          io.v[j].x = bload32(vc, off, so);
+          io.v[j].y = bload32(vc, off + 4, so);
+          io.v[j].z = bload32(vc, off + 8, so);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const uint32_t row = row_of(min(tb + 16 * s + c, last));
       load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
     }
     if constexpr (!K8V3) {
-      constexpr int LPR = D / 16;    // lanes per V row (16 B each)
-      constexpr int RPI = 64 / LPR;  // rows per load instruction
 #pragma unroll
       for (int j = 0; j < C::VLOADS; ++j) {
-        const int tt = j * RPI + lane / LPR;
-        const uint32_t row = row_of(min(tb + tt, last));
+        const uint32_t row = row_of(min(tb + j * RPI + lane / LPR, last));
         io.v[j] = bload128(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
       }
     } else {
 #pragma unroll
       for (int j = 0; j < C::VLOADS; ++j) {
         const int job = j * 64 + lane;
-        const int tt = job / C::NG, gi = job % C::NG;
-        const uint32_t row = row_of(min(tb + tt, last));
-        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)(gi * 12);
+        const uint32_t row = row_of(min(tb + job / C::NG, last));
+        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
         io.v[j].x = bload32(vc, base);
         io.v[j].y = bload32(vc, base + 4);
         io.v[j].z = bload32(vc, base + 8);
       }
     }
   };
-  auto issue_scales = [&](int tb) {
+  auto issue_scales = [&](int tb, uint32_t r0) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const uint32_t row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
-      io.ks[s] = bloadf4(ks, row * 4u);
-      if constexpr (C::NB == 1) {
-        io.vs[s][0] = bloadf4(vs, row * 4u);
+      uint32_t row, so;
+      if (tile_in_block) {
+        row = (uint32_t)(16 * s + 4 * g);
+        so = r0;
       } else {
-        const float4_t n0 = bloadf4(vs, row * 8u), n1 = bloadf4(vs, row * 8u + 16u);
+        row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
+        so = 0;
+      }
+      io.ks[s] = bloadf4(ks, row * 4u, so * 4u);
+      if constexpr (C::NB == 1) {
+        io.vs[s][0] = bloadf4(vs, row * 4u, so * 4u);
+      } else {
+        const float4_t n0 = bloadf4(vs, row * 8u, so * 8u), n1 = bloadf4(vs, row * 8u + 16u, so * 8u);
         io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
         io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
       }
@@ -282,19 +275,16 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
 #pragma unroll
   for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  int tb = t0 + kTile * wave;
-  if (tb < t1) {
-    issue_kv(tb);
-    issue_scales(tb);
-  }
-  while (tb < t1) {
+  // One 32-token tile: MASKED only for a wave's last tile (may run past t1);
+  // PREFETCH issues the loads of the wave's next tile, which then always exists.
+  auto process = [&](int tb, auto masked_tag, auto prefetch_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool PREFETCH = decltype(prefetch_tag)::value;
     const int tn = tb + kTile * kDecWaves;
-    const bool more = tn < t1;
+    uint32_t rn = 0;
 
     // ---- 1. V tile -> LDS (int8 rows, or K8V3 codes expanded to fp16 rows) ----
     if constexpr (!K8V3) {
-      constexpr int LPR = D / 16;
-      constexpr int RPI = 64 / LPR;
 #pragma unroll
       for (int j = 0; j < C::VLOADS; ++j) {
         const int tt = j * RPI + lane / LPR;
@@ -341,42 +331,47 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       sc[s] = cacc;
     }
 
-    // ---- 3. prefetch next tile's K and V ----
-    if (more) issue_kv(tn);
+    // ---- 3. prefetch the next tile's K and V ----
+    if constexpr (PREFETCH) {
+      if (tile_in_block) rn = tile_row0(tn);
+      issue_kv(tn, rn);
+    }
 
     // ---- 4. online softmax (log2 domain; q carries scale*log2e) ----
+    // The running max is raised lazily: only when some head's tile max
+    // exceeds it by more than kMaxSlack, so p <= 2^kMaxSlack and most tiles
+    // skip the accumulator rescale.
     float p[2][4];
-    bool valid[2][4];
     float mt = kNegInf;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        valid[s][i] = (tb + 16 * s + 4 * g + i) < t1;
-        const float x = sc[s][i] * io.ks[s][i];
-        p[s][i] = valid[s][i] ? x : kNegInf;
-        mt = fmaxf(mt, p[s][i]);
+        float x = sc[s][i] * io.ks[s][i];
+        if constexpr (MASKED) x = (tb + 16 * s + 4 * g + i) < t1 ? x : kNegInf;
+        p[s][i] = x;
+        mt = fmaxf(mt, x);
       }
     }
     mt = fmaxf(mt, shfl_xor_f(mt, 16));
     mt = fmaxf(mt, shfl_xor_f(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const bool any = m_new != kNegInf;
-    const float alpha = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    float psum = 0.0f;
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+      l_run *= alpha;
+#pragma unroll
+      for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
+      m_run = m_new;
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = (valid[s][i] && any) ? __builtin_amdgcn_exp2f(p[s][i] - m_new) : 0.0f;
+        const float e = __builtin_amdgcn_exp2f(p[s][i] - m_run);  // exp2(-inf) = 0 for masked tokens
         p[s][i] = e;
-        psum += e;
+        l_run += e;
       }
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
 
     // ---- 5. P' = p * (V scale | Lloyd-Max norm) as fp16 hi + lo ----
     // A single fp16 rounding of the weights costs up to 2^-11 relative per
@@ -388,7 +383,9 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float w = valid[s][i] ? p[s][i] * io.vs[s][nb][i] : 0.0f;
+          float w = p[s][i] * io.vs[s][nb][i];
+          // masked tokens: p = 0 but the scale past the row end may be any value
+          if constexpr (MASKED) w = (tb + 16 * s + 4 * g + i) < t1 ? w : 0.0f;
           const _Float16 wh = (_Float16)w;
           pbh[nb][4 * s + i] = wh;
           pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
@@ -396,8 +393,8 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       }
     }
 
-    // ---- 6. prefetch next tile's scales ----
-    if (more) issue_scales(tn);
+    // ---- 6. prefetch the next tile's scales ----
+    if constexpr (PREFETCH) issue_scales(tn, rn);
 
     // ---- 7. PV: A = V^T through LDS transpose reads, B = P'^T ----
 #pragma unroll
@@ -421,7 +418,78 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       acc[n] = mfma16x16x32(va, pbh[nb], acc[n]);
       acc[n] = mfma16x16x32(va, pbl[nb], acc[n]);
     }
-    tb = tn;
+  };
+
+  int tb = t0 + kTile * wave;
+
+  // ---- block ids of the split -> LDS ----
+  const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
+  for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
+
+  // ---- q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
+  // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32) ----
+  {
+    float x[C::KCH];
+    const _Float16* qp =
+        a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + (c < G ? c : 0)) * a.q_stride_h + g * C::KCH;
+    if (a.q_vec) {
+#pragma unroll
+      for (int i = 0; i < C::KCH / 8; ++i) {
+        const half8_t v8 = (c < G) ? *reinterpret_cast<const half8_t*>(qp + 8 * i) : half8_t{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)v8[e];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) x[i] = (c < G) ? (float)qp[i] : 0.0f;
+    }
+#pragma unroll
+    for (int hs = 1; hs < C::KCH; hs <<= 1) {
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        if ((i & hs) == 0) {
+          const float x0 = x[i], x1 = x[i + hs];
+          x[i] = x0 + x1;
+          x[i + hs] = x0 - x1;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) {
+      const bool upper = (lane & m) != 0;
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        const float p = shfl_xor_f(x[i], m);
+        x[i] = upper ? (p - x[i]) : (x[i] + p);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < C::NQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float val = x[8 * m + e] * a.qscale;
+        const _Float16 hi = (_Float16)val;
+        qhi[m][e] = hi;
+        qlo[m][e] = (_Float16)(val - (float)hi);
+      }
+    }
+  }
+  __syncthreads();  // block ids visible
+  // (Issuing the first tile before this prologue hides its latency but keeps
+  // the tile's registers live across the q rotation, costing a wave of
+  // occupancy per SIMD -- slower overall.)
+  if (tb < t1) {
+    const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
+    issue_kv(tb, r0);
+    issue_scales(tb, r0);
+  }
+
+  if (tb < t1) {
+    while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
+      process(tb, std::false_type{}, std::true_type{});
+      tb += kTile * kDecWaves;
+    }
+    process(tb, std::true_type{}, std::false_type{});
   }
 
   // ---- merge the waves of the workgroup in LDS ----
@@ -430,7 +498,8 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
   l_tot += shfl_xor_f(l_tot, 32);
   __syncthreads();  // every wave is done with its V staging
   float* mrg = reinterpret_cast<float*>(smem);
-  float* w_acc = mrg + wave * (16 * D + 32);  // [16 heads][D], then m[16], l[16]
+  const int wstride = G * D + 32;
+  float* w_acc = mrg + wave * wstride;  // [G heads][D], then m[16], l[16]
   if (c < G) {
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) {
@@ -438,8 +507,8 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
       for (int r = 0; r < 4; ++r) w_acc[c * D + 16 * n + 4 * g + r] = acc[n][r];
     }
     if (g == 0) {
-      w_acc[16 * D + c] = m_run;
-      w_acc[16 * D + 16 + c] = l_tot;
+      w_acc[G * D + c] = m_run;
+      w_acc[G * D + 16 + c] = l_tot;
     }
   }
   __syncthreads();
@@ -448,15 +517,15 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
     const int cc = i / D, d = i - cc * D;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, mrg[w * (16 * D + 32) + 16 * D + cc]);
+    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, mrg[w * wstride + G * D + cc]);
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) {
-      const float* wa = mrg + w * (16 * D + 32);
-      const float mw = wa[16 * D + cc];
+      const float* wa = mrg + w * wstride;
+      const float mw = wa[G * D + cc];
       const float f = (mw == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       num += f * wa[cc * D + d];
-      den += f * wa[16 * D + 16 + cc];
+      den += f * wa[G * D + 16 + cc];
     }
     const int hq = h * G + cc;
     if (n_split_b == 1) {
@@ -532,8 +601,21 @@ static SplitPlan plan_split(int batch, int num_kv_heads, int max_context_len) {
 
 template <int D, bool K8V3>
 static int launch_decode(DecodeArgs& a, int batch, hipStream_t stream) {
+  using C = DecCfg<D, K8V3>;
+  const int merge = kDecWaves * (a.group * D + 32) * 4;
+  a.smem_main = ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
+  const int smem = a.smem_main + kMaxSplitBlocks * 4;
+  static bool attr_set = false;  // allow more than 64 KiB of dynamic LDS (head_dim 256)
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      set_error("s8kv_decode: cannot raise the dynamic LDS limit");
+      return S8KV_ERR_LAUNCH;
+    }
+    attr_set = true;
+  }
   dim3 grid(a.num_kv_heads, batch, a.n_splits);
-  hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), 0, stream, a);
+  hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, a);
   int rc = check_launch("s8kv_decode");
   if (rc == S8KV_OK && a.n_splits > 1) {
     hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_kv_heads, batch), dim3(256), 0, stream, a);
@@ -575,6 +657,7 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
   }
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
+  a.q_vec = ((uintptr_t)a.q % 16 == 0) && (a.q_stride_b % 8 == 0) && (a.q_stride_h % 8 == 0);
   SplitPlan p = plan_split(batch, num_kv_heads, max_context_len);
   a.split_tokens = p.split_tokens;
   a.n_splits = p.n_splits;

@@ -34,17 +34,18 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+// `off` is the per-lane (VGPR) byte offset, `soff` a wave-uniform (SGPR) one.
+__device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
 }
-__device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+__device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, 0));
 }
-__device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+__device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, 0);
 }
-__device__ __forceinline__ float4_t bloadf4(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+__device__ __forceinline__ float4_t bloadf4(rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
 }
 __device__ __forceinline__ void bstore128(u32x4_t v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, 0);
