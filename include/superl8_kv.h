@@ -70,8 +70,11 @@ int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens, int num_k
 
 /*
  * Bytes of scratch device memory the decode entry points need for this
- * geometry (0 when no split of the context is used).  Depends only on its
- * arguments, so a caller can size the workspace once per graph bucket.
+ * geometry on the current device (partial softmax states of rows split across
+ * workgroups).  Depends only on its arguments and the device's compute-unit
+ * count, so a caller can size the workspace once per graph bucket;
+ * max_context_len does not change it.  The workspace needs no initialisation
+ * and calls that overlap on one workspace race.
  */
 int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                    int max_context_len);
@@ -88,8 +91,9 @@ int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
  * block_table: int32 [batch, >= ceil(max_context_len/block_size)] with row
  * stride block_table_stride; row b is read only for its first
  * ceil(context_lens[b]/block_size) entries.  context_lens: int32 [batch].
- * max_context_len >= max(context_lens) sizes the context split; a row whose
- * context_lens entry exceeds it is truncated to max_context_len tokens.
+ * max_context_len >= max(context_lens) bounds the block-table width read; a
+ * row whose context_lens entry exceeds it is truncated to max_context_len
+ * tokens.  A row with context length 0 yields zeros.
  * out: fp16 [batch, num_q_heads, head_dim] contiguous.
  * Row b, head h attends tokens [0, context_lens[b]) of KV head
  * h / (num_q_heads / num_kv_heads) with softmax scale `scale`, applying the

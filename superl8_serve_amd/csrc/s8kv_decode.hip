@@ -1,11 +1,23 @@
 // Ragged-batch GQA decode attention over the paged int8 / K8V3 cache.
 //
-// Work decomposition: one workgroup (4 waves) per (kv head h, sequence b,
-// context split), in that grid order (XCD balance, see the kernel).  Each wave walks 32-token tiles of its split (tiles w, w+4,
-// ... of the split) and keeps an online softmax for the G = Hq/Hkv query heads
-// that share the KV head, so every KV byte is read once for all G heads.
+// Scheduling (stream-K): the grid holds about as many workgroups as the GPU
+// keeps resident, wg_per_head of them per KV head.  For its head, each
+// workgroup takes an equal, contiguous slice of the concatenation of all rows'
+// tokens (each row padded to a multiple of 32), so ragged context lengths
+// never leave part of the GPU idle.  A slice may end inside one row and start
+// the next; the part of a row inside one slice is a "segment".  A row covered
+// by a single segment is written directly, otherwise every segment writes a
+// (max, sum, acc) partial and merge_kernel combines them.  Each row also
+// occupies `ghost` stream tokens that are not processed: they charge the fixed
+// cost of a segment (q set-up, merge) to the slice that holds it.  A
+// segment's set-up loads (q, first block ids) are issued before the previous
+// segment's merge so their latency hides behind it.  Workgroup id
+// wg = j * Hkv + h, so the round-robin deal of workgroups to the 8 XCDs gives
+// every XCD the same share of every head.
 //
-// Per 32-token tile a wave does:
+// Inside a segment the 4 waves of the workgroup take 32-token tiles in turn
+// (tiles w, w+4, ...) and keep an online softmax for the G = Hq/Hkv query heads
+// of the KV head, so every KV byte is read once for all G heads.  Per tile:
 //   QK  : S[token][head] on MFMA 16x16x32 f16.  A = K rows (int8 -> fp16 is
 //         exact) loaded straight from HBM in MFMA operand layout; B = the
 //         rotated, pre-scaled q split into fp16 hi + lo parts (two MFMAs), so
@@ -13,17 +25,15 @@
 //   softmax: lane (head c = lane%16, group g = lane/16) owns tokens
 //         {4g..4g+3} and {16+4g..16+4g+3} of the tile; the running max is
 //         shared across the 4 groups with two lane shuffles.
-//   PV  : O^T[dim][head] on MFMA 16x16x32 f16.  B = P^T taken from the lane's
-//         own softmax values (times the per-token V scale / norm, split into
-//         fp16 hi + lo) -- no shuffle; A = V^T read from an LDS copy of the tile with the gfx950
-//         transpose read ds_read_b64_tr_b8 (int8) / ds_read_b64_tr_b16 (K8V3
-//         dequantized to fp16 in LDS).
-// The 4 waves of a workgroup merge in LDS.  With more than one context split
-// per row every workgroup writes (max, sum, acc) partials to the workspace and
-// merge_kernel combines them.  (Combining them in the last-arriving workgroup
-// needs agent-scope release/acquire fences, which on this multi-XCD part
-// write back and invalidate the whole L2 per workgroup -- far costlier than a
-// second launch.)
+//   PV  : O^T[dim][head] on MFMA 16x16x32 f16.  B = P^T from the lane's own
+//         softmax values (times the per-token V scale / norm, split into fp16
+//         hi + lo) -- no shuffle; A = V^T read from an LDS copy of the tile
+//         with the gfx950 transpose reads ds_read_b64_tr_b8 (int8) /
+//         ds_read_b64_tr_b16 (K8V3 codes expanded to fp16 in LDS).
+// The next tile's loads are issued while the current one computes.
+// (Combining partials in the last-arriving workgroup would need agent-scope
+// release/acquire fences, which on this multi-XCD part write back and
+// invalidate the whole L2 per workgroup -- far costlier than a second launch.)
 #include <stdlib.h>
 
 #include <type_traits>
@@ -36,9 +46,11 @@ namespace s8kv {
 constexpr int kDecWaves = 4;
 constexpr int kTile = 32;
 constexpr float kNegInf = -__builtin_inff();
-constexpr float kMaxSlack = 8.0f;  // lazy softmax max: rescale only past this (log2 units)
-constexpr int kMaxSplitTokens = 2048;                     // bounds the staged block ids
-constexpr int kMaxSplitBlocks = kMaxSplitTokens / 4 + 2;  // block_size >= 4
+constexpr float kMaxSlack = 8.0f;                        // lazy softmax max: rescale only past this (log2 units)
+constexpr int kSubTokens = 2048;                         // block ids are staged in LDS per 2048 tokens
+constexpr int kMaxSubBlocks = kSubTokens / 4 + 2;        // block_size >= 4
+constexpr int kMaxResidentPerCU = 8;                     // bound used to size the workspace
+constexpr int kGhostTokens = 256;                        // stream tokens charged per row start
 
 template <int D, bool K8V3>
 struct DecCfg {
@@ -60,7 +72,7 @@ struct DecCfg {
 struct DecodeArgs {
   const _Float16* q;
   int64_t q_stride_b, q_stride_h;
-  int num_q_heads, num_kv_heads, group;
+  int batch, num_q_heads, num_kv_heads, group;
   const void* k_cache;
   const void* k_scale;
   const void* v_cache;   // int8 V or int32 packed V
@@ -74,19 +86,53 @@ struct DecodeArgs {
   int max_context_len;  // every row is clamped to it (block-table rows hold this many tokens)
   int smem_main;        // LDS bytes before the staged block ids (V staging, then the merge)
   int q_vec;            // q rows are 16-byte aligned: load them with 16-byte loads
-  int split_tokens;
-  int n_splits;
-  float qscale;    // softmax scale * log2(e) * 1/sqrt(D) (rotation norm)
+  int wg_per_head;      // workgroups per KV head (slices of the token stream)
+  int slots;            // partial slots per head: batch + wg_per_head
+  int ghost;            // stream tokens charged per row for its fixed costs (multiple of 32)
+  float qscale;         // softmax scale * log2(e) * 1/sqrt(D) (rotation norm)
   _Float16* out;
-  float* ws_ml;    // [B][n_splits][Hq][2]
-  float* ws_acc;   // [B][n_splits][Hq][D]
+  float* ws_ml;         // [Hkv][slots][G][2]  (max, sum) of each segment
+  float* ws_acc;        // [Hkv][slots][G][D]  unnormalized output of each segment
 };
+
+__device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
+  return max(0, min(a.context_lens[b], a.max_context_len));
+}
+__device__ __forceinline__ int padded32(int n) { return (n + 31) & ~31; }
+
+// Length of row b's part of the token stream: its tokens padded to a multiple
+// of 32, plus `ghost` tokens that stand for a segment's fixed costs (q set-up,
+// merge) so that slices holding row starts get fewer real tokens.  Empty rows
+// take no space.
+__device__ __forceinline__ int stream_len(const DecodeArgs& a, int L) { return L > 0 ? padded32(L) + a.ghost : 0; }
+
+// Slice length of each workgroup of a head: equal shares of the token stream,
+// a multiple of 32.  decode_kernel and merge_kernel must agree.
+__device__ __forceinline__ int slice_len(int total, int wg_per_head) {
+  const int s = (total + wg_per_head - 1) / wg_per_head;
+  return max(kTile, padded32(s));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// Stream length of all rows (every wave computes it; no barrier).
+__device__ __forceinline__ int stream_total(const DecodeArgs& a, int lane) {
+  int t = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int r = c0 + lane;
+    t += wave_sum_i(r < a.batch ? stream_len(a, row_len(a, r)) : 0);
+  }
+  return __builtin_amdgcn_readfirstlane(t);
+}
 
 // Position of tile token tt (0..31) in the LDS-staged V tile: lane group g's
 // eight transpose-read rows (tokens 4g..4g+3 and 16+4g..16+4g+3) are
 // consecutive rows 8g..8g+7.
 __device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
-
 
 template <int KCH>
 __device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4], uint32_t soff = 0) {
@@ -113,9 +159,6 @@ __device__ __forceinline__ u32x2_t cb_lookup4(uint32_t sel, uint32_t lo03, uint3
   return r;
 }
 
-// Split the workgroup's tiles over its waves and stream them with a one-tile
-// software pipeline: the next tile's K/V loads are issued right after this
-// tile's QK MFMAs, its scales after this tile's softmax.
 template <int D, bool K8V3>
 struct TileIO {
   using C = DecCfg<D, K8V3>;
@@ -126,58 +169,78 @@ struct TileIO {
 };
 
 template <int D, bool K8V3>
-__global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
   // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids]
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
 
-  // Workgroups are dealt to the 8 XCDs round-robin by linear id, so the KV
-  // head varies fastest and the context split slowest: every XCD then gets
-  // an equal share of (row, head) pairs, whereas split-fastest ordering would
-  // send all first splits (present for every row) to one XCD.
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int split = blockIdx.z;
-  const int L = min(a.context_lens[b], a.max_context_len);
-  const int t0 = split * a.split_tokens;
+  const int Hkv = a.num_kv_heads;
+  const int h = blockIdx.x % Hkv;
+  const int j = blockIdx.x / Hkv;
   const int G = a.group;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int c = lane & 15;
-  const int g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  if (L <= 0) {  // empty row: defined as zeros
-    if (split == 0) {
-      for (int i = tid; i < G * D; i += 64 * kDecWaves)
-        a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
-    }
-    return;
+  // ---- this workgroup's slice [lo, hi) of the token stream ----
+  const int total = stream_total(a, lane);
+  if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
+    for (int b = 0; b < a.batch; ++b)
+      if (row_len(a, b) == 0)
+        for (int i = tid; i < G * D; i += 64 * kDecWaves)
+          a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
   }
-  if (t0 >= L) return;
-  const int t1 = min(L, t0 + a.split_tokens);
-  const int n_split_b = (L + a.split_tokens - 1) / a.split_tokens;
-  const int last = L - 1;
-  const int bs_log2 = a.bs_log2;
-  const int fb = t0 >> bs_log2;  // first block of the split
+  const int S = slice_len(total, a.wg_per_head);
+  const int lo = j * S;
+  if (lo >= total) return;
+  const int hi = min(total, lo + S);
 
-  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
-  half8_t qhi[C::NQK], qlo[C::NQK];  // rotated, pre-scaled q (filled after the first loads issue)
+  // ---- first row whose stream range holds lo: wave-level prefix scan ----
+  int b = 0, pb = 0;  // row, and the start of its stream range
+  {
+    int carry = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int r = c0 + lane;
+      const int v = r < a.batch ? stream_len(a, row_len(a, r)) : 0;
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+      }
+      incl += carry;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(incl > lo);
+      if (m != 0) {
+        const int f = __builtin_ctzll(m);
+        b = c0 + f;
+        pb = __shfl(incl - v, f);
+        break;
+      }
+      carry = __shfl(incl, 63);
+    }
+  }
+  b = __builtin_amdgcn_readfirstlane(b);
+  pb = __builtin_amdgcn_readfirstlane(pb);
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
   const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
   char* vstage = smem + wave * C::VSTAGE;
-  const uint32_t hkv = (uint32_t)a.num_kv_heads;
+  const uint32_t hkv = (uint32_t)Hkv;
+  const int bs_log2 = a.bs_log2;
   const uint32_t bsm = (1u << bs_log2) - 1u;
-
-  // storage row of token `tok` (already clamped to the row's last token)
-  auto row_of = [&](int tok) -> uint32_t {
-    const uint32_t blk = (uint32_t)bt_lds[(tok >> bs_log2) - fb];
-    return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tok & bsm);
-  };
+  // A 32-token tile never crosses a block when block_size >= 32: the tile's
+  // first storage row is then wave-uniform and rides in the buffer loads'
+  // scalar offset, while each lane's vector offset is a loop constant.
+  const bool tile_in_block = bs_log2 >= 5;
+  constexpr int LPR = D / 16;    // int8 V: lanes per 16-byte-chunked row
+  constexpr int RPI = 64 / LPR;  // int8 V: rows per load instruction
+  // block ids staged per segment start: the first sub-split's (at most kSubTokens tokens)
+  const int bt_width = (a.max_context_len + (1 << bs_log2) - 1) >> bs_log2;  // readable entries per row
+  const int bt_first = (kSubTokens >> bs_log2) + 1;
+  constexpr int kBtRegs = (kMaxSubBlocks + 64 * kDecWaves - 1) / (64 * kDecWaves);
 
   // K8V3 codebook byte tables (fp16 of the fp32 codebook).
   uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
@@ -185,388 +248,492 @@ __global__ __launch_bounds__(64 * kDecWaves, 2) void decode_kernel(DecodeArgs a)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
-      const uint32_t lo = hb & 0xFFu, hi = hb >> 8;
-      if (i < 4) { tlo03 |= lo << (8 * i); thi03 |= hi << (8 * i); }
-      else { tlo47 |= lo << (8 * (i - 4)); thi47 |= hi << (8 * (i - 4)); }
+      const uint32_t lw = hb & 0xFFu, hw = hb >> 8;
+      if (i < 4) { tlo03 |= lw << (8 * i); thi03 |= hw << (8 * i); }
+      else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
     }
   }
 
-  TileIO<D, K8V3> io;
-  // A 32-token tile never crosses a block when block_size >= 32: the tile's
-  // first storage row is then wave-uniform and rides in the buffer loads'
-  // scalar offset, while each lane's vector offset is a loop constant.
-  const bool tile_in_block = bs_log2 >= 5;
-  constexpr int LPR = D / 16;    // int8 V: lanes per 16-byte-chunked row
-  constexpr int RPI = 64 / LPR;  // int8 V: rows per load instruction
-  auto tile_row0 = [&](int tb) -> uint32_t {
-    const uint32_t blk = (uint32_t)bt_lds[(tb >> bs_log2) - fb];
-    return __builtin_amdgcn_readfirstlane(((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tb & bsm));
-  };
-  auto issue_kv = [&](int tb, uint32_t r0) {
-    if (tile_in_block) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        load_kchunk<C::KCH>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
-      if constexpr (!K8V3) {
-#pragma unroll
-        for (int j = 0; j < C::VLOADS; ++j)
-          io.v[j] = bload128(vc, (uint32_t)((j * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
-      } else {
-#pragma unroll
-        for (int j = 0; j < C::VLOADS; ++j) {
-          const int job = j * 64 + lane;
-          const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-          const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
-          io.v[j].x = bload32(vc, off, so);
-          io.v[j].y = bload32(vc, off + 4, so);
-          io.v[j].z = bload32(vc, off + 8, so);
-        }
-      }
-      return;
+  // Advance (b, pb) to the first row from b on whose real tokens
+  // [pb + ghost, pb + ghost + padded32(L)) overlap [lo, hi); returns its
+  // length, or 0 when the slice holds no further segment.
+  auto find_segment = [&](int& rb, int& rpb) -> int {
+    for (; rb < a.batch && rpb + a.ghost < hi; ++rb) {
+      const int L = __builtin_amdgcn_readfirstlane(row_len(a, rb));
+      if (L == 0) continue;
+      if (rpb + a.ghost + padded32(L) > lo) return L;
+      rpb += stream_len(a, L);
     }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const uint32_t row = row_of(min(tb + 16 * s + c, last));
-      load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
-    }
-    if constexpr (!K8V3) {
-#pragma unroll
-      for (int j = 0; j < C::VLOADS; ++j) {
-        const uint32_t row = row_of(min(tb + j * RPI + lane / LPR, last));
-        io.v[j] = bload128(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < C::VLOADS; ++j) {
-        const int job = j * 64 + lane;
-        const uint32_t row = row_of(min(tb + job / C::NG, last));
-        const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
-        io.v[j].x = bload32(vc, base);
-        io.v[j].y = bload32(vc, base + 4);
-        io.v[j].z = bload32(vc, base + 8);
-      }
-    }
-  };
-  auto issue_scales = [&](int tb, uint32_t r0) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      uint32_t row, so;
-      if (tile_in_block) {
-        row = (uint32_t)(16 * s + 4 * g);
-        so = r0;
-      } else {
-        row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
-        so = 0;
-      }
-      io.ks[s] = bloadf4(ks, row * 4u, so * 4u);
-      if constexpr (C::NB == 1) {
-        io.vs[s][0] = bloadf4(vs, row * 4u, so * 4u);
-      } else {
-        const float4_t n0 = bloadf4(vs, row * 8u, so * 8u), n1 = bloadf4(vs, row * 8u + 16u, so * 8u);
-        io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
-        io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
-      }
-    }
+    return 0;
   };
 
-  float m_run = kNegInf;
-  float l_run = 0.0f;
-  float4_t acc[C::NPV];
-#pragma unroll
-  for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  // One 32-token tile: MASKED only for a wave's last tile (may run past t1);
-  // PREFETCH issues the loads of the wave's next tile, which then always exists.
-  auto process = [&](int tb, auto masked_tag, auto prefetch_tag) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    constexpr bool PREFETCH = decltype(prefetch_tag)::value;
-    const int tn = tb + kTile * kDecWaves;
-    uint32_t rn = 0;
-
-    // ---- 1. V tile -> LDS (int8 rows, or K8V3 codes expanded to fp16 rows) ----
-    if constexpr (!K8V3) {
-#pragma unroll
-      for (int j = 0; j < C::VLOADS; ++j) {
-        const int tt = j * RPI + lane / LPR;
-        *reinterpret_cast<u32x4_t*>(vstage + lds_row_of(tt) * C::VROW + (lane % LPR) * 16) = io.v[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < C::VLOADS; ++j) {
-        const int job = j * 64 + lane;
-        const int tt = job / C::NG, gi = job % C::NG;
-        const uint32_t w0 = io.v[j].x, w1 = io.v[j].y, w2 = io.v[j].z;
-        char* dst = vstage + lds_row_of(tt) * C::VROW + gi * 64;
-#pragma unroll
-        for (int q4 = 0; q4 < 8; q4 += 2) {
-          u32x4_t o;
-          {
-            const int i = 4 * q4;
-            const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-            const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
-            o.x = r.x; o.y = r.y;
-          }
-          {
-            const int i = 4 * q4 + 4;
-            const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-            const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
-            o.z = r.x; o.w = r.y;
-          }
-          *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
-        }
-      }
-    }
-
-    // ---- 2. QK ----
-    float4_t sc[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < C::NQK; ++m) {
-        const half8_t ka = i8x8_to_f16(u32x2_t{io.k[s][2 * m], io.k[s][2 * m + 1]});
-        cacc = mfma16x16x32(ka, qhi[m], cacc);
-        cacc = mfma16x16x32(ka, qlo[m], cacc);
-      }
-      sc[s] = cacc;
-    }
-
-    // ---- 3. prefetch the next tile's K and V ----
-    if constexpr (PREFETCH) {
-      if (tile_in_block) rn = tile_row0(tn);
-      issue_kv(tn, rn);
-    }
-
-    // ---- 4. online softmax (log2 domain; q carries scale*log2e) ----
-    // The running max is raised lazily: only when some head's tile max
-    // exceeds it by more than kMaxSlack, so p <= 2^kMaxSlack and most tiles
-    // skip the accumulator rescale.
-    float p[2][4];
-    float mt = kNegInf;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = sc[s][i] * io.ks[s][i];
-        if constexpr (MASKED) x = (tb + 16 * s + 4 * g + i) < t1 ? x : kNegInf;
-        p[s][i] = x;
-        mt = fmaxf(mt, x);
-      }
-    }
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
-    if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
-      l_run *= alpha;
-#pragma unroll
-      for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
-      m_run = m_new;
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(p[s][i] - m_run);  // exp2(-inf) = 0 for masked tokens
-        p[s][i] = e;
-        l_run += e;
-      }
-    }
-
-    // ---- 5. P' = p * (V scale | Lloyd-Max norm) as fp16 hi + lo ----
-    // A single fp16 rounding of the weights costs up to 2^-11 relative per
-    // term, which outputs formed by cancellation of large terms amplify.
-    half8_t pbh[C::NB], pbl[C::NB];
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float w = p[s][i] * io.vs[s][nb][i];
-          // masked tokens: p = 0 but the scale past the row end may be any value
-          if constexpr (MASKED) w = (tb + 16 * s + 4 * g + i) < t1 ? w : 0.0f;
-          const _Float16 wh = (_Float16)w;
-          pbh[nb][4 * s + i] = wh;
-          pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
-        }
-      }
-    }
-
-    // ---- 6. prefetch the next tile's scales ----
-    if constexpr (PREFETCH) issue_scales(tn, rn);
-
-    // ---- 7. PV: A = V^T through LDS transpose reads, B = P'^T ----
-#pragma unroll
-    for (int n = 0; n < C::NPV; ++n) {
-      half8_t va;
-      if constexpr (!K8V3) {
-        const int off = (8 * g + ((lane >> 1) & 7)) * C::VROW + 16 * n + 8 * (lane & 1);
-        const i32x2_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((S8KV_LDS i32x2_t*)(vstage + off));
-        va = i8x8_to_f16(__builtin_bit_cast(u32x2_t, t));
-      } else {
-        const int r0 = 8 * g + ((lane >> 2) & 3);
-        const int colb = (16 * n + 4 * (lane & 3)) * 2;
-        const i16x4_t lo =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + r0 * C::VROW + colb));
-        const i16x4_t hi =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + (r0 + 4) * C::VROW + colb));
-        const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
-        va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-      }
-      const int nb = C::NB == 1 ? 0 : (16 * n) / 128;
-      acc[n] = mfma16x16x32(va, pbh[nb], acc[n]);
-      acc[n] = mfma16x16x32(va, pbl[nb], acc[n]);
-    }
-  };
-
-  int tb = t0 + kTile * wave;
-
-  // ---- block ids of the split -> LDS ----
-  const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
-  for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
-
-  // ---- q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
-  // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32) ----
-  {
-    float x[C::KCH];
+  // Set-up loads of a segment that starts at token 0 of row rb (or at s0 for
+  // the slice's first row): the lane's raw q fragment and the first
+  // sub-split's block ids, issued early so their latency overlaps other work.
+  half8_t qraw[C::KCH / 8];
+  int btv[kBtRegs];
+  auto prefetch_segment = [&](int rb, int s0) {
+    const int tid_o = opaque_int(threadIdx.x);
+    const int cl = tid_o & 15, gl = (tid_o & 63) >> 4;
     const _Float16* qp =
-        a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + (c < G ? c : 0)) * a.q_stride_h + g * C::KCH;
+        a.q + (int64_t)rb * a.q_stride_b + (int64_t)(h * G + (cl < G ? cl : 0)) * a.q_stride_h + gl * C::KCH;
     if (a.q_vec) {
 #pragma unroll
+      for (int i = 0; i < C::KCH / 8; ++i)
+        qraw[i] = (cl < G) ? *reinterpret_cast<const half8_t*>(qp + 8 * i) : half8_t{};
+    } else {  // unaligned q view: element loads, 8 in flight at a time (rare path)
+#pragma unroll
       for (int i = 0; i < C::KCH / 8; ++i) {
-        const half8_t v8 = (c < G) ? *reinterpret_cast<const half8_t*>(qp + 8 * i) : half8_t{};
+        half8_t t;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)v8[e];
+        for (int e = 0; e < 8; ++e) t[e] = (cl < G) ? qp[8 * i + e] : (_Float16)0.0f;
+        qraw[i] = t;
+        asm volatile("" : "+v"(qraw[i]));
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < C::KCH; ++i) x[i] = (c < G) ? (float)qp[i] : 0.0f;
     }
+    const int fb = s0 >> bs_log2;
+    const int32_t* bt_row = a.block_table + (int64_t)rb * a.bt_stride + fb;
 #pragma unroll
-    for (int hs = 1; hs < C::KCH; hs <<= 1) {
+    for (int k = 0; k < kBtRegs; ++k) {
+      const int i = tid_o + k * 64 * kDecWaves;
+      btv[k] = (i < bt_first && fb + i < bt_width) ? bt_row[i] : 0;
+    }
+  };
+  auto store_prefetched_bt = [&]() {
+    const int tid_o = opaque_int(threadIdx.x);
 #pragma unroll
-      for (int i = 0; i < C::KCH; ++i) {
-        if ((i & hs) == 0) {
-          const float x0 = x[i], x1 = x[i + hs];
-          x[i] = x0 + x1;
-          x[i + hs] = x0 - x1;
+    for (int k = 0; k < kBtRegs; ++k) {
+      const int i = tid_o + k * 64 * kDecWaves;
+      if (i < bt_first) bt_lds[i] = btv[k];
+    }
+  };
+
+  int L = find_segment(b, pb);
+  if (L == 0) return;
+  prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
+  store_prefetched_bt();
+
+  // ---- segments: rows overlapping [lo, hi), in order ----
+  for (;;) {
+    __syncthreads();  // staged block ids visible; the previous merge is done with LDS
+    // per-lane values of this segment's q set-up and merge, from an opaque
+    // copy of the thread id (see the tile loop below)
+    const int tid = opaque_int(threadIdx.x);
+    const int lane = tid & 63;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int padL = padded32(L);
+    const int rs = pb + a.ghost;              // stream position of the row's token 0
+    const int s0 = max(lo, rs) - rs;          // segment [s0, s1) in row coordinates
+    const int s1 = min(hi, rs + padL) - rs;   // multiples of 32; s0 < L
+    const bool whole_row = (s0 == 0) && (s1 == padL);
+    const int last = L - 1;
+    const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+
+    // q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
+    // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32)
+    half8_t qhi[C::NQK], qlo[C::NQK];
+    {
+      float x[C::KCH];
+#pragma unroll
+      for (int i = 0; i < C::KCH / 8; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)qraw[i][e];
+      }
+#pragma unroll
+      for (int hs = 1; hs < C::KCH; hs <<= 1) {
+#pragma unroll
+        for (int i = 0; i < C::KCH; ++i) {
+          if ((i & hs) == 0) {
+            const float x0 = x[i], x1 = x[i + hs];
+            x[i] = x0 + x1;
+            x[i + hs] = x0 - x1;
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 16; m <= 32; m <<= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < C::KCH; ++i) {
+          const float p = shfl_xor_f(x[i], m);
+          x[i] = upper ? (p - x[i]) : (x[i] + p);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < C::NQK; ++m) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float val = x[8 * m + e] * a.qscale;
+          const _Float16 qh = (_Float16)val;
+          qhi[m][e] = qh;
+          qlo[m][e] = (_Float16)(val - (float)qh);
         }
       }
     }
-#pragma unroll
-    for (int m = 16; m <= 32; m <<= 1) {
-      const bool upper = (lane & m) != 0;
-#pragma unroll
-      for (int i = 0; i < C::KCH; ++i) {
-        const float p = shfl_xor_f(x[i], m);
-        x[i] = upper ? (p - x[i]) : (x[i] + p);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < C::NQK; ++m) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float val = x[8 * m + e] * a.qscale;
-        const _Float16 hi = (_Float16)val;
-        qhi[m][e] = hi;
-        qlo[m][e] = (_Float16)(val - (float)hi);
-      }
-    }
-  }
-  __syncthreads();  // block ids visible
-  // (Issuing the first tile before this prologue hides its latency but keeps
-  // the tile's registers live across the q rotation, costing a wave of
-  // occupancy per SIMD -- slower overall.)
-  if (tb < t1) {
-    const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
-    issue_kv(tb, r0);
-    issue_scales(tb, r0);
-  }
 
-  if (tb < t1) {
-    while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
-      process(tb, std::false_type{}, std::true_type{});
-      tb += kTile * kDecWaves;
-    }
-    process(tb, std::true_type{}, std::false_type{});
-  }
+    float m_run = kNegInf;
+    float l_run = 0.0f;
+    float4_t acc[C::NPV];
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  // ---- merge the waves of the workgroup in LDS ----
-  float l_tot = l_run;
-  l_tot += shfl_xor_f(l_tot, 16);
-  l_tot += shfl_xor_f(l_tot, 32);
-  __syncthreads();  // every wave is done with its V staging
-  float* mrg = reinterpret_cast<float*>(smem);
-  const int wstride = G * D + 32;
-  float* w_acc = mrg + wave * wstride;  // [G heads][D], then m[16], l[16]
-  if (c < G) {
+    // ---- sub-splits of <= kSubTokens tokens; the first one's block ids are staged ----
+    for (int u0 = s0; u0 < s1; u0 += kSubTokens) {
+      const int u1 = min(s1, u0 + kSubTokens);
+      const int t1 = min(u1, L);               // valid tokens end
+      const int fb = u0 >> bs_log2;
+      // Lane-derived addresses of the tile loop are recomputed per sub-split:
+      // the opaque copy of the thread id stops the compiler from hoisting them
+      // out of the segment loop, where they would stay live across the q
+      // set-up and the merge and cost a wave per SIMD of occupancy.
+      const int lane = opaque_int(tid) & 63;  // shadows the segment's lane, c, g
+      const int c = lane & 15;
+      const int g = lane >> 4;
+      if (u0 != s0) {  // later sub-splits of a long segment: stage their block ids now
+        const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
+        __syncthreads();
+        for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
+        __syncthreads();
+      }
+
+      // storage row of token `tok` (already clamped to the row's last token)
+      auto row_of = [&](int tok) -> uint32_t {
+        const uint32_t blk = (uint32_t)bt_lds[(tok >> bs_log2) - fb];
+        return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tok & bsm);
+      };
+      auto tile_row0 = [&](int tb) -> uint32_t {
+        const uint32_t blk = (uint32_t)bt_lds[(tb >> bs_log2) - fb];
+        return __builtin_amdgcn_readfirstlane(((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tb & bsm));
+      };
+
+      TileIO<D, K8V3> io;
+      auto issue_kv = [&](int tb, uint32_t r0) {
+        if (tile_in_block) {
 #pragma unroll
-    for (int n = 0; n < C::NPV; ++n) {
+          for (int s = 0; s < 2; ++s)
+            load_kchunk<C::KCH>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
+          if constexpr (!K8V3) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w_acc[c * D + 16 * n + 4 * g + r] = acc[n][r];
-    }
-    if (g == 0) {
-      w_acc[G * D + c] = m_run;
-      w_acc[G * D + 16 + c] = l_tot;
-    }
-  }
-  __syncthreads();
-  const int64_t part0 = (int64_t)b * a.n_splits;
-  for (int i = tid; i < G * D; i += 64 * kDecWaves) {
-    const int cc = i / D, d = i - cc * D;
-    float M = kNegInf;
+            for (int jj = 0; jj < C::VLOADS; ++jj)
+              io.v[jj] = bload128(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
+          } else {
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, mrg[w * wstride + G * D + cc]);
-    float num = 0.0f, den = 0.0f;
+            for (int jj = 0; jj < C::VLOADS; ++jj) {
+              const int job = jj * 64 + lane;
+              const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
+              const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
+              io.v[jj].x = bload32(vc, off, so);
+              io.v[jj].y = bload32(vc, off + 4, so);
+              io.v[jj].z = bload32(vc, off + 8, so);
+            }
+          }
+          return;
+        }
 #pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) {
-      const float* wa = mrg + w * wstride;
-      const float mw = wa[G * D + cc];
-      const float f = (mw == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      num += f * wa[cc * D + d];
-      den += f * wa[G * D + 16 + cc];
-    }
-    const int hq = h * G + cc;
-    if (n_split_b == 1) {
-      a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
-    } else {
-      const int64_t pi = (part0 + split) * a.num_q_heads + hq;
-      a.ws_acc[pi * D + d] = num;
-      if (d == 0) {
-        a.ws_ml[pi * 2] = M;
-        a.ws_ml[pi * 2 + 1] = den;
+        for (int s = 0; s < 2; ++s) {
+          const uint32_t row = row_of(min(tb + 16 * s + c, last));
+          load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
+        }
+        if constexpr (!K8V3) {
+#pragma unroll
+          for (int jj = 0; jj < C::VLOADS; ++jj) {
+            const uint32_t row = row_of(min(tb + jj * RPI + lane / LPR, last));
+            io.v[jj] = bload128(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
+          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < C::VLOADS; ++jj) {
+            const int job = jj * 64 + lane;
+            const uint32_t row = row_of(min(tb + job / C::NG, last));
+            const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
+            io.v[jj].x = bload32(vc, base);
+            io.v[jj].y = bload32(vc, base + 4);
+            io.v[jj].z = bload32(vc, base + 8);
+          }
+        }
+      };
+      auto issue_scales = [&](int tb, uint32_t r0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          uint32_t row, so;
+          if (tile_in_block) {
+            row = (uint32_t)(16 * s + 4 * g);
+            so = r0;
+          } else {
+            row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
+            so = 0;
+          }
+          io.ks[s] = bloadf4(ks, row * 4u, so * 4u);
+          if constexpr (C::NB == 1) {
+            io.vs[s][0] = bloadf4(vs, row * 4u, so * 4u);
+          } else {
+            const float4_t n0 = bloadf4(vs, row * 8u, so * 8u), n1 = bloadf4(vs, row * 8u + 16u, so * 8u);
+            io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
+            io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
+          }
+        }
+      };
+
+      // One 32-token tile: MASKED only for a wave's last tile of the sub-split
+      // (may run past t1); PREFETCH issues the loads of the wave's next tile,
+      // which then always exists.
+      auto process = [&](int tb, auto masked_tag, auto prefetch_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        constexpr bool PREFETCH = decltype(prefetch_tag)::value;
+        const int tn = tb + kTile * kDecWaves;
+        uint32_t rn = 0;
+
+        // 1. V tile -> LDS (int8 rows, or K8V3 codes expanded to fp16 rows)
+        if constexpr (!K8V3) {
+#pragma unroll
+          for (int jj = 0; jj < C::VLOADS; ++jj) {
+            const int tt = jj * RPI + lane / LPR;
+            *reinterpret_cast<u32x4_t*>(vstage + lds_row_of(tt) * C::VROW + (lane % LPR) * 16) = io.v[jj];
+          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < C::VLOADS; ++jj) {
+            const int job = jj * 64 + lane;
+            const int tt = job / C::NG, gi = job % C::NG;
+            const uint32_t w0 = io.v[jj].x, w1 = io.v[jj].y, w2 = io.v[jj].z;
+            char* dst = vstage + lds_row_of(tt) * C::VROW + gi * 64;
+#pragma unroll
+            for (int q4 = 0; q4 < 8; q4 += 2) {
+              u32x4_t o;
+              {
+                const int i = 4 * q4;
+                const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
+                const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+                o.x = r.x; o.y = r.y;
+              }
+              {
+                const int i = 4 * q4 + 4;
+                const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
+                const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+                o.z = r.x; o.w = r.y;
+              }
+              *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
+            }
+          }
+        }
+
+        // 2. QK
+        float4_t sc[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < C::NQK; ++m) {
+            const half8_t ka = i8x8_to_f16(u32x2_t{io.k[s][2 * m], io.k[s][2 * m + 1]});
+            cacc = mfma16x16x32(ka, qhi[m], cacc);
+            cacc = mfma16x16x32(ka, qlo[m], cacc);
+          }
+          sc[s] = cacc;
+        }
+
+        // 3. prefetch the next tile's K and V
+        if constexpr (PREFETCH) {
+          if (tile_in_block) rn = tile_row0(tn);
+          issue_kv(tn, rn);
+        }
+
+        // 4. online softmax (log2 domain; q carries scale*log2e).  The running
+        // max is raised lazily: only when some head's tile max exceeds it by
+        // more than kMaxSlack, so p <= 2^kMaxSlack and most tiles skip the
+        // accumulator rescale.
+        float p[2][4];
+        float mt = kNegInf;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = sc[s][i] * io.ks[s][i];
+            if constexpr (MASKED) x = (tb + 16 * s + 4 * g + i) < t1 ? x : kNegInf;
+            p[s][i] = x;
+            mt = fmaxf(mt, x);
+          }
+        }
+        mt = fmaxf(mt, shfl_xor_f(mt, 16));
+        mt = fmaxf(mt, shfl_xor_f(mt, 32));
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
+          const float m_new = fmaxf(m_run, mt);
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+          l_run *= alpha;
+#pragma unroll
+          for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
+          m_run = m_new;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_amdgcn_exp2f(p[s][i] - m_run);  // exp2(-inf) = 0 for masked tokens
+            p[s][i] = e;
+            l_run += e;
+          }
+        }
+
+        // 5. P' = p * (V scale | Lloyd-Max norm) as fp16 hi + lo.  A single
+        // fp16 rounding of the weights costs up to 2^-11 relative per term,
+        // which outputs formed by cancellation of large terms amplify.
+        half8_t pbh[C::NB], pbl[C::NB];
+#pragma unroll
+        for (int nb = 0; nb < C::NB; ++nb) {
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float w = p[s][i] * io.vs[s][nb][i];
+              // masked tokens: p = 0 but the scale past the row end may be any value
+              if constexpr (MASKED) w = (tb + 16 * s + 4 * g + i) < t1 ? w : 0.0f;
+              const _Float16 wh = (_Float16)w;
+              pbh[nb][4 * s + i] = wh;
+              pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
+            }
+          }
+        }
+
+        // 6. prefetch the next tile's scales
+        if constexpr (PREFETCH) issue_scales(tn, rn);
+
+        // 7. PV: A = V^T through LDS transpose reads, B = P'^T
+#pragma unroll
+        for (int n = 0; n < C::NPV; ++n) {
+          half8_t va;
+          if constexpr (!K8V3) {
+            const int off = (8 * g + ((lane >> 1) & 7)) * C::VROW + 16 * n + 8 * (lane & 1);
+            const i32x2_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((S8KV_LDS i32x2_t*)(vstage + off));
+            va = i8x8_to_f16(__builtin_bit_cast(u32x2_t, t));
+          } else {
+            const int r0 = 8 * g + ((lane >> 2) & 3);
+            const int colb = (16 * n + 4 * (lane & 3)) * 2;
+            const i16x4_t lw =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + r0 * C::VROW + colb));
+            const i16x4_t hw =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vstage + (r0 + 4) * C::VROW + colb));
+            const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
+            va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+          }
+          const int nb = C::NB == 1 ? 0 : (16 * n) / 128;
+          acc[n] = mfma16x16x32(va, pbh[nb], acc[n]);
+          acc[n] = mfma16x16x32(va, pbl[nb], acc[n]);
+        }
+      };
+
+      int tb = u0 + kTile * wave;
+      if (tb < t1) {
+        const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
+        issue_kv(tb, r0);
+        issue_scales(tb, r0);
+        while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
+          process(tb, std::false_type{}, std::true_type{});
+          tb += kTile * kDecWaves;
+        }
+        process(tb, std::true_type{}, std::false_type{});
       }
     }
+
+    // ---- next segment: its set-up loads overlap this segment's merge ----
+    int nb = b + 1, npb = pb + stream_len(a, L);
+    const int nL = find_segment(nb, npb);
+    // (unconditional, from a valid row when there is no next segment: values
+    // set on only one path would stay live across the tile loop)
+    prefetch_segment(nL != 0 ? nb : b, 0);
+
+    // ---- merge the waves of the workgroup in LDS ----
+    {
+    const int tid = opaque_int(threadIdx.x);
+    const int lane = tid & 63;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    float l_tot = l_run;
+    l_tot += shfl_xor_f(l_tot, 16);
+    l_tot += shfl_xor_f(l_tot, 32);
+    __syncthreads();  // every wave is done with its V staging and the staged block ids
+    float* mrg = reinterpret_cast<float*>(smem);
+    const int wstride = G * D + 32;
+    float* w_acc = mrg + wave * wstride;  // [G heads][D], then m[16], l[16]
+    if (c < G) {
+#pragma unroll
+      for (int n = 0; n < C::NPV; ++n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w_acc[c * D + 16 * n + 4 * g + r] = acc[n][r];
+      }
+      if (g == 0) {
+        w_acc[G * D + c] = m_run;
+        w_acc[G * D + 16 + c] = l_tot;
+      }
+    }
+    __syncthreads();
+    store_prefetched_bt();  // bt_lds is free: every wave left its tile loop
+    const int64_t slot = ((int64_t)h * a.slots + (j + b)) * G;  // (row, slice) -> unique slot j + b
+    for (int i = tid; i < G * D; i += 64 * kDecWaves) {
+      const int cc = i / D, d = i - cc * D;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, mrg[w * wstride + G * D + cc]);
+      float num = 0.0f, den = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float* wa = mrg + w * wstride;
+        const float mw = wa[G * D + cc];
+        const float f = (mw == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+        num += f * wa[cc * D + d];
+        den += f * wa[G * D + 16 + cc];
+      }
+      if (whole_row) {
+        a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
+      } else {
+        a.ws_acc[(slot + cc) * D + d] = num;
+        if (d == 0) {
+          a.ws_ml[(slot + cc) * 2] = M;
+          a.ws_ml[(slot + cc) * 2 + 1] = den;
+        }
+      }
+    }
+    }
+    if (nL == 0) break;
+    b = nb;
+    pb = npb;
+    L = nL;
   }
 }
 
-// Combine the context splits of (row b, kv head h): one workgroup per pair,
-// each thread producing outputs (head, dim) of the G query heads.
+// Combine the segments of (row b, KV head h): recompute the row's position in
+// the token stream (as decode_kernel does) and merge the partials of slices
+// j_first..j_last, stored at slots j + b.
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int L = min(a.context_lens[b], a.max_context_len);
-  if (L <= 0) return;
-  const int n = (L + a.split_tokens - 1) / a.split_tokens;
-  if (n <= 1) return;
+  const int L = row_len(a, b);
+  if (L == 0) return;
+  const int lane = threadIdx.x & 63;
+  const int total = stream_total(a, lane);
+  int pb = 0;
+  for (int c0 = 0; c0 < b; c0 += 64) {
+    const int r = c0 + lane;
+    pb += wave_sum_i(r < b ? stream_len(a, row_len(a, r)) : 0);
+  }
+  const int S = slice_len(total, a.wg_per_head);
+  const int rs = pb + a.ghost;
+  const int jf = rs / S, jl = (rs + padded32(L) - 1) / S;
+  if (jf == jl) return;  // one segment: decode_kernel wrote the row
   const int G = a.group;
-  const int64_t part0 = (int64_t)b * a.n_splits;
   for (int i = threadIdx.x; i < G * D; i += 256) {
     const int cc = i / D, d = i - cc * D;
-    const int hq = h * G + cc;
     float M = kNegInf;
-    for (int sp = 0; sp < n; ++sp) M = fmaxf(M, a.ws_ml[((part0 + sp) * a.num_q_heads + hq) * 2]);
+    for (int jj = jf; jj <= jl; ++jj) M = fmaxf(M, a.ws_ml[(((int64_t)h * a.slots + jj + b) * G + cc) * 2]);
     float num = 0.0f, den = 0.0f;
-    for (int sp = 0; sp < n; ++sp) {
-      const int64_t pi = (part0 + sp) * a.num_q_heads + hq;
+    for (int jj = jf; jj <= jl; ++jj) {
+      const int64_t pi = ((int64_t)h * a.slots + jj + b) * G + cc;
       const float ms = a.ws_ml[pi * 2];
       const float f = (ms == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
       den += f * a.ws_ml[pi * 2 + 1];
       num += f * a.ws_acc[pi * D + d];
     }
-    a.out[((int64_t)b * a.num_q_heads + hq) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
+    a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
   }
 }
 
@@ -574,61 +741,92 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // Host side
 // ---------------------------------------------------------------------------
 
-struct SplitPlan {
-  int split_tokens;
-  int n_splits;
-};
+// Compute units of the current device (cached per device id).
+static int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < kMaxDevices && cached[dev] > 0) return cached[dev];
+  int cus = 256;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev] = cus;
+  return cus;
+}
 
-// Tiles per wave so that a batch of rows with mean length ~max/2 yields about
-// 8 waves per SIMD (256 CUs x 4 SIMDs).  S8KV_DECODE_TILES_PER_WAVE overrides.
-static SplitPlan plan_split(int batch, int num_kv_heads, int max_context_len) {
-  int tpw = 0;
-  if (const char* env = getenv("S8KV_DECODE_TILES_PER_WAVE")) tpw = atoi(env);
-  if (tpw <= 0) {
-    const int64_t est_tiles = (int64_t)batch * num_kv_heads * ((max_context_len / 2 + kTile - 1) / kTile);
-    const int64_t target_waves = 8192;
-    int64_t t = est_tiles / target_waves;
-    tpw = 1;
-    while (tpw * 2 <= t && tpw < 64) tpw *= 2;
+// Workgroups per KV head: about the number the GPU keeps resident, split
+// evenly over the heads.  S8KV_DECODE_WG_PER_HEAD overrides it (clamped to
+// the bound the workspace is sized for) to exercise other slicings.
+static int max_wg_per_head(int num_kv_heads) {
+  const int w = device_cus() * kMaxResidentPerCU / num_kv_heads;
+  return w > 0 ? w : 1;
+}
+static int plan_wg_per_head(int num_kv_heads, int resident_per_cu) {
+  const int cap = max_wg_per_head(num_kv_heads);
+  int w = device_cus() * resident_per_cu / num_kv_heads;
+  if (const char* env = getenv("S8KV_DECODE_WG_PER_HEAD")) {
+    const int v = atoi(env);
+    if (v > 0) w = v;
   }
-  while (tpw > 1 && tpw * kTile * kDecWaves > kMaxSplitTokens) tpw >>= 1;
-  SplitPlan p;
-  p.split_tokens = tpw * kTile * kDecWaves;
-  const int mc = max_context_len > 0 ? max_context_len : 1;
-  p.n_splits = (mc + p.split_tokens - 1) / p.split_tokens;
-  return p;
+  return w < 1 ? 1 : (w > cap ? cap : w);
 }
 
 template <int D, bool K8V3>
-static int launch_decode(DecodeArgs& a, int batch, hipStream_t stream) {
+static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
-  const int merge = kDecWaves * (a.group * D + 32) * 4;
-  a.smem_main = ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
-  const int smem = a.smem_main + kMaxSplitBlocks * 4;
-  static bool attr_set = false;  // allow more than 64 KiB of dynamic LDS (head_dim 256)
-  if (!attr_set) {
+  const auto smem_main_for = [](int group) {
+    const int merge = kDecWaves * (group * D + 32) * 4;
+    return ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
+  };
+  a.smem_main = smem_main_for(a.group);
+  const int smem = a.smem_main + kMaxSubBlocks * 4;
+  // Resident workgroups per CU at this LDS size (depends on the GQA group),
+  // queried once per group size.
+  static int resident_by_group[17] = {};
+  static bool lds_raised = false;
+  if (!lds_raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            smem_main_for(16) + kMaxSubBlocks * 4) != hipSuccess) {
       set_error("s8kv_decode: cannot raise the dynamic LDS limit");
       return S8KV_ERR_LAUNCH;
     }
-    attr_set = true;
+    lds_raised = true;
   }
-  dim3 grid(a.num_kv_heads, batch, a.n_splits);
-  hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, a);
+  int& resident = resident_by_group[a.group];
+  if (resident == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3>, 64 * kDecWaves, smem) != hipSuccess ||
+        n <= 0)
+      n = 2;
+    resident = n < kMaxResidentPerCU ? n : kMaxResidentPerCU;
+  }
+  a.wg_per_head = plan_wg_per_head(a.num_kv_heads, resident);
+  a.ghost = kGhostTokens;
+  if (const char* env = getenv("S8KV_DECODE_GHOST")) a.ghost = (atoi(env) < 0 ? 0 : atoi(env) + 31) / 32 * 32;
+  a.slots = a.batch + a.wg_per_head;
+  hipLaunchKernelGGL((decode_kernel<D, K8V3>), dim3(a.wg_per_head * a.num_kv_heads), dim3(64 * kDecWaves), smem,
+                     stream, a);
   int rc = check_launch("s8kv_decode");
-  if (rc == S8KV_OK && a.n_splits > 1) {
-    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_kv_heads, batch), dim3(256), 0, stream, a);
+  if (rc == S8KV_OK) {
+    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_kv_heads, a.batch), dim3(256), 0, stream, a);
     rc = check_launch("s8kv_decode(merge)");
   }
   return rc;
 }
 
+static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim) {
+  const int64_t wph = max_wg_per_head(num_kv_heads);
+  return (int64_t)num_q_heads * (batch + wph) * (head_dim + 2) * 4;
+}
+
 static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                          int64_t num_blocks, int block_size, int max_context_len, float scale, void* workspace,
-                         int64_t workspace_bytes, void* stream) {
+                         int64_t workspace_bytes_given, void* stream) {
   S8KV_REQUIRE(batch >= 0, S8KV_ERR_INVALID, "decode: batch < 0");
   if (batch == 0) return S8KV_OK;
+  S8KV_REQUIRE(batch <= 65535, S8KV_ERR_UNSUPPORTED, "decode: batch %d > 65535", batch);
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "decode: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "decode: more than 16 q heads per kv head");
@@ -639,10 +837,13 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
                "decode: block_size %d must be a power of two >= 4", block_size);
   S8KV_REQUIRE(num_blocks > 0, S8KV_ERR_INVALID, "decode: num_blocks must be > 0");
   S8KV_REQUIRE(max_context_len >= 0, S8KV_ERR_INVALID, "decode: max_context_len < 0");
+  S8KV_REQUIRE((int64_t)batch * (max_context_len + 31) < (int64_t(1) << 31), S8KV_ERR_UNSUPPORTED,
+               "decode: batch * max_context_len too large");
   S8KV_REQUIRE(a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.block_table && a.context_lens && a.out,
                S8KV_ERR_INVALID, "decode: null pointer argument");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "decode: per-layer cache exceeds 4 GiB");
+  a.batch = batch;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
@@ -658,23 +859,18 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
   a.q_vec = ((uintptr_t)a.q % 16 == 0) && (a.q_stride_b % 8 == 0) && (a.q_stride_h % 8 == 0);
-  SplitPlan p = plan_split(batch, num_kv_heads, max_context_len);
-  a.split_tokens = p.split_tokens;
-  a.n_splits = p.n_splits;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
-  const int64_t need = s8kv_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, max_context_len);
-  if (need > 0) {
-    S8KV_REQUIRE(workspace != nullptr && workspace_bytes >= need, S8KV_ERR_WORKSPACE,
-                 "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes);
-    a.ws_ml = reinterpret_cast<float*>(workspace);
-    a.ws_acc = a.ws_ml + (int64_t)batch * p.n_splits * num_q_heads * 2;
-  }
+  const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+  S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
+               "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes_given);
+  a.ws_ml = reinterpret_cast<float*>(workspace);
+  a.ws_acc = a.ws_ml + (need / ((int64_t)(head_dim + 2) * 4)) * 2;
   hipStream_t s = (hipStream_t)stream;
   switch (head_dim) {
-    case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false>(a, batch, s);
-    case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false>(a, batch, s);
-    case 128: return k8v3 ? launch_decode<128, true>(a, batch, s) : launch_decode<128, false>(a, batch, s);
-    case 256: return k8v3 ? launch_decode<256, true>(a, batch, s) : launch_decode<256, false>(a, batch, s);
+    case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false>(a, s);
+    case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false>(a, s);
+    case 128: return k8v3 ? launch_decode<128, true>(a, s) : launch_decode<128, false>(a, s);
+    case 256: return k8v3 ? launch_decode<256, true>(a, s) : launch_decode<256, false>(a, s);
   }
   return S8KV_ERR_UNSUPPORTED;
 }
@@ -685,10 +881,9 @@ using namespace s8kv;
 
 extern "C" int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                               int max_context_len) {
+  (void)max_context_len;
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
-  SplitPlan p = plan_split(batch, num_kv_heads, max_context_len);
-  if (p.n_splits <= 1) return 0;
-  return (int64_t)batch * p.n_splits * num_q_heads * (head_dim + 2) * 4;
+  return workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
 }
 
 extern "C" int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,

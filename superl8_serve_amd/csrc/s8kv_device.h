@@ -108,6 +108,14 @@ __device__ __forceinline__ float materialize(float x) {
   return x;
 }
 
+// An opaque copy of a per-lane value: values derived from it are recomputed
+// where they are used instead of being hoisted out of enclosing loops (and
+// held in VGPRs across them).
+__device__ __forceinline__ int opaque_int(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Round-half-even to int, clamped to [-127, 127].  `y` and `scale` are fp32;
 // the division is IEEE correctly rounded (HIP's default fp32 divide).
 __device__ __forceinline__ int rtn_i8(float y, float scale) {

@@ -197,13 +197,34 @@ def test_decode_int8_outlier_channels():
     _assert_attention_close(_decode_gpu_int8(case, cache), _decode_ref(case, cache), "decode outliers")
 
 
-@pytest.mark.parametrize("tpw", ["1", "2"])
-def test_decode_int8_many_splits(tpw, monkeypatch):
-    """Small splits force the multi-split partial + merge path."""
-    monkeypatch.setenv("S8KV_DECODE_TILES_PER_WAVE", tpw)
-    case = make_case(55, 3, 16, 4, 128, 16, [1000, 129, 640])
+@pytest.mark.parametrize(
+    "wg_per_head,ghost,batch,hq,hkv,bs,lens",
+    [
+        # one workgroup per head: every row in one slice, rows past 2048 tokens
+        # streamed in several block-id stages
+        (1, 128, 4, 16, 4, 16, [1000, 129, 5000, 0]),
+        # slices longer than 2048 tokens that end inside a row
+        (2, 0, 4, 8, 2, 256, [5000, 100, 0, 37]),
+        # many short rows: slices span several rows, rows span slices
+        (7, 0, 64, 32, 8, 32, "short"),
+        (7, 128, 64, 32, 8, 32, "short"),
+        # per-row charge larger than the slices: some slices hold no tokens
+        (40, 512, 64, 32, 8, 16, "short"),
+        # block_size < 32: tiles cross blocks
+        (3, 64, 5, 16, 4, 8, [300, 1, 64, 2500, 31]),
+    ],
+)
+def test_decode_int8_slicings(wg_per_head, ghost, batch, hq, hkv, bs, lens, monkeypatch):
+    """Other slicings of the token stream across workgroups: whole rows, rows
+    split across slices (partials + merge), slices spanning several rows, and
+    slices that fall between rows' tokens."""
+    monkeypatch.setenv("S8KV_DECODE_WG_PER_HEAD", str(wg_per_head))
+    monkeypatch.setenv("S8KV_DECODE_GHOST", str(ghost))
+    if lens == "short":
+        lens = np.random.default_rng(5).integers(0, 120, size=batch).tolist()
+    case = make_case(55 + wg_per_head, batch, hq, hkv, 128, bs, lens)
     cache = oracle_fill_int8(case)
-    _assert_attention_close(_decode_gpu_int8(case, cache), _decode_ref(case, cache), f"decode tpw={tpw}")
+    _assert_attention_close(_decode_gpu_int8(case, cache), _decode_ref(case, cache), f"decode wg/head={wg_per_head}")
 
 
 def test_decode_q_transpose_view():
