@@ -139,32 +139,33 @@ def make_step(w):
     return step
 
 
-def time_decode_kernel(w, reps: int) -> float:
-    """Average duration (s) of one decode op, from HIP events recorded on the
-    launch stream around each op while the GPU is kept ahead of the host by a
-    preceding spin kernel (so host launch latency never enters the interval)."""
+def time_decode_kernel(w, reps: int) -> dict:
+    """Average durations of the decode attention kernel and of its merge
+    kernel, from HIP events the library records on the launch stream around
+    each kernel (s8kv_timing_begin/end), over `reps` eager passes of the 36
+    decode calls.  A preceding spin kernel keeps the GPU ahead of the host so
+    host launch latency never enters an interval."""
+    import ctypes
+
     import torch
 
-    from superl8_serve_amd import ops
+    from superl8_serve_amd import _lib, ops
 
+    lib = _lib.load()
     scale = 1.0 / math.sqrt(D)
-    stream = torch.cuda.current_stream()
-    n = reps * NUM_LAYERS
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2e8))  # ~0.1 s of GPU spin while the host enqueues
-    i = 0
+    _lib.check(lib.s8kv_timing_begin(), "s8kv_timing_begin")
     for _ in range(reps):
         for layer in range(NUM_LAYERS):
-            starts[i].record(stream)
             ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
                                          w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
-            ends[i].record(stream)
-            i += 1
+    n = ctypes.c_int(0)
+    dk, mk = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    _lib.check(lib.s8kv_timing_end(ctypes.byref(n), ctypes.byref(dk), ctypes.byref(mk)), "s8kv_timing_end")
     torch.cuda.synchronize()
-    times = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return float(np.mean(times)) * 1e-3
+    launches = max(n.value, 1)
+    return {"decode_s": dk.value * 1e-3 / launches, "merge_s": mk.value * 1e-3 / launches, "launches": n.value}
 
 
 def cpu_baseline(lens: np.ndarray, bt_np: np.ndarray, layers: int) -> dict:
@@ -174,7 +175,9 @@ def cpu_baseline(lens: np.ndarray, bt_np: np.ndarray, layers: int) -> dict:
 
     from oracle import cpu_path
 
-    threads = os.cpu_count() or 1
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(SEED)
     h = cpu_path.hadamard(D)
@@ -227,13 +230,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-layers", type=int, default=NUM_LAYERS, help="layers in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
+                    help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
     ap.add_argument("--kernel-reps", type=int, default=3, help="event-timed decode passes over the 36 layers")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+        print(f"bench.py: measures one GPU only; --gpus {args.gpus} is not supported "
               "(the path shards by sequence or KV head with no exchange; see the design notes)", file=sys.stderr)
         sys.exit(2)
 
@@ -273,8 +278,13 @@ def main():
 
     b = step_bytes(w["lens"])
     value = b["step"] / (ms * 1e-3) / 1e9
-    dec_s = time_decode_kernel(w, args.kernel_reps)
+    kt = time_decode_kernel(w, args.kernel_reps)
+    dec_s = kt["decode_s"]
     achieved = b["decode_layer"] / dec_s / 1e9
+    traffic = None
+    if args.traffic_json and os.path.exists(args.traffic_json):
+        with open(args.traffic_json) as f:
+            traffic = json.load(f).get("decode_kernel_hbm_bytes_per_launch")
     result = {
         "metric": "paged int8 decode-attn+append HBM GB/s (% of peak) at Qwen3-8B shapes, b=64",
         "value": round(value, 2),
@@ -297,10 +307,11 @@ def main():
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "roofline": {
-            "kernel": "decode_kernel<128,int8> (+ split merge)",
+            "kernel": "decode_kernel<128, int8>",
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "avg_launch_us": round(dec_s * 1e6, 2), "algorithmic_bytes_per_launch": b["decode_layer"],
+            "merge_kernel_avg_us": round(kt["merge_s"] * 1e6, 2), "timed_launches": kt["launches"],
         },
     }
     if args.cpu_layers > 0:

@@ -122,6 +122,18 @@ int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
                      void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Kernel timing (diagnostics; no counterpart in the reference).  Between
+ * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
+ * graph capture launches its two kernels with HIP events stamped with each
+ * kernel's start and end; s8kv_timing_end() waits for them and returns the
+ * number of decode calls and the summed durations (ms) of the attention
+ * kernel and of the merge kernel.
+ * Used by the benchmark to time the attention kernel on its own stream.
+ */
+int s8kv_timing_begin(void);
+int s8kv_timing_end(int* launches, double* decode_ms, double* merge_ms);
+
+/*
  * Copy whole physical blocks across every layer of up to 8 cache tensors
  * (copy-on-write of a shared prefix block; compaction of the pool).
  * The reference has no block copy: prefix sharing is refcounted

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports, calls or
 links this module.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker.
+``cpu_baseline`` leg of ``bench.py`` use it, and only to check or time results.
 
 This is a numpy restatement of what the reference (jajmangold/superl8-serve)
 does on its quantized paged-KV path.  The reference's arithmetic lives in the

@@ -36,7 +36,11 @@
 // invalidate the whole L2 per workgroup -- far costlier than a second launch.)
 #include <stdlib.h>
 
+#include <array>
 #include <type_traits>
+#include <vector>
+
+#include <hip/hip_ext.h>
 
 #include "s8kv_device.h"
 #include "s8kv_host.h"
@@ -702,36 +706,62 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
 // Combine the segments of (row b, KV head h): recompute the row's position in
 // the token stream (as decode_kernel does) and merge the partials of slices
-// j_first..j_last, stored at slots j + b.
+// j_first..j_last, stored at slots j + b.  One pass over the context lengths;
+// the partials are read four slices at a time.
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+  __shared__ int red[2][4];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const int tid = threadIdx.x;
   const int L = row_len(a, b);
-  if (L == 0) return;
-  const int lane = threadIdx.x & 63;
-  const int total = stream_total(a, lane);
-  int pb = 0;
-  for (int c0 = 0; c0 < b; c0 += 64) {
-    const int r = c0 + lane;
-    pb += wave_sum_i(r < b ? stream_len(a, row_len(a, r)) : 0);
+  int tot = 0, before = 0;
+  for (int r = tid; r < a.batch; r += 256) {
+    const int v = stream_len(a, row_len(a, r));
+    tot += v;
+    before += r < b ? v : 0;
   }
+  tot = wave_sum_i(tot);
+  before = wave_sum_i(before);
+  if ((tid & 63) == 0) {
+    red[0][tid >> 6] = tot;
+    red[1][tid >> 6] = before;
+  }
+  __syncthreads();
+  if (L == 0) return;
+  const int total = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  const int pb = red[1][0] + red[1][1] + red[1][2] + red[1][3];
   const int S = slice_len(total, a.wg_per_head);
   const int rs = pb + a.ghost;
   const int jf = rs / S, jl = (rs + padded32(L) - 1) / S;
   if (jf == jl) return;  // one segment: decode_kernel wrote the row
   const int G = a.group;
-  for (int i = threadIdx.x; i < G * D; i += 256) {
+  for (int i = tid; i < G * D; i += 256) {
     const int cc = i / D, d = i - cc * D;
-    float M = kNegInf;
-    for (int jj = jf; jj <= jl; ++jj) M = fmaxf(M, a.ws_ml[(((int64_t)h * a.slots + jj + b) * G + cc) * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int jj = jf; jj <= jl; ++jj) {
-      const int64_t pi = ((int64_t)h * a.slots + jj + b) * G + cc;
-      const float ms = a.ws_ml[pi * 2];
-      const float f = (ms == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-      den += f * a.ws_ml[pi * 2 + 1];
-      num += f * a.ws_acc[pi * D + d];
+    float M = kNegInf, num = 0.0f, den = 0.0f;
+    for (int j0 = jf; j0 <= jl; j0 += 4) {
+      float ms[4], ls[4], xs[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int jj = min(j0 + u, jl);
+        const int64_t pi = ((int64_t)h * a.slots + jj + b) * G + cc;
+        ms[u] = j0 + u <= jl ? a.ws_ml[pi * 2] : kNegInf;
+        ls[u] = a.ws_ml[pi * 2 + 1];
+        xs[u] = a.ws_acc[pi * D + d];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (ms[u] == kNegInf) continue;  // past jl, or a segment that saw no token
+        if (ms[u] > M) {
+          const float f = __builtin_amdgcn_exp2f(M - ms[u]);  // 0 while M = -inf
+          num *= f;
+          den *= f;
+          M = ms[u];
+        }
+        const float f = __builtin_amdgcn_exp2f(ms[u] - M);
+        num += f * xs[u];
+        den += f * ls[u];
+      }
     }
     a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
   }
@@ -740,6 +770,29 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+
+// Kernel timing (diagnostics): while enabled, every decode call launches its
+// two kernels with HIP events stamped with each kernel's start and end time
+// (hipExtLaunchKernelGGL).  Calls under graph capture are not timed.
+struct TimingState {
+  bool on = false;
+  std::vector<std::array<hipEvent_t, 4>> events;
+  size_t used = 0;
+};
+static TimingState g_timing;
+
+static hipEvent_t* timing_slot(hipStream_t stream) {
+  if (!g_timing.on) return nullptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  if (g_timing.used == g_timing.events.size()) {
+    std::array<hipEvent_t, 4> e{};
+    for (auto& x : e)
+      if (hipEventCreate(&x) != hipSuccess) return nullptr;
+    g_timing.events.push_back(e);
+  }
+  return g_timing.events[g_timing.used++].data();
+}
 
 // Compute units of the current device (cached per device id).
 static int device_cus() {
@@ -806,11 +859,20 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   a.ghost = kGhostTokens;
   if (const char* env = getenv("S8KV_DECODE_GHOST")) a.ghost = (atoi(env) < 0 ? 0 : atoi(env) + 31) / 32 * 32;
   a.slots = a.batch + a.wg_per_head;
-  hipLaunchKernelGGL((decode_kernel<D, K8V3>), dim3(a.wg_per_head * a.num_kv_heads), dim3(64 * kDecWaves), smem,
-                     stream, a);
+  const dim3 grid(a.wg_per_head * a.num_kv_heads), mgrid(a.num_kv_heads, a.batch);
+  hipEvent_t* ev = timing_slot(stream);
+  if (ev) {  // events stamped with the kernels' own start and end times
+    hipExtLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, a);
+  }
   int rc = check_launch("s8kv_decode");
   if (rc == S8KV_OK) {
-    hipLaunchKernelGGL((merge_kernel<D>), dim3(a.num_kv_heads, a.batch), dim3(256), 0, stream, a);
+    if (ev) {
+      hipExtLaunchKernelGGL((merge_kernel<D>), mgrid, dim3(256), 0, stream, ev[2], ev[3], 0, a);
+    } else {
+      hipLaunchKernelGGL((merge_kernel<D>), mgrid, dim3(256), 0, stream, a);
+    }
     rc = check_launch("s8kv_decode(merge)");
   }
   return rc;
@@ -878,6 +940,34 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
 }  // namespace s8kv
 
 using namespace s8kv;
+
+extern "C" int s8kv_timing_begin(void) {
+  g_timing.on = true;
+  g_timing.used = 0;
+  return S8KV_OK;
+}
+
+extern "C" int s8kv_timing_end(int* launches, double* decode_ms, double* merge_ms) {
+  g_timing.on = false;
+  double dk = 0.0, mk = 0.0;
+  for (size_t i = 0; i < g_timing.used; ++i) {
+    auto& e = g_timing.events[i];
+    if (hipEventSynchronize(e[3]) != hipSuccess) {
+      set_error("s8kv_timing_end: event synchronize failed");
+      return S8KV_ERR_LAUNCH;
+    }
+    float a = 0.f, b = 0.f;
+    hipEventElapsedTime(&a, e[0], e[1]);
+    hipEventElapsedTime(&b, e[2], e[3]);
+    dk += a;
+    mk += b;
+  }
+  if (launches) *launches = (int)g_timing.used;
+  if (decode_ms) *decode_ms = dk;
+  if (merge_ms) *merge_ms = mk;
+  g_timing.used = 0;
+  return S8KV_OK;
+}
 
 extern "C" int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                               int max_context_len) {

@@ -1,5 +1,5 @@
 """Torch-facing ops with the signatures the reference's cache code calls on the
-``superl8`` module (SURVEY boundary; call sites in
+``superl8`` module (the drop-in boundary; call sites in
 ``superl8serve/engine/kv_cache.py``).
 
 Each op checks shapes/dtypes on the host, turns tensors into pointers and
