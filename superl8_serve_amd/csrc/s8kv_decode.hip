@@ -54,7 +54,9 @@ constexpr float kMaxSlack = 8.0f;                        // lazy softmax max: re
 constexpr int kSubTokens = 2048;                         // block ids are staged in LDS per 2048 tokens
 constexpr int kMaxSubBlocks = kSubTokens / 4 + 2;        // block_size >= 4
 constexpr int kMaxResidentPerCU = 8;                     // bound used to size the workspace
+constexpr int kLensLds = 1024;                           // context lengths kept in LDS (rows beyond: global reads)
 constexpr int kGhostTokens = 256;                        // stream tokens charged per row start
+constexpr int kSlotSkewPermille = 200;                   // slice weight skew across residency slots
 
 template <int D, bool K8V3>
 struct DecCfg {
@@ -93,10 +95,13 @@ struct DecodeArgs {
   int wg_per_head;      // workgroups per KV head (slices of the token stream)
   int slots;            // partial slots per head: batch + wg_per_head
   int ghost;            // stream tokens charged per row for its fixed costs (multiple of 32)
+  int slot_classes;     // residency slots per CU the grid fills (slice weighting classes)
+  int slot_skew;        // slice weight skew between the first and last slot, in 1/1000
   float qscale;         // softmax scale * log2(e) * 1/sqrt(D) (rotation norm)
   _Float16* out;
   float* ws_ml;         // [Hkv][slots][G][2]  (max, sum) of each segment
   float* ws_acc;        // [Hkv][slots][G][D]  unnormalized output of each segment
+  int* ws_desc;         // [batch][2]  first and last slice of each split row, -1 if not split
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -110,11 +115,30 @@ __device__ __forceinline__ int padded32(int n) { return (n + 31) & ~31; }
 // take no space.
 __device__ __forceinline__ int stream_len(const DecodeArgs& a, int L) { return L > 0 ? padded32(L) + a.ghost : 0; }
 
-// Slice length of each workgroup of a head: equal shares of the token stream,
-// a multiple of 32.  decode_kernel and merge_kernel must agree.
-__device__ __forceinline__ int slice_len(int total, int wg_per_head) {
-  const int s = (total + wg_per_head - 1) / wg_per_head;
-  return max(kTile, padded32(s));
+// Slices of a head's token stream, one per workgroup j of the head.
+// Workgroups fill the CUs' residency slots in index order (class
+// c = j * classes / W is the slot), and waves of later-dispatched workgroups
+// lose instruction issue to older ones on the same CU, so a slot-c slice is
+// weighted by 1 + skew * (classes - 1 - 2c) / (classes - 1).  Slice lengths
+// are multiples of 32; the last slice runs to the end of the stream.
+__device__ __forceinline__ int slot_first(int c, int W, int classes) { return (c * W + classes - 1) / classes; }
+__device__ __forceinline__ float slot_weight(int c, int classes, int skew_permille) {
+  return classes > 1 ? 1.0f + 0.001f * (float)(skew_permille * (classes - 1 - 2 * c) / (classes - 1)) : 1.0f;
+}
+// Stream position where workgroup j's slice starts (0 <= j < W).
+__device__ __forceinline__ int slice_start(int j, int total, int W, int ncls, int skew_permille) {
+  const int classes = max(1, min(ncls, min(W, kMaxResidentPerCU)));
+  float wsum = 0.0f;
+  for (int c = 0; c < classes; ++c)
+    wsum += (float)(slot_first(c + 1, W, classes) - slot_first(c, W, classes)) * slot_weight(c, classes, skew_permille);
+  const float unit = (float)total / wsum;
+  int pos = 0;
+  for (int c = 0; c < classes; ++c) {
+    const int n = min(j, slot_first(c + 1, W, classes)) - slot_first(c, W, classes);
+    if (n <= 0) break;
+    pos += n * max(kTile, padded32((int)ceilf(unit * slot_weight(c, classes, skew_permille))));
+  }
+  return pos;
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -123,12 +147,17 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// Context length of row b from the LDS copy of the first kLensLds rows.
+__device__ __forceinline__ int lens_at(const DecodeArgs& a, const int* lens_lds, int b) {
+  return b < kLensLds ? lens_lds[b] : row_len(a, b);
+}
+
 // Stream length of all rows (every wave computes it; no barrier).
-__device__ __forceinline__ int stream_total(const DecodeArgs& a, int lane) {
+__device__ __forceinline__ int stream_total(const DecodeArgs& a, const int* lens_lds, int lane) {
   int t = 0;
   for (int c0 = 0; c0 < a.batch; c0 += 64) {
     const int r = c0 + lane;
-    t += wave_sum_i(r < a.batch ? stream_len(a, row_len(a, r)) : 0);
+    t += wave_sum_i(r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0);
   }
   return __builtin_amdgcn_readfirstlane(t);
 }
@@ -175,9 +204,10 @@ struct TileIO {
 template <int D, bool K8V3>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
-  // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids]
+  // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids][context lengths]
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
+  int* lens_lds = bt_lds + kMaxSubBlocks;
 
   const int Hkv = a.num_kv_heads;
   const int h = blockIdx.x % Hkv;
@@ -187,18 +217,24 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
+  // ---- context lengths -> LDS (one global round trip for the whole prologue) ----
+  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = row_len(a, i);
+  __syncthreads();
+
   // ---- this workgroup's slice [lo, hi) of the token stream ----
-  const int total = stream_total(a, lane);
+  const int total = stream_total(a, lens_lds, lane);
   if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
     for (int b = 0; b < a.batch; ++b)
-      if (row_len(a, b) == 0)
+      if (lens_at(a, lens_lds, b) == 0) {
         for (int i = tid; i < G * D; i += 64 * kDecWaves)
           a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
+        if (h == 0 && tid == 0) a.ws_desc[2 * b] = -1;
+      }
   }
-  const int S = slice_len(total, a.wg_per_head);
-  const int lo = j * S;
+  const int lo = slice_start(j, total, a.wg_per_head, a.slot_classes, a.slot_skew);
   if (lo >= total) return;
-  const int hi = min(total, lo + S);
+  const int hi =
+      j + 1 >= a.wg_per_head ? total : min(total, slice_start(j + 1, total, a.wg_per_head, a.slot_classes, a.slot_skew));
 
   // ---- first row whose stream range holds lo: wave-level prefix scan ----
   int b = 0, pb = 0;  // row, and the start of its stream range
@@ -206,7 +242,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     int carry = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
       const int r = c0 + lane;
-      const int v = r < a.batch ? stream_len(a, row_len(a, r)) : 0;
+      const int v = r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0;
       int incl = v;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -263,7 +299,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // length, or 0 when the slice holds no further segment.
   auto find_segment = [&](int& rb, int& rpb) -> int {
     for (; rb < a.batch && rpb + a.ghost < hi; ++rb) {
-      const int L = __builtin_amdgcn_readfirstlane(row_len(a, rb));
+      const int L = __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, rb));
       if (L == 0) continue;
       if (rpb + a.ghost + padded32(L) > lo) return L;
       rpb += stream_len(a, L);
@@ -672,6 +708,17 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     __syncthreads();
     store_prefetched_bt();  // bt_lds is free: every wave left its tile loop
     const int64_t slot = ((int64_t)h * a.slots + (j + b)) * G;  // (row, slice) -> unique slot j + b
+    // the merge kernel learns the slices of a split row from these: first and
+    // last slice, or -1 for a row finished here (stream positions are the same
+    // for every head, so head 0 writes them)
+    if (h == 0 && tid == 0) {
+      if (whole_row) {
+        a.ws_desc[2 * b] = -1;
+      } else {
+        if (s0 == 0) a.ws_desc[2 * b] = j;
+        if (s1 == padL) a.ws_desc[2 * b + 1] = j;
+      }
+    }
     for (int i = tid; i < G * D; i += 64 * kDecWaves) {
       const int cc = i / D, d = i - cc * D;
       float M = kNegInf;
@@ -704,39 +751,19 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   }
 }
 
-// Combine the segments of (row b, KV head h): recompute the row's position in
-// the token stream (as decode_kernel does) and merge the partials of slices
-// j_first..j_last, stored at slots j + b.  One pass over the context lengths;
-// the partials are read four slices at a time.
+// Combine the segments of (row b, KV head h): decode_kernel recorded the
+// first and last slice of every split row (-1 for rows it finished); the
+// partials of slices j_first..j_last are at slots j + b and are read four at a
+// time.
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-  __shared__ int red[2][4];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int L = row_len(a, b);
-  int tot = 0, before = 0;
-  for (int r = tid; r < a.batch; r += 256) {
-    const int v = stream_len(a, row_len(a, r));
-    tot += v;
-    before += r < b ? v : 0;
-  }
-  tot = wave_sum_i(tot);
-  before = wave_sum_i(before);
-  if ((tid & 63) == 0) {
-    red[0][tid >> 6] = tot;
-    red[1][tid >> 6] = before;
-  }
-  __syncthreads();
-  if (L == 0) return;
-  const int total = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-  const int pb = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-  const int S = slice_len(total, a.wg_per_head);
-  const int rs = pb + a.ghost;
-  const int jf = rs / S, jl = (rs + padded32(L) - 1) / S;
-  if (jf == jl) return;  // one segment: decode_kernel wrote the row
+  const int jf = a.ws_desc[2 * b];
+  if (jf < 0) return;
+  const int jl = a.ws_desc[2 * b + 1];
   const int G = a.group;
-  for (int i = tid; i < G * D; i += 256) {
+  for (int i = threadIdx.x; i < G * D; i += 256) {
     const int cc = i / D, d = i - cc * D;
     float M = kNegInf, num = 0.0f, den = 0.0f;
     for (int j0 = jf; j0 <= jl; j0 += 4) {
@@ -833,7 +860,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
     return ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
   };
   a.smem_main = smem_main_for(a.group);
-  const int smem = a.smem_main + kMaxSubBlocks * 4;
+  const int smem = a.smem_main + (kMaxSubBlocks + kLensLds) * 4;
   // Resident workgroups per CU at this LDS size (depends on the GQA group),
   // queried once per group size.
   static int resident_by_group[17] = {};
@@ -841,7 +868,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   if (!lds_raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            smem_main_for(16) + kMaxSubBlocks * 4) != hipSuccess) {
+                            smem_main_for(16) + (kMaxSubBlocks + kLensLds) * 4) != hipSuccess) {
       set_error("s8kv_decode: cannot raise the dynamic LDS limit");
       return S8KV_ERR_LAUNCH;
     }
@@ -857,6 +884,9 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   }
   a.wg_per_head = plan_wg_per_head(a.num_kv_heads, resident);
   a.ghost = kGhostTokens;
+  a.slot_classes = resident;
+  a.slot_skew = kSlotSkewPermille;
+  if (const char* env = getenv("S8KV_DECODE_SLOT_SKEW")) a.slot_skew = atoi(env);
   if (const char* env = getenv("S8KV_DECODE_GHOST")) a.ghost = (atoi(env) < 0 ? 0 : atoi(env) + 31) / 32 * 32;
   a.slots = a.batch + a.wg_per_head;
   const dim3 grid(a.wg_per_head * a.num_kv_heads), mgrid(a.num_kv_heads, a.batch);
@@ -880,7 +910,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
 
 static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim) {
   const int64_t wph = max_wg_per_head(num_kv_heads);
-  return (int64_t)num_q_heads * (batch + wph) * (head_dim + 2) * 4;
+  return (int64_t)num_q_heads * (batch + wph) * (head_dim + 2) * 4 + (int64_t)batch * 8;
 }
 
 static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -925,8 +955,10 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
   const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
   S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
                "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes_given);
+  const int64_t partials = (int64_t)num_q_heads * (batch + max_wg_per_head(num_kv_heads));  // (head, slot) pairs
   a.ws_ml = reinterpret_cast<float*>(workspace);
-  a.ws_acc = a.ws_ml + (need / ((int64_t)(head_dim + 2) * 4)) * 2;
+  a.ws_acc = a.ws_ml + partials * 2;
+  a.ws_desc = reinterpret_cast<int*>(a.ws_acc + partials * head_dim);
   hipStream_t s = (hipStream_t)stream;
   switch (head_dim) {
     case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false>(a, s);

@@ -198,28 +198,32 @@ def test_decode_int8_outlier_channels():
 
 
 @pytest.mark.parametrize(
-    "wg_per_head,ghost,batch,hq,hkv,bs,lens",
+    "wg_per_head,ghost,batch,hq,hkv,bs,lens,skew",
     [
         # one workgroup per head: every row in one slice, rows past 2048 tokens
         # streamed in several block-id stages
-        (1, 128, 4, 16, 4, 16, [1000, 129, 5000, 0]),
+        (1, 128, 4, 16, 4, 16, [1000, 129, 5000, 0], 0),
         # slices longer than 2048 tokens that end inside a row
-        (2, 0, 4, 8, 2, 256, [5000, 100, 0, 37]),
+        (2, 0, 4, 8, 2, 256, [5000, 100, 0, 37], 0),
         # many short rows: slices span several rows, rows span slices
-        (7, 0, 64, 32, 8, 32, "short"),
-        (7, 128, 64, 32, 8, 32, "short"),
+        (7, 0, 64, 32, 8, 32, "short", 0),
+        (7, 128, 64, 32, 8, 32, "short", 0),
         # per-row charge larger than the slices: some slices hold no tokens
-        (40, 512, 64, 32, 8, 16, "short"),
+        (40, 512, 64, 32, 8, 16, "short", 0),
         # block_size < 32: tiles cross blocks
-        (3, 64, 5, 16, 4, 8, [300, 1, 64, 2500, 31]),
+        (3, 64, 5, 16, 4, 8, [300, 1, 64, 2500, 31], 0),
+        # slices weighted by residency slot (unequal slice lengths)
+        (7, 256, 64, 32, 8, 32, "short", 300),
+        (5, 0, 4, 8, 2, 256, [5000, 100, 0, 3000], 150),
     ],
 )
-def test_decode_int8_slicings(wg_per_head, ghost, batch, hq, hkv, bs, lens, monkeypatch):
+def test_decode_int8_slicings(wg_per_head, ghost, batch, hq, hkv, bs, lens, skew, monkeypatch):
     """Other slicings of the token stream across workgroups: whole rows, rows
     split across slices (partials + merge), slices spanning several rows, and
     slices that fall between rows' tokens."""
     monkeypatch.setenv("S8KV_DECODE_WG_PER_HEAD", str(wg_per_head))
     monkeypatch.setenv("S8KV_DECODE_GHOST", str(ghost))
+    monkeypatch.setenv("S8KV_DECODE_SLOT_SKEW", str(skew))
     if lens == "short":
         lens = np.random.default_rng(5).integers(0, 120, size=batch).tolist()
     case = make_case(55 + wg_per_head, batch, hq, hkv, 128, bs, lens)
