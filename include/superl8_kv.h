@@ -122,6 +122,33 @@ int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
                      void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Multi-query verify attention over the int8 paged cache: tree verify and
+ * chunked prefill.  No single reference op: it computes what the reference
+ * gets from S sequential paged decodes in chain verify
+ * (gqa_attention.py:217-292, one decode per draft with context L+t+1) and from
+ * read_dense + attn_int8_fwd(causal=True) with bottom-right alignment in
+ * chunked prefill (gqa_attention.py:105-129, gated_gqa_attention.py:153-191);
+ * for a tree it generalizes the chain to an ancestor mask.
+ *
+ * q: fp16 [batch, num_q_heads, max_queries, head_dim] with element strides
+ * q_stride_b, q_stride_h, q_stride_s (head_dim contiguous).  Row b has
+ * prefix_lens[b] prefix keys followed by query_lens[b] draft keys (or
+ * max_queries when query_lens is NULL), already appended to the cache at
+ * positions prefix_lens[b] .. prefix_lens[b]+n-1.  Query s of row b attends
+ * every prefix key plus draft key i when i <= s (tree_mask NULL: chain /
+ * causal chunk) or when bit i of tree_mask[b*max_queries + s] is set (tree;
+ * at most 64 drafts).  Keys at positions >= max_context_len are not read.
+ * out: fp16 [batch, num_q_heads, max_queries, head_dim] contiguous; queries
+ * s >= query_lens[b] produce zeros.  head_dim 64, 128 or 256.
+ */
+int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
+                     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s, const int8_t* k_cache,
+                     const float* k_scale, const int8_t* v_cache, const float* v_scale, int64_t num_blocks,
+                     int block_size, const int32_t* block_table, int64_t block_table_stride,
+                     const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
+                     int max_context_len, float scale, void* out, void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its two kernels with HIP events stamped with each

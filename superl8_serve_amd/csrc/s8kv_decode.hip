@@ -404,7 +404,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       for (int m = 0; m < C::NQK; ++m) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float val = x[8 * m + e] * a.qscale;
+          // (materialized: hi and lo must both come from this one fp32 value;
+          // a fused fp16(x*s) for the lo term can differ from fp16(val) by one
+          // ulp, which would leave hi + lo off by 2^-11)
+          const float val = materialize(x[8 * m + e] * a.qscale);
           const _Float16 qh = (_Float16)val;
           qhi[m][e] = qh;
           qlo[m][e] = (_Float16)(val - (float)qh);
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
           for (int s = 0; s < 2; ++s) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              float w = p[s][i] * io.vs[s][nb][i];
+              float w = materialize(p[s][i] * io.vs[s][nb][i]);  // one value for hi and lo
               // masked tokens: p = 0 but the scale past the row end may be any value
               if constexpr (MASKED) w = (tb + 16 * s + 4 * g + i) < t1 ? w : 0.0f;
               const _Float16 wh = (_Float16)w;

@@ -1,0 +1,428 @@
+// Multi-query verify attention over the paged int8 cache: tree verify (each
+// draft query sees the prefix plus its ancestors in the draft tree) and
+// chunked prefill / chain verify (query s sees the prefix plus drafts 0..s).
+//
+// Layout of the work: a workgroup of 4 waves owns 64 query rows of one
+// (sequence, KV head) pair -- row r is query position r / G of q head
+// h*G + r % G -- and streams the pair's keys in 32-key tiles.  Each tile's K
+// and V rows are loaded once per workgroup, converted int8 -> fp16 (exact) on
+// the way into LDS (double-buffered), and shared by the 4 waves; a wave owns 16
+// query rows, the 16 columns of its MFMA tiles:
+//   QK  : S^T[key][row] on MFMA 16x16x32 f16, A = K rows from LDS, B = the
+//         rotated, pre-scaled q split into fp16 hi + lo (two MFMAs).
+//   mask: keys below the prefix are visible to every row; draft key i is
+//         visible to row position s if i <= s (chain) or bit i of the row's
+//         tree mask is set (tree).
+//   softmax: online, log2 domain, lazy max (as the decode kernel).
+//   PV  : O^T[dim][row] on MFMA, A = V^T via ds_read_b64_tr_b16 from LDS,
+//         B = P * v_scale as fp16 hi + lo.
+// Rows past a sequence's query count are written as zeros.
+#include <type_traits>
+
+#include "s8kv_device.h"
+#include "s8kv_host.h"
+
+namespace s8kv {
+namespace verify {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;
+constexpr int kRowsPerWg = 16 * kWaves;
+constexpr int kSubKeys = 2048;                 // block ids staged in LDS per 2048 keys
+constexpr int kMaxSubBlocks = kSubKeys / 4 + 2;  // block_size >= 4
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kMaxSlack = 8.0f;
+
+template <int D>
+struct Cfg {
+  static constexpr int KCH = D / 4;      // dims per lane per key row (MFMA A / B chunk of the lane group)
+  static constexpr int NQK = D / 32;     // QK MFMAs per 16-key subtile
+  static constexpr int NPV = D / 16;     // PV MFMAs per tile
+  static constexpr int KROW = 2 * D + 16;  // LDS pitch of an fp16 K row (bytes)
+  static constexpr int VROW = 2 * D + 32;  // LDS pitch of an fp16 V row (bytes)
+  static constexpr int KBYTES = kTile * KROW;
+  static constexpr int VBYTES = kTile * VROW;
+  static constexpr int BUF = KBYTES + VBYTES + 2 * kTile * 4;  // K, V, k_scale, v_scale
+  static constexpr int CHUNKS = kTile * D / 16;                 // 16-byte int8 chunks per K (or V) tile
+  static constexpr int LOADS = (CHUNKS + kThreads - 1) / kThreads;
+  static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
+};
+
+struct VerifyArgs {
+  const _Float16* q;
+  int64_t q_stride_b, q_stride_h, q_stride_s;
+  int batch, num_q_heads, num_kv_heads, group, max_queries;
+  const void* k_cache;
+  const float* k_scale;
+  const void* v_cache;
+  const float* v_scale;
+  uint32_t kc_bytes, ks_bytes;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* prefix_lens;
+  const int32_t* query_lens;  // nullable: every row has max_queries queries
+  const int64_t* tree_mask;   // nullable: chain; else [batch][max_queries] ancestor bits
+  int bs_log2;
+  int max_context_len;
+  int n_qblocks;              // 64-row query blocks per (sequence, KV head)
+  float qscale;
+  _Float16* out;              // [batch][Hq][max_queries][D]
+};
+
+// Position of tile key tt (0..31) in the LDS V tile: lane group g's eight
+// transpose-read rows (keys 4g..4g+3 and 16+4g..16+4g+3) are rows 8g..8g+7.
+__device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
+  using C = Cfg<D>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
+
+  // workgroups of one (sequence, KV head) pair share an XCD (and its L2)
+  const int P = a.batch * a.num_kv_heads;
+  const int xcd = blockIdx.x & 7;
+  const int rest = blockIdx.x >> 3;
+  const int qb = rest % a.n_qblocks;
+  const int p = (rest / a.n_qblocks) * 8 + xcd;
+  if (p >= P) return;
+  const int b = p / a.num_kv_heads;
+  const int h = p - b * a.num_kv_heads;
+  const int G = a.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
+  const int prefix = max(0, a.prefix_lens[b]);
+  const int row0 = qb * kRowsPerWg;                 // first row of the workgroup
+  const int pos_hi = min(nq, (row0 + kRowsPerWg + G - 1) / G);  // positions of this block that exist
+  const bool tree = a.tree_mask != nullptr;
+  // keys any row of this block can see
+  int kv_end = prefix + (tree ? nq : pos_hi);
+  kv_end = min(kv_end, a.max_context_len);
+  if (row0 / G >= nq) kv_end = 0;  // no query of this block exists
+
+  // this lane's column: query row r -> (position, q head)
+  const int r = row0 + wave * 16 + c;
+  const int pos = r / G;
+  const int head = h * G + (r - pos * G);
+  const bool row_live = pos < nq;
+  const uint64_t tmask = (tree && row_live) ? (uint64_t)a.tree_mask[(int64_t)b * a.max_queries + pos] : 0ull;
+
+  // ---- q: rotate (FWHT), pre-scale, split into fp16 hi + lo ----
+  half8_t qhi[C::NQK], qlo[C::NQK];
+  {
+    float x[C::KCH];
+    const _Float16* qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)head * a.q_stride_h +
+                         (int64_t)(row_live ? pos : 0) * a.q_stride_s + g * C::KCH;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) x[i] = row_live ? (float)qp[i] : 0.0f;
+#pragma unroll
+    for (int hs = 1; hs < C::KCH; hs <<= 1) {
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        if ((i & hs) == 0) {
+          const float x0 = x[i], x1 = x[i + hs];
+          x[i] = x0 + x1;
+          x[i + hs] = x0 - x1;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) {
+      const bool upper = (lane & m) != 0;
+#pragma unroll
+      for (int i = 0; i < C::KCH; ++i) {
+        const float pv = shfl_xor_f(x[i], m);
+        x[i] = upper ? (pv - x[i]) : (x[i] + pv);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < C::NQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // (materialized: hi and lo must both come from this one fp32 value; a
+        // fused fp16(x*s) for the lo term can differ from fp16(val) by one ulp)
+        const float val = materialize(x[8 * m + e] * a.qscale);
+        const _Float16 qh = (_Float16)val;
+        qhi[m][e] = qh;
+        qlo[m][e] = (_Float16)(val - (float)qh);
+      }
+    }
+  }
+
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+  float4_t acc[C::NPV];
+#pragma unroll
+  for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.kc_bytes);
+  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.ks_bytes);
+  const int bs_log2 = a.bs_log2;
+  const uint32_t bsm = (1u << bs_log2) - 1u;
+  const uint32_t hkv = (uint32_t)a.num_kv_heads;
+  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+
+  for (int u0 = 0; u0 < kv_end; u0 += kSubKeys) {
+    const int u1 = min(kv_end, u0 + kSubKeys);
+    const int fb = u0 >> bs_log2;
+    const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
+    __syncthreads();  // previous users of bt_lds and the tile buffers are done
+    for (int i = tid; i < nblk; i += kThreads) bt_lds[i] = bt_row[fb + i];
+    __syncthreads();
+
+    // storage row of key kk (clamped to the last key, so every address is a real row)
+    auto row_of = [&](int kk) -> uint32_t {
+      kk = min(kk, u1 - 1);
+      const uint32_t blk = (uint32_t)bt_lds[(kk >> bs_log2) - fb];
+      return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)kk & bsm);
+    };
+
+    // ---- cooperative tile load: int8 K/V chunks and scales -> registers ----
+    u32x4_t kreg[C::LOADS], vreg[C::LOADS];
+    float sreg = 0.0f;
+    auto load_tile = [&](int base) {
+#pragma unroll
+      for (int i = 0; i < C::LOADS; ++i) {
+        const int ch = tid + i * kThreads;
+        if (ch < C::CHUNKS) {
+          const int tt = ch / (D / 16), part = ch % (D / 16);
+          const uint32_t row = row_of(base + tt);
+          kreg[i] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
+          vreg[i] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
+        }
+      }
+      if (tid < 2 * kTile) {
+        const uint32_t row = row_of(base + (tid & (kTile - 1)));
+        sreg = __builtin_bit_cast(float, bload32(tid < kTile ? ks : vs, row * 4u));
+      }
+    };
+    // registers -> LDS buffer, converting int8 to fp16
+    auto store_tile = [&](int buf) {
+      char* kb = smem + buf * C::BUF;
+      char* vb = kb + C::KBYTES;
+      float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
+#pragma unroll
+      for (int i = 0; i < C::LOADS; ++i) {
+        const int ch = tid + i * kThreads;
+        if (ch < C::CHUNKS) {
+          const int tt = ch / (D / 16), part = ch % (D / 16);
+          const half8_t k0 = i8x8_to_f16(u32x2_t{kreg[i].x, kreg[i].y});
+          const half8_t k1 = i8x8_to_f16(u32x2_t{kreg[i].z, kreg[i].w});
+          *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = k0;
+          *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = k1;
+          const half8_t v0 = i8x8_to_f16(u32x2_t{vreg[i].x, vreg[i].y});
+          const half8_t v1 = i8x8_to_f16(u32x2_t{vreg[i].z, vreg[i].w});
+          *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32) = v0;
+          *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32 + 16) = v1;
+        }
+      }
+      if (tid < 2 * kTile) sb[tid] = sreg;
+    };
+
+    // ---- one 32-key tile from LDS buffer `buf` ----
+    auto process = [&](int buf, int base, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const char* kb = smem + buf * C::BUF;
+      const char* vb = kb + C::KBYTES;
+      const float* sb = reinterpret_cast<const float*>(vb + C::VBYTES);
+      float4_t sc[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
+        const char* krow = kb + (16 * s + c) * C::KROW + g * C::KCH * 2;
+#pragma unroll
+        for (int m = 0; m < C::NQK; ++m) {
+          const half8_t ka = *reinterpret_cast<const half8_t*>(krow + 16 * m);
+          cacc = mfma16x16x32(ka, qhi[m], cacc);
+          cacc = mfma16x16x32(ka, qlo[m], cacc);
+        }
+        sc[s] = cacc;
+      }
+      float4_t ksc[2], vsc[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        ksc[s] = *reinterpret_cast<const float4_t*>(sb + 16 * s + 4 * g);
+        vsc[s] = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * s + 4 * g);
+      }
+      float pr[2][4];
+      float mt = kNegInf;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = sc[s][i] * ksc[s][i];
+          if constexpr (MASKED) {
+            const int kk = base + 16 * s + 4 * g + i;
+            const int di = kk - prefix;  // draft index when >= 0
+            bool vis = kk < kv_end && row_live;
+            if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask >> di) & 1ull)) : di <= pos);
+            x = vis ? x : kNegInf;
+          }
+          pr[s][i] = x;
+          mt = fmaxf(mt, x);
+        }
+      }
+      mt = fmaxf(mt, shfl_xor_f(mt, 16));
+      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
+        m_run = m_new;
+      }
+      half8_t pbh, pbl;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = pr[s][i];
+          const float e = x == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(x - m_run);
+          l_run += e;
+          const float w = materialize(e * vsc[s][i]);  // one value for hi and lo
+          const _Float16 wh = (_Float16)w;
+          pbh[4 * s + i] = wh;
+          pbl[4 * s + i] = (_Float16)(w - (float)wh);
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < C::NPV; ++n) {
+        const int r0 = 8 * g + ((lane >> 2) & 3);
+        const int colb = (16 * n + 4 * (lane & 3)) * 2;
+        const i16x4_t lw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + r0 * C::VROW + colb));
+        const i16x4_t hw =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + (r0 + 4) * C::VROW + colb));
+        const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
+        const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        acc[n] = mfma16x16x32(va, pbh, acc[n]);
+        acc[n] = mfma16x16x32(va, pbl, acc[n]);
+      }
+    };
+
+    const int ntiles = (u1 - u0 + kTile - 1) / kTile;
+    load_tile(u0);
+    store_tile(0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+      const int base = u0 + t * kTile;
+      const bool more = t + 1 < ntiles;
+      if (more) load_tile(base + kTile);
+      // a tile needs masking when it reaches the drafts or the end of the visible
+      // keys (wave-uniform: MFMAs must run with every lane active; rows past the
+      // query count are zeroed at the end instead)
+      if (base + kTile <= prefix && base + kTile <= kv_end)
+        process(t & 1, base, std::false_type{});
+      else
+        process(t & 1, base, std::true_type{});
+      if (more) store_tile((t + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- normalize and write this wave's 16 rows ----
+  float l_tot = l_run;
+  l_tot += shfl_xor_f(l_tot, 16);
+  l_tot += shfl_xor_f(l_tot, 32);
+  if (pos < a.max_queries && (r - pos * G) < G) {
+    const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    _Float16* op = a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) {
+      half4_t o;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(acc[n][rr] * inv);
+      *reinterpret_cast<half4_t*>(op + 16 * n + 4 * g) = o;
+    }
+  }
+}
+
+template <int D>
+static int launch(VerifyArgs& a, hipStream_t stream) {
+  using C = Cfg<D>;
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
+      set_error("s8kv_verify: cannot set the dynamic LDS size");
+      return S8KV_ERR_LAUNCH;
+    }
+    attr = true;
+  }
+  const int P = a.batch * a.num_kv_heads;
+  const int64_t grid = (int64_t)8 * a.n_qblocks * ((P + 7) / 8);
+  if (grid > INT32_MAX) {
+    set_error("s8kv_verify: grid too large");
+    return S8KV_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((verify_kernel<D>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
+  return check_launch("s8kv_verify");
+}
+
+}  // namespace verify
+}  // namespace s8kv
+
+using namespace s8kv;
+
+extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                                const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
+  S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
+  if (batch == 0 || max_queries == 0) return S8KV_OK;
+  S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
+               "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
+  S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
+  S8KV_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
+               "verify: head_dim %d not in {64, 128, 256}", head_dim);
+  S8KV_REQUIRE(is_pow2(block_size) && block_size >= 4, S8KV_ERR_UNSUPPORTED,
+               "verify: block_size %d must be a power of two >= 4", block_size);
+  S8KV_REQUIRE(num_blocks > 0 && max_context_len >= 0, S8KV_ERR_INVALID, "verify: bad num_blocks/max_context_len");
+  S8KV_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && block_table && prefix_lens && out, S8KV_ERR_INVALID,
+               "verify: null pointer argument");
+  const int64_t rows = num_blocks * num_kv_heads * block_size;
+  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "verify: per-layer cache exceeds 4 GiB");
+  verify::VerifyArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.q_stride_s = q_stride_s;
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.max_queries = max_queries;
+  a.k_cache = k_cache;
+  a.k_scale = k_scale;
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.kc_bytes = (uint32_t)(rows * head_dim);
+  a.ks_bytes = (uint32_t)(rows * 4);
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.prefix_lens = prefix_lens;
+  a.query_lens = query_lens;
+  a.tree_mask = tree_mask;
+  a.bs_log2 = log2i(block_size);
+  a.max_context_len = max_context_len;
+  a.n_qblocks = (a.group * max_queries + verify::kRowsPerWg - 1) / verify::kRowsPerWg;
+  a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
+  a.out = (_Float16*)out;
+  hipStream_t s = (hipStream_t)stream;
+  switch (head_dim) {
+    case 64: return verify::launch<64>(a, s);
+    case 128: return verify::launch<128>(a, s);
+    case 256: return verify::launch<256>(a, s);
+  }
+  return S8KV_ERR_UNSUPPORTED;
+}

@@ -24,6 +24,7 @@ __all__ = [
     "attn_paged_decode_cached",
     "attn_paged_decode_k8v3",
     "decode_workspace_bytes",
+    "attn_paged_verify",
     "copy_blocks",
 ]
 
@@ -237,6 +238,70 @@ def attn_paged_decode_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
     _lib.check(rc, "attn_paged_decode_k8v3")
+    return out
+
+
+def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix_lens, block_size, *,
+                      query_lens=None, tree_mask=None, max_context_len, scale):
+    """Multi-query attention of draft / chunk queries over the int8 paged cache.
+
+    ``q``: fp16 ``[B, Hq, S, D]`` (any strides with D contiguous, e.g. the
+    ``[B, S, Hq, D] -> [B, Hq, S, D]`` transpose view).  Row b's S drafts sit
+    at cache positions ``prefix_lens[b] ..`` (appended beforehand).  Query s
+    sees the prefix plus draft i when ``i <= s`` (``tree_mask`` None: chain
+    verify, gqa_attention.py:217-292, and bottom-right causal chunked prefill,
+    gqa_attention.py:105-129) or when bit i of ``tree_mask[b, s]`` (int64
+    ``[B, S]``) is set (tree verify).  Queries ``s >= query_lens[b]`` give
+    zeros.  Returns fp16 ``[B, Hq, S, D]``."""
+    _on_gpu("q", q, torch.float16)
+    dev = q.device
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _on_gpu("block_table", block_table, torch.int32, dev)
+    _on_gpu("prefix_lens", prefix_lens, torch.int32, dev)
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(int(block_size) == bs, f"block_size {block_size} does not match the cache ({bs})")
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
+    _require(q.dim() == 4 and q.shape[3] == d, f"verify q must be [B, Hq, S, {d}], got {tuple(q.shape)}")
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    b, hq, s_, _ = q.shape
+    _require(block_table.dim() == 2 and block_table.shape[0] == b, f"block_table must be [{b}, max_blocks]")
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    _require(prefix_lens.dim() == 1 and prefix_lens.shape[0] == b, f"prefix_lens must be [{b}]")
+    prefix_lens = prefix_lens.contiguous()
+    ql_ptr = None
+    if query_lens is not None:
+        _on_gpu("query_lens", query_lens, torch.int32, dev)
+        _require(query_lens.dim() == 1 and query_lens.shape[0] == b, f"query_lens must be [{b}]")
+        query_lens = query_lens.contiguous()
+        ql_ptr = query_lens.data_ptr()
+    tm_ptr = None
+    if tree_mask is not None:
+        _on_gpu("tree_mask", tree_mask, torch.int64, dev)
+        _require(tuple(tree_mask.shape) == (b, s_), f"tree_mask must be int64 [{b}, {s_}]")
+        _require(s_ <= 64, "tree verify supports at most 64 drafts per row")
+        tree_mask = tree_mask.contiguous()
+        tm_ptr = tree_mask.data_ptr()
+    max_context_len = int(max_context_len)
+    _require(0 <= max_context_len <= block_table.shape[1] * bs,
+             f"max_context_len {max_context_len} exceeds the block table capacity {block_table.shape[1] * bs}")
+    out = torch.empty((b, hq, s_, d), dtype=torch.float16, device=dev)
+    if b == 0 or s_ == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_verify_int8(
+        q.data_ptr(), b, hq, hkv, d, s_, q.stride(0), q.stride(1), q.stride(2),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+        block_table.data_ptr(), block_table.stride(0), prefix_lens.data_ptr(), ql_ptr, tm_ptr,
+        max_context_len, float(scale), out.data_ptr(), _stream(q),
+    )
+    _lib.check(rc, "attn_paged_verify")
     return out
 
 
