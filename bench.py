@@ -225,6 +225,153 @@ def calibrate_copy(mib: int) -> None:
     print(json.dumps({"calibration_copy_bytes_read": moved, "calibration_copy_bytes_written": moved}))
 
 
+# ---------------------------------------------------------------------------
+# Verify workloads (not the headline metric): chunked prefill and tree verify
+# ---------------------------------------------------------------------------
+
+VERIFY_LAYERS = 4  # distinct per-layer storage, rotated so no layer is served from the Infinity Cache
+
+
+def verify_workload(kind: str, device):
+    """Chunked prefill: 16 sequences sharing a 4096-token prefix (the prefix
+    blocks appear in every block table) each append a 512-token chunk and
+    attend bottom-right causally.  Tree verify: 32 sequences with 8192-token
+    prefixes each append 16..64 draft nodes of a random tree (BFS, 1-4
+    children per expanded node) and attend prefix + ancestors.  Seeds 3 / 4."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    rng = np.random.default_rng(3 if kind == "chunk" else 4)
+    if kind == "chunk":
+        b_, prefix_len, nq_max = 16, 4096, 512
+        nq = np.full(b_, nq_max)
+        shared = prefix_len // BS
+        own = (nq_max + BS - 1) // BS
+        n_blocks = shared + b_ * own + 4
+        perm = rng.permutation(n_blocks)
+        bt = np.zeros((b_, shared + own), np.int32)
+        for i in range(b_):
+            bt[i, :shared] = perm[:shared]
+            bt[i, shared:] = perm[shared + i * own: shared + (i + 1) * own]
+        prefix = np.full(b_, prefix_len)
+        tree = None
+    else:
+        b_, prefix_len = 32, 8192
+        nq = rng.integers(16, 65, size=b_)
+        nq_max = 64
+        per = (prefix_len + 64 + BS - 1) // BS
+        n_blocks = b_ * per + 4
+        perm = rng.permutation(n_blocks)
+        bt = perm[: b_ * per].reshape(b_, per).astype(np.int32)
+        prefix = np.full(b_, prefix_len)
+        tree = np.zeros((b_, nq_max), np.int64)
+        for i in range(b_):
+            masks, frontier, nxt = [1], [0], 1
+            while nxt < nq[i]:
+                parent = frontier.pop(0)
+                for _ in range(int(rng.integers(1, 5))):
+                    if nxt >= nq[i]:
+                        break
+                    masks.append(masks[parent] | (1 << nxt))
+                    frontier.append(nxt)
+                    nxt += 1
+            tree[i, : nq[i]] = [m - (1 << 64) if m >= 1 << 63 else m for m in masks]
+    width = bt.shape[1]
+    shape = (VERIFY_LAYERS, n_blocks, HKV, BS, D)
+    kc = torch.zeros(shape, dtype=torch.int8, device=device)
+    vc = torch.zeros(shape, dtype=torch.int8, device=device)
+    ks = torch.ones(shape[:4], dtype=torch.float32, device=device)
+    vs = torch.ones(shape[:4], dtype=torch.float32, device=device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(3 if kind == "chunk" else 4)
+    # prefix tokens (the shared prefix once for the chunk workload)
+    rows = range(1) if kind == "chunk" else range(b_)
+    pre_slots = np.concatenate([bt[i, np.arange(prefix_len) // BS] * BS + np.arange(prefix_len) % BS for i in rows])
+    new_slots = np.concatenate([bt[i, (prefix_len + np.arange(nq[i])) // BS] * BS + (prefix_len + np.arange(nq[i])) % BS
+                                for i in range(b_)]).astype(np.int32)
+    ch = [torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(device) for _ in range(VERIFY_LAYERS)]
+    sm = torch.from_numpy(pre_slots.astype(np.int32)).to(device)
+    for layer in range(VERIFY_LAYERS):
+        kp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
+        vp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
+        ops.quantize_kv_write_paged(kp, vp, kc[layer], ks[layer], vc[layer], vs[layer], sm)
+    t_new = int(new_slots.size)
+    k_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
+    v_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
+    q = [_fp16_outliers(gen, (b_, nq_max, HQ, D), ch[l], device).transpose(1, 2) for l in range(VERIFY_LAYERS)]
+    w = {"kc": kc, "vc": vc, "ks": ks, "vs": vs, "bt": torch.from_numpy(bt).to(device),
+         "prefix": torch.from_numpy(prefix.astype(np.int32)).to(device),
+         "ql": torch.from_numpy(nq.astype(np.int32)).to(device),
+         "tree": None if tree is None else torch.from_numpy(tree).to(device),
+         "new_sm": torch.from_numpy(new_slots).to(device), "k_new": k_new, "v_new": v_new, "q": q,
+         "max_ctx": width * BS}
+    # useful work: every query attends prefix + its visible drafts
+    if kind == "chunk":
+        ctx = [prefix_len + s + 1 for i in range(b_) for s in range(nq[i])]
+        kv_tokens = prefix_len + int(nq.sum())  # distinct keys read (shared prefix once)
+    else:
+        ctx = [prefix_len + bin(int(m) & ((1 << 64) - 1)).count("1") for i in range(b_) for m in tree[i, : nq[i]]]
+        kv_tokens = int((prefix + nq).sum())
+    flops = 4 * D * HQ * int(np.sum(ctx))
+    hbm = kv_tokens * HKV * BYTES_PER_TOKEN_HEAD + 2 * 2 * b_ * HQ * nq_max * D
+    append_bytes = t_new * HKV * (D * 4 + BYTES_PER_TOKEN_HEAD) + 4 * t_new
+    torch.cuda.synchronize()
+    return w, {"batch": b_, "prefix": prefix_len, "queries": int(nq.sum()), "flops_layer": flops,
+               "kv_bytes_layer": hbm, "append_bytes_layer": append_bytes}
+
+
+def run_verify(kind: str, steps: int, warmup: int) -> None:
+    import torch
+
+    from superl8_serve_amd import ops
+
+    w, info = verify_workload(kind, "cuda")
+    scale = 1.0 / math.sqrt(D)
+
+    def layer_ops(layer, append=True):
+        if append:
+            ops.quantize_kv_write_paged(w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer],
+                                        w["vc"][layer], w["vs"][layer], w["new_sm"])
+        return ops.attn_paged_verify(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer],
+                                     w["bt"], w["prefix"], BS, query_lens=w["ql"], tree_mask=w["tree"],
+                                     max_context_len=w["max_ctx"], scale=scale)
+
+    for i in range(warmup * VERIFY_LAYERS):
+        layer_ops(i % VERIFY_LAYERS)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # attention alone
+    st.record()
+    for i in range(steps * VERIFY_LAYERS):
+        layer_ops(i % VERIFY_LAYERS, append=False)
+    en.record()
+    torch.cuda.synchronize()
+    t_attn = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
+    st.record()
+    for i in range(steps * VERIFY_LAYERS):
+        layer_ops(i % VERIFY_LAYERS)
+    en.record()
+    torch.cuda.synchronize()
+    t_layer = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
+    tflops = info["flops_layer"] / t_attn / 1e12
+    gbps = info["kv_bytes_layer"] / t_attn / 1e9
+    name = "chunked prefill (16 x (4096 shared prefix + 512 chunk))" if kind == "chunk" else \
+        "tree verify (32 x (8192 prefix + 16..64 draft tree))"
+    print(json.dumps({
+        "metric": f"paged int8 verify attention TFLOP/s, {name}, Qwen3-8B heads",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_layer_attention": round(t_attn * 1e3, 4), "ms_per_layer_append_plus_attention": round(t_layer * 1e3, 4),
+        "higher_is_better": True, "dtype": "int8 cache, fp16 MFMA (hi+lo split operands)",
+        "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20)",
+        "config": {"workload": name, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
+                   "layers_rotated": VERIFY_LAYERS, **info},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "kv_gbps": round(gbps, 1),
+                     "note": "useful flops (4*D*Hq per visible key); the kernel issues 2x MFMAs (hi+lo operands)"},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,6 +382,8 @@ def main():
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
     ap.add_argument("--kernel-reps", type=int, default=3, help="event-timed decode passes over the 36 layers")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree"], default="decode",
+                    help="decode: the Qwen3-8B batch-64 decode step (headline); chunk / tree: verify attention")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -252,6 +401,9 @@ def main():
     _lib.load()
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
+        return
+    if args.workload != "decode":
+        run_verify(args.workload, args.steps, args.warmup)
         return
 
     device = "cuda"

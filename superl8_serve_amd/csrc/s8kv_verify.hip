@@ -186,26 +186,28 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     };
 
     // ---- cooperative tile load: int8 K/V chunks and scales -> registers ----
-    u32x4_t kreg[C::LOADS], vreg[C::LOADS];
-    float sreg = 0.0f;
-    auto load_tile = [&](int base) {
+    struct TileRegs {
+      u32x4_t k[C::LOADS], v[C::LOADS];
+      float s;
+    };
+    auto load_tile = [&](TileRegs& R, int base) {
 #pragma unroll
       for (int i = 0; i < C::LOADS; ++i) {
         const int ch = tid + i * kThreads;
         if (ch < C::CHUNKS) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
           const uint32_t row = row_of(base + tt);
-          kreg[i] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
-          vreg[i] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
+          R.k[i] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
+          R.v[i] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
         }
       }
       if (tid < 2 * kTile) {
         const uint32_t row = row_of(base + (tid & (kTile - 1)));
-        sreg = __builtin_bit_cast(float, bload32(tid < kTile ? ks : vs, row * 4u));
+        R.s = __builtin_bit_cast(float, bload32(tid < kTile ? ks : vs, row * 4u));
       }
     };
     // registers -> LDS buffer, converting int8 to fp16
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](const TileRegs& R, int buf) {
       char* kb = smem + buf * C::BUF;
       char* vb = kb + C::KBYTES;
       float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
@@ -214,17 +216,17 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         const int ch = tid + i * kThreads;
         if (ch < C::CHUNKS) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
-          const half8_t k0 = i8x8_to_f16(u32x2_t{kreg[i].x, kreg[i].y});
-          const half8_t k1 = i8x8_to_f16(u32x2_t{kreg[i].z, kreg[i].w});
+          const half8_t k0 = i8x8_to_f16(u32x2_t{R.k[i].x, R.k[i].y});
+          const half8_t k1 = i8x8_to_f16(u32x2_t{R.k[i].z, R.k[i].w});
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = k0;
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = k1;
-          const half8_t v0 = i8x8_to_f16(u32x2_t{vreg[i].x, vreg[i].y});
-          const half8_t v1 = i8x8_to_f16(u32x2_t{vreg[i].z, vreg[i].w});
+          const half8_t v0 = i8x8_to_f16(u32x2_t{R.v[i].x, R.v[i].y});
+          const half8_t v1 = i8x8_to_f16(u32x2_t{R.v[i].z, R.v[i].w});
           *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32) = v0;
           *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32 + 16) = v1;
         }
       }
-      if (tid < 2 * kTile) sb[tid] = sreg;
+      if (tid < 2 * kTile) sb[tid] = R.s;
     };
 
     // ---- one 32-key tile from LDS buffer `buf` ----
@@ -308,22 +310,34 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       }
     };
 
-    const int ntiles = (u1 - u0 + kTile - 1) / kTile;
-    load_tile(u0);
-    store_tile(0);
-    __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
-      const int base = u0 + t * kTile;
-      const bool more = t + 1 < ntiles;
-      if (more) load_tile(base + kTile);
-      // a tile needs masking when it reaches the drafts or the end of the visible
-      // keys (wave-uniform: MFMAs must run with every lane active; rows past the
-      // query count are zeroed at the end instead)
+    // Tiles alternate between two LDS buffers; their global loads are issued
+    // two tiles ahead into two register sets (A for even tiles, B for odd),
+    // so a load has two tiles of compute to arrive.
+    auto compute = [&](int buf, int base) {
+      // a tile needs masking when it reaches the drafts or the end of the
+      // visible keys (wave-uniform: MFMAs must run with every lane active;
+      // rows past the query count are zeroed at the end instead)
       if (base + kTile <= prefix && base + kTile <= kv_end)
-        process(t & 1, base, std::false_type{});
+        process(buf, base, std::false_type{});
       else
-        process(t & 1, base, std::true_type{});
-      if (more) store_tile((t + 1) & 1);
+        process(buf, base, std::true_type{});
+    };
+    const int ntiles = (u1 - u0 + kTile - 1) / kTile;
+    TileRegs ra, rb;
+    load_tile(ra, u0);
+    if (ntiles > 1) load_tile(rb, u0 + kTile);
+    store_tile(ra, 0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {
+      const int base = u0 + t * kTile;
+      if (t + 2 < ntiles) load_tile(ra, base + 2 * kTile);
+      compute(0, base);
+      if (t + 1 < ntiles) store_tile(rb, 1);
+      __syncthreads();
+      if (t + 1 >= ntiles) break;
+      if (t + 3 < ntiles) load_tile(rb, base + 3 * kTile);
+      compute(1, base + kTile);
+      if (t + 2 < ntiles) store_tile(ra, 0);
       __syncthreads();
     }
   }
