@@ -372,6 +372,131 @@ def run_verify(kind: str, steps: int, warmup: int) -> None:
     }))
 
 
+# ---------------------------------------------------------------------------
+# K8V3 decode step (int8 K, 3-bit Lloyd-Max V) and block copy
+# ---------------------------------------------------------------------------
+
+K8V3_BATCH = 32
+K8V3_BYTES_PER_TOKEN_HEAD = D + 4 + D * 3 // 8 + 4 * (D // 128)  # 184 B
+
+
+def run_k8v3(steps: int, warmup: int) -> None:
+    """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
+    36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
+    needed, distinct storage per layer."""
+    import torch
+
+    from oracle import kv_oracle as O
+    from superl8_serve_amd import ops
+
+    dev = "cuda"
+    rng = np.random.default_rng(2)
+    lens = rng.integers(8192, 32769, size=K8V3_BATCH)
+    need = (lens + BS - 1) // BS
+    n_blocks = int(math.ceil(1.2 * need.sum()))
+    perm = rng.permutation(n_blocks)
+    width = int(need.max())
+    bt = np.zeros((K8V3_BATCH, width), np.int32)
+    pos = 0
+    for b in range(K8V3_BATCH):
+        bt[b, : need[b]] = perm[pos: pos + need[b]]
+        pos += need[b]
+    prefix = lens - 1
+    shape = (NUM_LAYERS, n_blocks, HKV, BS, D)
+    kc = torch.zeros(shape, dtype=torch.int8, device=dev)
+    ks = torch.ones(shape[:4], dtype=torch.float32, device=dev)
+    vp = torch.zeros(shape[:4] + (D * 3 // 32,), dtype=torch.int32, device=dev)
+    vn = torch.zeros(shape[:4] + (D // 128,), dtype=torch.float32, device=dev)
+    cb = torch.from_numpy(O.gaussian_codebook(3, 128)).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    chunk = 65536
+    for layer in range(NUM_LAYERS):
+        ch = torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(dev)
+        for b in range(K8V3_BATCH):
+            for c0 in range(0, int(prefix[b]), chunk):
+                n = min(chunk, int(prefix[b]) - c0)
+                p_ = np.arange(c0, c0 + n)
+                sm = torch.from_numpy((bt[b, p_ // BS] * BS + p_ % BS).astype(np.int32)).to(dev)
+                kp = _fp16_outliers(gen, (n, HKV, D), ch, dev)
+                vq = _fp16_outliers(gen, (n, HKV, D), ch, dev)
+                ops.quantize_kv_write_paged_k8v3(kp, vq, kc[layer], ks[layer], vp[layer], vn[layer], cb, sm)
+    new_sm = torch.from_numpy(np.array([bt[b, prefix[b] // BS] * BS + prefix[b] % BS for b in range(K8V3_BATCH)],
+                                       np.int32)).to(dev)
+    k_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(NUM_LAYERS)]
+    v_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(NUM_LAYERS)]
+    q = [torch.randn((K8V3_BATCH, 1, HQ, D), generator=gen, device=dev).half().transpose(1, 2) for _ in range(NUM_LAYERS)]
+    btd = torch.from_numpy(bt).to(dev)
+    cl = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    max_ctx = width * BS
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        for layer in range(NUM_LAYERS):
+            ops.quantize_kv_write_paged_k8v3(k_new[layer], v_new[layer], kc[layer], ks[layer], vp[layer], vn[layer],
+                                             cb, new_sm)
+            ops.attn_paged_decode_k8v3(q[layer], kc[layer], ks[layer], vp[layer], vn[layer], cb, btd, cl, BS,
+                                       max_context_len=max_ctx, scale=scale)
+
+    torch.cuda.synchronize()
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+    t = K8V3_BATCH
+    append = t * HKV * D * 4 + 4 * t + t * HKV * K8V3_BYTES_PER_TOKEN_HEAD
+    decode = int(lens.sum()) * HKV * K8V3_BYTES_PER_TOKEN_HEAD + 2 * t * HQ * D * 2 + 4 * int(need.sum()) + 4 * t + 32
+    step_b = NUM_LAYERS * (append + decode)
+    value = step_b / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "paged k8v3 decode-attn+append HBM GB/s (% of peak) at Qwen3-8B shapes, b=32, 8k-32k context",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "int8 K / 3-bit V",
+        "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20, seed 2)",
+        "config": {"workload": "Qwen3-8B K8V3 decode step: 36 layers x (append 1 token/seq + decode)",
+                   "batch": t, "sum_context_tokens": int(lens.sum()), "pool_blocks_per_layer": n_blocks,
+                   "bytes_per_step": step_b},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2)}))
+
+
+def run_copy(steps: int) -> None:
+    """copy_blocks over a 4096-block synthetic pool (Qwen3-8B int8 block: K, V,
+    two scale tensors; 1 layer): 1024 random source blocks moved to 1024 other
+    random blocks, as a compaction pass does."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    rng = np.random.default_rng(5)
+    n = 4096
+    t = [torch.randint(-127, 128, (1, n, HKV, BS, D), dtype=torch.int8, device="cuda") for _ in range(2)]
+    t += [torch.rand((1, n, HKV, BS), device="cuda") for _ in range(2)]
+    perm = rng.permutation(n)
+    src, dst = perm[:1024].tolist(), perm[1024:2048].tolist()
+    ops.copy_blocks(t, src, dst)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(steps):
+        ops.copy_blocks(t, src, dst)
+    en.record()
+    torch.cuda.synchronize()
+    sec = st.elapsed_time(en) * 1e-3 / steps
+    moved = 1024 * (2 * HKV * BS * D + 2 * HKV * BS * 4)
+    print(json.dumps({"metric": "copy_blocks GB/s (read + write), 1024 random blocks of a 4096-block pool",
+                      "value": round(2 * moved / sec / 1e9, 1), "unit": "GB/s", "us_per_call": round(sec * 1e6, 1),
+                      "bytes_moved": moved, "pct_of_hbm_peak": round(100 * 2 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -382,8 +507,9 @@ def main():
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
     ap.add_argument("--kernel-reps", type=int, default=3, help="event-timed decode passes over the 36 layers")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree"], default="decode",
-                    help="decode: the Qwen3-8B batch-64 decode step (headline); chunk / tree: verify attention")
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy"], default="decode",
+                    help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
+                         "attention; k8v3: the K8V3 decode step (batch 32, 8k-32k); copy: copy_blocks")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -402,8 +528,14 @@ def main():
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
         return
-    if args.workload != "decode":
+    if args.workload in ("chunk", "tree"):
         run_verify(args.workload, args.steps, args.warmup)
+        return
+    if args.workload == "k8v3":
+        run_k8v3(args.steps, args.warmup)
+        return
+    if args.workload == "copy":
+        run_copy(args.steps)
         return
 
     device = "cuda"
