@@ -1,0 +1,497 @@
+"""Host-side paged KV cache for the MI355X kernels.
+
+Same public interface, layout and bookkeeping as the reference's
+``PagedKVCache`` (superl8serve/engine/kv_cache.py:432-1299) so a caller can
+switch to it unchanged:
+
+* storage (kv_cache.py:484-512): int8 ``k_cache`` / ``v_cache``
+  ``[L, N, Hkv, bs, D]``, fp32 ``k_scale`` / ``v_scale`` ``[L, N, Hkv, bs]``; or, for
+  ``v_quant="lloydmax3"``, ``v_packed`` int32 ``[L, N, Hkv, bs, 3D/32]``,
+  ``v_norm`` fp32 ``[L, N, Hkv, bs, D/128]`` and a per-layer ``v_codebook``;
+* slots and blocks (kv_cache.py:703-755): LIFO free lists of slots and physical
+  blocks, blocks pulled one at a time as a slot grows, reference counts so that
+  blocks shared through the prefix cache are freed by their last holder;
+* prefix cache (kv_cache.py:757-898): a token trie with entries at every
+  block-aligned boundary, a global access counter for LRU, eviction of the
+  least recently used entry on an entry-count cap, and a budget on the number of
+  distinct blocks the cache pins (default half the pool);
+* slot mappings, block tables and pinned staging for graph replays
+  (kv_cache.py:900-995, 1118-1127);
+* writes and attention through the gfx950 kernels (``ops``): append (int8 and
+  fused K8V3), batched paged decode, and multi-query verify.
+
+Beyond the reference: copy-on-write of a shared last block and compaction of
+the pool (moving live blocks into free holes) through the block-copy kernel.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+from .codebook import gaussian_codebook
+
+
+def _unpack3(words: torch.Tensor, d: int) -> torch.Tensor:
+    """Bit-plane words ``[..., 3d/32]`` -> 3-bit codes ``[..., d]`` (word 3g+b
+    holds bit b of codes 32g..32g+31, element 32g+i at bit i)."""
+    w = words.reshape(*words.shape[:-1], d // 32, 3).to(torch.int64) & 0xFFFFFFFF
+    bit = torch.arange(32, device=words.device)
+    planes = (w.unsqueeze(-1) >> bit) & 1  # [..., g, 3, 32]
+    codes = planes[..., 0, :] | (planes[..., 1, :] << 1) | (planes[..., 2, :] << 2)
+    return codes.reshape(*words.shape[:-1], d)
+
+
+def block_bytes(num_kv_heads: int, block_size: int, head_dim: int, v_quant: str = "int8",
+                lloyd_block: int = 128) -> int:
+    """HBM bytes of one block in one layer (kv_cache.py:98-120)."""
+    tokens = num_kv_heads * block_size
+    k_side = tokens * (head_dim + 4)
+    if v_quant == "lloydmax3":
+        return k_side + tokens * (head_dim * 3 // 32 * 4 + head_dim // lloyd_block * 4)
+    return k_side + tokens * (head_dim + 4)
+
+
+class _Entry:
+    __slots__ = ("blocks", "num_tokens", "lru")
+
+    def __init__(self, blocks: list[int], num_tokens: int, lru: int):
+        self.blocks = blocks
+        self.num_tokens = num_tokens
+        self.lru = lru
+
+
+class _Node:
+    __slots__ = ("children", "entry")
+
+    def __init__(self):
+        self.children: dict[int, _Node] = {}
+        self.entry: _Entry | None = None
+
+
+class PagedKVCache:
+    def __init__(self, num_layers, num_slots, num_kv_heads, max_len, head_dim, *, device, block_size: int = 16,
+                 num_blocks: int | None = None, max_prefix_entries: int | None = None,
+                 max_prefix_blocks: int | None = None, max_prefix_block_fraction: float = 0.5,
+                 kv_layers: list[int] | None = None, v_quant: str = "int8", lloyd_block: int = 128):
+        if v_quant not in ("int8", "lloydmax3"):
+            raise ValueError(f"v_quant must be 'int8' or 'lloydmax3', got {v_quant!r}")
+        self.block_size = block_size
+        self._row_of_layer = None if kv_layers is None else {l: i for i, l in enumerate(kv_layers)}
+        self.num_layers = num_layers if kv_layers is None else len(kv_layers)
+        self.v_quant = v_quant
+        self.lloyd_block = lloyd_block
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.max_len = max_len
+        self.max_blocks_per_seq = -(-max_len // block_size)
+        self.num_blocks = num_blocks or num_slots * self.max_blocks_per_seq
+        self.num_slots = num_slots
+        self.device = device
+        geom = (self.num_layers, self.num_blocks, num_kv_heads, block_size)
+        self.k_cache = torch.zeros(geom + (head_dim,), dtype=torch.int8, device=device)
+        self.k_scale = torch.ones(geom, dtype=torch.float32, device=device)
+        if v_quant == "lloydmax3":
+            self.v_packed = torch.zeros(geom + (head_dim * 3 // 32,), dtype=torch.int32, device=device)
+            self.v_norm = torch.zeros(geom + (head_dim // lloyd_block,), dtype=torch.float32, device=device)
+            cb = torch.from_numpy(gaussian_codebook(3, lloyd_block)).to(device)
+            self.v_codebook = cb.unsqueeze(0).repeat(self.num_layers, 1)
+            self.v_cache = None
+            self.v_scale = None
+        else:
+            self.v_cache = torch.zeros(geom + (head_dim,), dtype=torch.int8, device=device)
+            self.v_scale = torch.ones(geom, dtype=torch.float32, device=device)
+            self.v_packed = self.v_norm = self.v_codebook = None
+        # LIFO pools: the next block / slot handed out is the last one returned
+        self._free_blocks: list[int] = list(range(self.num_blocks))
+        self._free_slots: list[int] = list(range(num_slots))
+        self._slot_blocks: list[list[int]] = [[] for _ in range(num_slots)]
+        self._block_refcount: dict[int, int] = {}
+        # prefix cache
+        self._trie = _Node()
+        self._lru_clock = 0
+        self._max_prefix_entries = max_prefix_entries
+        self._prefix_entry_count = 0
+        if max_prefix_blocks is not None:
+            self._max_prefix_blocks: int | None = max_prefix_blocks
+        elif max_prefix_block_fraction is not None:
+            self._max_prefix_blocks = max(1, int(self.num_blocks * max_prefix_block_fraction))
+        else:
+            self._max_prefix_blocks = None
+        self._prefix_block_refs: dict[int, int] = {}
+        # pinned host staging for graph-replayed decode
+        self._pin = device != "cpu" and torch.cuda.is_available()
+        self._slot_map_host: torch.Tensor | None = None
+        self._block_table_host: torch.Tensor | None = None
+
+    # ------------------------------------------------------------------ layout
+
+    def _layer_row(self, layer: int) -> int:
+        if self._row_of_layer is None:
+            return layer
+        if layer not in self._row_of_layer:
+            raise KeyError(f"layer {layer} bears no KV cache")
+        return self._row_of_layer[layer]
+
+    def _tensors(self) -> list[torch.Tensor]:
+        if self.v_quant == "lloydmax3":
+            return [self.k_cache, self.k_scale, self.v_packed, self.v_norm]
+        return [self.k_cache, self.k_scale, self.v_cache, self.v_scale]
+
+    # ------------------------------------------------------- slots and blocks
+
+    def alloc(self) -> int:
+        if not self._free_slots:
+            raise RuntimeError("PagedKVCache: no free slots")
+        return self._free_slots.pop()
+
+    def _release_block(self, blk: int) -> None:
+        left = self._block_refcount.get(blk, 1) - 1
+        if left > 0:
+            self._block_refcount[blk] = left
+        else:
+            self._block_refcount.pop(blk, None)
+            self._free_blocks.append(blk)
+
+    def free(self, slot: int) -> None:
+        for blk in self._slot_blocks[slot]:
+            self._release_block(blk)
+        self._slot_blocks[slot] = []
+        self._free_slots.append(slot)
+
+    def has_free_slot(self) -> bool:
+        return len(self._free_slots) > 0
+
+    def has_free_block(self) -> bool:
+        return len(self._free_blocks) > 0
+
+    @property
+    def used_blocks(self) -> int:
+        return self.num_blocks - len(self._free_blocks)
+
+    def ensure_capacity(self, slots: list[int], lengths: list[int]) -> None:
+        for slot, n in zip(slots, lengths):
+            owned = self._slot_blocks[slot]
+            want = -(-n // self.block_size)
+            while len(owned) < want:
+                if not self._free_blocks:
+                    raise RuntimeError("PagedKVCache: no free blocks")
+                blk = self._free_blocks.pop()
+                owned.append(blk)
+                self._block_refcount[blk] = 1
+
+    def share_blocks(self, slot: int, blocks: list[int]) -> None:
+        self._slot_blocks[slot] = list(blocks)
+        for blk in blocks:
+            self._block_refcount[blk] = self._block_refcount.get(blk, 1) + 1
+
+    # ----------------------------------------------------------- prefix cache
+
+    def _tick_lru(self) -> int:
+        self._lru_clock += 1
+        return self._lru_clock
+
+    def _oldest_entry(self):
+        """(parent, token, node) of the least recently used entry, in trie
+        pre-order (first found wins ties), or None."""
+        best = None
+        stack = [(self._trie, iter(self._trie.children.items()))]
+        while stack:
+            parent, it = stack[-1]
+            nxt = next(it, None)
+            if nxt is None:
+                stack.pop()
+                continue
+            tok, node = nxt
+            if node.entry is not None and (best is None or node.entry.lru < best[2].entry.lru):
+                best = (parent, tok, node)
+            stack.append((node, iter(node.children.items())))
+        return best
+
+    def _evict_one_prefix(self) -> bool:
+        found = self._oldest_entry()
+        if found is None:
+            return False
+        parent, tok, node = found
+        entry, node.entry = node.entry, None
+        for blk in entry.blocks:
+            pins = self._prefix_block_refs.get(blk, 0) - 1
+            if pins > 0:
+                self._prefix_block_refs[blk] = pins
+            else:
+                self._prefix_block_refs.pop(blk, None)
+            self._release_block(blk)
+        self._prefix_entry_count -= 1
+        if not node.children:
+            del parent.children[tok]
+        return True
+
+    def _enforce_prefix_budget(self) -> None:
+        if self._max_prefix_blocks is None:
+            return
+        while len(self._prefix_block_refs) > self._max_prefix_blocks and self._evict_one_prefix():
+            pass
+
+    @property
+    def pinned_prefix_blocks(self) -> int:
+        return len(self._prefix_block_refs)
+
+    def prefix_block_bytes(self) -> int:
+        return (len(self._prefix_block_refs) * self.num_layers
+                * block_bytes(self.num_kv_heads, self.block_size, self.head_dim, self.v_quant, self.lloyd_block))
+
+    def store_prefix(self, token_ids: list[int], slot: int) -> None:
+        bs = self.block_size
+        whole = len(token_ids) // bs
+        if whole == 0:
+            return
+        owned = list(self._slot_blocks[slot])
+        now = self._tick_lru()
+        node = self._trie
+        for i, tok in enumerate(token_ids):
+            node = node.children.setdefault(tok, _Node())
+            n = i + 1
+            if n % bs or n // bs > whole:
+                continue
+            if node.entry is not None:
+                node.entry.lru = now
+                continue
+            if self._max_prefix_entries is not None and self._prefix_entry_count >= self._max_prefix_entries:
+                self._evict_one_prefix()
+            blocks = owned[: n // bs]
+            node.entry = _Entry(blocks, n, now)
+            for blk in blocks:
+                self._block_refcount[blk] = self._block_refcount.get(blk, 1) + 1
+                self._prefix_block_refs[blk] = self._prefix_block_refs.get(blk, 0) + 1
+            self._prefix_entry_count += 1
+        self._enforce_prefix_budget()
+
+    def lookup_prefix(self, token_ids: list[int]) -> tuple[int, list[int]]:
+        now = self._tick_lru()
+        node = self._trie
+        length, blocks = 0, []
+        for i, tok in enumerate(token_ids):
+            node = node.children.get(tok)
+            if node is None:
+                break
+            e = node.entry
+            if e is not None and i + 1 >= e.num_tokens:
+                length, blocks = e.num_tokens, list(e.blocks)
+                e.lru = now
+        return length, blocks
+
+    # --------------------------------------------- mappings and block tables
+
+    def flat_slot_mapping(self, slot: int, length: int) -> list[int]:
+        bs = self.block_size
+        owned = self._slot_blocks[slot]
+        return [owned[p // bs] * bs + p % bs for p in range(length)]
+
+    def slot_mapping_for(self, slots: list[int], positions: list[int]) -> torch.Tensor:
+        bs = self.block_size
+        flat = [self._slot_blocks[s][p // bs] * bs + p % bs for s, p in zip(slots, positions)]
+        return torch.tensor(flat, dtype=torch.int32, device=self.device)
+
+    _slot_mapping = slot_mapping_for
+
+    def block_table(self, slots: list[int]) -> torch.Tensor:
+        table = torch.zeros(len(slots), self.max_blocks_per_seq, dtype=torch.int32)
+        for i, s in enumerate(slots):
+            owned = self._slot_blocks[s]
+            if owned:
+                table[i, : len(owned)] = torch.tensor(owned, dtype=torch.int32)
+        return table.to(self.device)
+
+    def _ensure_decode_staging(self, batch: int) -> None:
+        if self._slot_map_host is None or self._slot_map_host.numel() < batch:
+            self._slot_map_host = torch.empty(batch, dtype=torch.int32, pin_memory=self._pin)
+        if self._block_table_host is None or self._block_table_host.shape[0] < batch:
+            self._block_table_host = torch.zeros(batch, self.max_blocks_per_seq, dtype=torch.int32,
+                                                 pin_memory=self._pin)
+
+    def fill_slot_mapping(self, dst: torch.Tensor, slots: list[int], positions: list[int]) -> None:
+        """Refresh a graph's slot-mapping buffer in place: pinned staging plus one
+        non-blocking copy (kv_cache.py:971-980)."""
+        n = len(slots)
+        self._ensure_decode_staging(n)
+        bs = self.block_size
+        flat = [self._slot_blocks[s][p // bs] * bs + p % bs for s, p in zip(slots, positions)]
+        self._slot_map_host[:n].copy_(torch.tensor(flat, dtype=torch.int32))
+        dst.copy_(self._slot_map_host[:n], non_blocking=self._pin)
+
+    def fill_block_table(self, dst: torch.Tensor, slots: list[int]) -> None:
+        """Refresh a graph's block-table buffer in place; short rows are zero
+        padded (kv_cache.py:982-995)."""
+        n = len(slots)
+        self._ensure_decode_staging(n)
+        host = self._block_table_host[:n]
+        host.zero_()
+        for i, s in enumerate(slots):
+            owned = self._slot_blocks[s]
+            if owned:
+                host[i, : len(owned)] = torch.tensor(owned, dtype=torch.int32)
+        dst.copy_(host, non_blocking=self._pin)
+
+    # ------------------------------------------------------------------ writes
+
+    def write_prefill_varlen(self, layer: int, slot_mapping: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k, v: fp16 ``[T, Hkv, D]``; one append of every token at its flat slot."""
+        row = self._layer_row(layer)
+        if self.v_quant == "lloydmax3":
+            ops.quantize_kv_write_paged_k8v3(k.contiguous(), v.contiguous(), self.k_cache[row], self.k_scale[row],
+                                             self.v_packed[row], self.v_norm[row], self.v_codebook[row],
+                                             slot_mapping, self.lloyd_block)
+        else:
+            ops.quantize_kv_write_paged(k.contiguous(), v.contiguous(), self.k_cache[row], self.k_scale[row],
+                                        self.v_cache[row], self.v_scale[row], slot_mapping)
+
+    def write_prefill(self, layer: int, k: torch.Tensor, v: torch.Tensor, *, slot: int, start: int = 0,
+                      positions: torch.Tensor | None = None) -> None:
+        """k, v: fp16 ``[1, Hkv, S, D]``.  Positions ``[0, S)`` (or `positions`),
+        skipping those below `start` (shared-prefix reuse)."""
+        s = k.shape[2]
+        if s == 0:
+            return
+        kt = k[0].transpose(0, 1)
+        vt = v[0].transpose(0, 1)
+        if positions is None:
+            first = min(max(start, 0), s)
+            if first == s:
+                return
+            mapping = torch.tensor(self.flat_slot_mapping(slot, s)[first:], dtype=torch.int32, device=self.device)
+            kt, vt = kt[first:], vt[first:]
+        else:
+            pos = positions.reshape(-1).to(device=self.device, dtype=torch.int64)
+            if start > 0:
+                keep = pos >= start
+                if not bool(keep.any()):
+                    return
+                pos, kt, vt = pos[keep], kt[keep], vt[keep]
+            owned = torch.tensor(self._slot_blocks[slot], dtype=torch.int64, device=self.device)
+            mapping = (owned[pos // self.block_size] * self.block_size + pos % self.block_size).to(torch.int32)
+        self.write_prefill_varlen(layer, mapping, kt, vt)
+
+    def write_decode_static(self, layer: int, slot_mapping: torch.Tensor, k_new: torch.Tensor,
+                            v_new: torch.Tensor) -> None:
+        """k_new, v_new: fp16 ``[B, Hkv, D]``, one token per sequence."""
+        self.write_prefill_varlen(layer, slot_mapping, k_new, v_new)
+
+    def write_decode(self, layer: int, slots: list[int], positions: list[int], k_new: torch.Tensor,
+                     v_new: torch.Tensor) -> None:
+        self.write_decode_static(layer, self.slot_mapping_for(slots, positions), k_new, v_new)
+
+    # --------------------------------------------------------------- attention
+
+    def decode_attn_static(self, layer: int, q: torch.Tensor, block_table: torch.Tensor, context_lens: torch.Tensor,
+                           max_context_len: int, *, scale: float) -> torch.Tensor:
+        row = self._layer_row(layer)
+        if self.v_quant == "lloydmax3":
+            return ops.attn_paged_decode_k8v3(q, self.k_cache[row], self.k_scale[row], self.v_packed[row],
+                                              self.v_norm[row], self.v_codebook[row], block_table, context_lens,
+                                              self.block_size, max_context_len=max_context_len, scale=scale)
+        return ops.attn_paged_decode_cached(q, self.k_cache[row], self.k_scale[row], self.v_cache[row],
+                                            self.v_scale[row], block_table, context_lens, self.block_size,
+                                            max_context_len=max_context_len, scale=scale)
+
+    def decode_attn(self, layer: int, q: torch.Tensor, slots: list[int], lengths: list[int], *,
+                    scale: float) -> torch.Tensor:
+        """`lengths[i]` is the position of the token just written, so row i
+        attends `lengths[i] + 1` tokens (kv_cache.py:1129-1146)."""
+        ctx = [n + 1 for n in lengths]
+        return self.decode_attn_static(layer, q, self.block_table(slots),
+                                       torch.tensor(ctx, dtype=torch.int32, device=self.device),
+                                       max(ctx) if ctx else 0, scale=scale)
+
+    def verify_attn(self, layer: int, q: torch.Tensor, slots: list[int], prefix_lens: list[int], *, scale: float,
+                    query_lens: list[int] | None = None, tree_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """Multi-query attention of drafts (already written at positions
+        ``prefix_lens[b] ..``): chain / chunk when `tree_mask` is None, else tree.
+        ``q``: fp16 ``[B, Hq, S, D]``."""
+        if self.v_quant != "int8":
+            raise NotImplementedError("verify attention is implemented for the int8 layout")
+        row = self._layer_row(layer)
+        s = q.shape[2]
+        ql = query_lens if query_lens is not None else [s] * len(slots)
+        max_ctx = max((p + n for p, n in zip(prefix_lens, ql)), default=0)
+        return ops.attn_paged_verify(
+            q, self.k_cache[row], self.k_scale[row], self.v_cache[row], self.v_scale[row], self.block_table(slots),
+            torch.tensor(prefix_lens, dtype=torch.int32, device=self.device), self.block_size,
+            query_lens=None if query_lens is None else torch.tensor(query_lens, dtype=torch.int32, device=self.device),
+            tree_mask=tree_mask, max_context_len=min(max_ctx, self.max_blocks_per_seq * self.block_size),
+            scale=scale)
+
+    def read_dense(self, layer: int, slot: int, length: int, *, window: int | None = None,
+                   dtype: torch.dtype = torch.float16) -> tuple[torch.Tensor, torch.Tensor]:
+        """Dequantized fp16 K, V ``[1, Hkv, n, D]`` of one sequence (the
+        reference's dense reader, kv_cache.py:1233-1299): K un-rotated."""
+        row = self._layer_row(layer)
+        first = max(0, length - window) if window is not None else 0
+        pos = torch.arange(first, length, device=self.device)
+        owned = torch.tensor(self._slot_blocks[slot], dtype=torch.int64, device=self.device)
+        blk = owned[pos // self.block_size]
+        off = pos % self.block_size
+        kq = self.k_cache[row][blk, :, off].float() * self.k_scale[row][blk, :, off].unsqueeze(-1)
+        d = self.head_dim
+        h = torch.ones(1, 1, dtype=torch.float32, device=self.device)
+        while h.shape[0] < d:
+            h = torch.cat([torch.cat([h, h], 1), torch.cat([h, -h], 1)], 0)
+        k = ((kq.to(dtype).float() @ (h / math.sqrt(d)))).to(dtype)
+        if self.v_quant == "lloydmax3":
+            codes = _unpack3(self.v_packed[row][blk, :, off], d)
+            nb = d // self.lloyd_block
+            cbv = self.v_codebook[row][codes.long()].reshape(*codes.shape[:-1], nb, self.lloyd_block)
+            v = (cbv * self.v_norm[row][blk, :, off].unsqueeze(-1)).reshape(codes.shape).to(dtype)
+        else:
+            v = (self.v_cache[row][blk, :, off].float() * self.v_scale[row][blk, :, off].unsqueeze(-1)).to(dtype)
+        return k.transpose(0, 1).unsqueeze(0), v.transpose(0, 1).unsqueeze(0)
+
+    # --------------------------------------------- copy-on-write, compaction
+
+    def copy_on_write_last_block(self, slot: int) -> int | None:
+        """Give `slot` a private copy of its last block when that block is shared
+        (refcount > 1): copy it on the GPU, drop one reference, point the slot's
+        table at the copy.  Returns the new block id, or None if nothing to do."""
+        owned = self._slot_blocks[slot]
+        if not owned or self._block_refcount.get(owned[-1], 1) <= 1:
+            return None
+        if not self._free_blocks:
+            raise RuntimeError("PagedKVCache: no free blocks")
+        old = owned[-1]
+        new = self._free_blocks.pop()
+        ops.copy_blocks(self._tensors(), [old], [new])
+        self._block_refcount[new] = 1
+        self._block_refcount[old] -= 1
+        owned[-1] = new
+        return new
+
+    def compact(self) -> list[tuple[int, int]]:
+        """Move every live block above the free watermark into the lowest free
+        holes, so the live set occupies blocks ``[0, used_blocks)``.  One GPU
+        block copy for all layers and tensors, then every reference (slot
+        tables, prefix entries, refcounts, pins) is rewritten.  Returns the
+        ``(src, dst)`` moves."""
+        used = self.used_blocks
+        live_high = sorted(b for b in self._block_refcount if b >= used)
+        holes = sorted(b for b in self._free_blocks if b < used)
+        moves = list(zip(live_high, holes))
+        if not moves:
+            return []
+        ops.copy_blocks(self._tensors(), [s for s, _ in moves], [d for _, d in moves])
+        remap = dict(moves)
+        for owned in self._slot_blocks:
+            owned[:] = [remap.get(b, b) for b in owned]
+        stack = [self._trie]
+        while stack:
+            node = stack.pop()
+            if node.entry is not None:
+                node.entry.blocks = [remap.get(b, b) for b in node.entry.blocks]
+            stack.extend(node.children.values())
+        self._block_refcount = {remap.get(b, b): c for b, c in self._block_refcount.items()}
+        self._prefix_block_refs = {remap.get(b, b): c for b, c in self._prefix_block_refs.items()}
+        # the holes are now live; the vacated blocks join the free list (the
+        # highest last, so the LIFO pool hands them out high-first as before)
+        moved_to = set(remap.values())
+        self._free_blocks = [b for b in self._free_blocks if b not in moved_to] + [s for s, _ in moves]
+        return moves
