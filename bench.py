@@ -11,6 +11,9 @@ Workload (one "step" = one decode step of the whole model's KV path):
   * fp16 K/V/q ~ N(0,1) with 1% (2 of 128) outlier channels scaled 20x;
   * distinct cache storage per layer, so the 256 MB Infinity Cache cannot
     serve one layer's KV to the next.
+Each layer runs as one launch that appends the new tokens and attends
+(attn_paged_decode_append; cache bytes and outputs identical to the
+reference's append-then-decode pair, which --separate-append runs instead).
 Inputs are resident in HBM before the timed region.  The 36-layer step is
 captured once in a HIP graph and replayed.  Every timed step re-appends at the
 same positions, so all steps do identical work.
@@ -69,7 +72,9 @@ def step_bytes(lens: np.ndarray) -> dict:
     append = t * HKV * D * 2 * 2 + 4 * t + t * HKV * BYTES_PER_TOKEN_HEAD
     blocks = int(((lens + BS - 1) // BS).sum())
     decode = int(lens.sum()) * HKV * BYTES_PER_TOKEN_HEAD + 2 * BATCH * HQ * D * 2 + 4 * blocks + 4 * BATCH
-    return {"append_layer": append, "decode_layer": decode, "step": NUM_LAYERS * (append + decode)}
+    # the one-launch step reads no slot mapping (the slot comes from the block table, counted in decode)
+    fused = append - 4 * t + decode
+    return {"append_layer": append, "decode_layer": decode, "fused_layer": fused, "step": NUM_LAYERS * (append + decode)}
 
 
 def _fp16_outliers(gen, shape, ch, device):
@@ -121,29 +126,40 @@ def build(device):
     }
 
 
-def make_step(w):
+def decode_layer(w, layer: int, fused: bool):
+    """One layer of the decode step: append the new token of every row, then
+    attend.  fused: one launch (attn_paged_decode_append); otherwise the
+    reference's two calls (quantize_kv_write_paged, attn_paged_decode_cached)."""
     from superl8_serve_amd import ops
 
     scale = 1.0 / math.sqrt(D)
+    if fused:
+        return ops.attn_paged_decode_append(
+            w["q"][layer], w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
+            w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
+    ops.quantize_kv_write_paged(w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer],
+                                w["vc"][layer], w["vs"][layer], w["new_sm"])
+    return ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer],
+                                        w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
+
+
+def make_step(w, fused: bool):
     outs = [None] * NUM_LAYERS
 
     def step():
         for layer in range(NUM_LAYERS):
-            ops.quantize_kv_write_paged(w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer],
-                                        w["vc"][layer], w["vs"][layer], w["new_sm"])
-            outs[layer] = ops.attn_paged_decode_cached(
-                w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer], w["bt"], w["cl"], BS,
-                max_context_len=MAX_LEN, scale=scale)
+            outs[layer] = decode_layer(w, layer, fused)
         return outs
 
     return step
 
 
-def time_decode_kernel(w, reps: int) -> dict:
+def time_decode_kernel(w, reps: int, fused: bool) -> dict:
     """Average durations of the decode attention kernel and of its merge
     kernel, from HIP events the library records on the launch stream around
     each kernel (s8kv_timing_begin/end), over `reps` eager passes of the 36
-    decode calls.  A preceding spin kernel keeps the GPU ahead of the host so
+    decode calls (the one-launch step when `fused`: its append rewrites the
+    same bytes).  A preceding spin kernel keeps the GPU ahead of the host so
     host launch latency never enters an interval."""
     import ctypes
 
@@ -158,8 +174,12 @@ def time_decode_kernel(w, reps: int) -> dict:
     _lib.check(lib.s8kv_timing_begin(), "s8kv_timing_begin")
     for _ in range(reps):
         for layer in range(NUM_LAYERS):
-            ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
-                                         w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
+            if fused:
+                decode_layer(w, layer, True)
+            else:
+                ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
+                                             w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN,
+                                             scale=scale)
     n = ctypes.c_int(0)
     dk, mk = ctypes.c_double(0.0), ctypes.c_double(0.0)
     _lib.check(lib.s8kv_timing_end(ctypes.byref(n), ctypes.byref(dk), ctypes.byref(mk)), "s8kv_timing_end")
@@ -506,6 +526,9 @@ def main():
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
     ap.add_argument("--kernel-reps", type=int, default=3, help="event-timed decode passes over the 36 layers")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
+                         "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
     ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy"], default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
@@ -540,7 +563,8 @@ def main():
 
     device = "cuda"
     w = build(device)
-    step = make_step(w)
+    fused = not args.separate_append
+    step = make_step(w, fused)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -562,13 +586,17 @@ def main():
 
     b = step_bytes(w["lens"])
     value = b["step"] / (ms * 1e-3) / 1e9
-    kt = time_decode_kernel(w, args.kernel_reps)
+    kt = time_decode_kernel(w, args.kernel_reps, fused)
     dec_s = kt["decode_s"]
-    achieved = b["decode_layer"] / dec_s / 1e9
+    kernel = "decode_kernel<128, int8, fused append>" if fused else "decode_kernel<128, int8>"
+    kernel_bytes = b["fused_layer"] if fused else b["decode_layer"]
+    achieved = kernel_bytes / dec_s / 1e9
     traffic = None
     if args.traffic_json and os.path.exists(args.traffic_json):
         with open(args.traffic_json) as f:
-            traffic = json.load(f).get("decode_kernel_hbm_bytes_per_launch")
+            tj = json.load(f)
+        if tj.get("kernel") == kernel:  # measured for this kernel
+            traffic = tj.get("decode_kernel_hbm_bytes_per_launch")
     result = {
         "metric": "paged int8 decode-attn+append HBM GB/s (% of peak) at Qwen3-8B shapes, b=64",
         "value": round(value, 2),
@@ -588,13 +616,15 @@ def main():
             "layers": NUM_LAYERS, "context": f"lognormal(median 2048, sigma {SIGMA}) clipped [256, 8192], seed {SEED}",
             "sum_context_tokens": int(w["lens"].sum()), "pool_blocks_per_layer": POOL_BLOCKS,
             "bytes_per_step": b["step"],
+            "append": "in the decode launch (attn_paged_decode_append)" if fused
+                      else "separate kernel (quantize_kv_write_paged)",
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "roofline": {
-            "kernel": "decode_kernel<128, int8>",
+            "kernel": kernel,
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-            "avg_launch_us": round(dec_s * 1e6, 2), "algorithmic_bytes_per_launch": b["decode_layer"],
+            "avg_launch_us": round(dec_s * 1e6, 2), "algorithmic_bytes_per_launch": kernel_bytes,
             "merge_kernel_avg_us": round(kt["merge_s"] * 1e6, 2), "timed_launches": kt["launches"],
         },
     }

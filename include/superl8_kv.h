@@ -107,6 +107,30 @@ int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int num_kv_heads
                      void* stream);
 
 /*
+ * One decode step of a layer in one launch: append, then attend.  Row b's new
+ * token (k_new / v_new [batch][num_kv_heads][head_dim] fp16, element strides
+ * given, unit stride on head_dim) is quantized exactly as s8kv_append_int8
+ * does and written at position context_lens[b] - 1 of row b's block table;
+ * the attention then covers positions 0 .. context_lens[b] - 1 as
+ * s8kv_decode_int8 does.  Replaces the pair quantize_kv_write_paged
+ * (write_decode_static, kv_cache.py:1103-1116) + attn_paged_decode_cached
+ * (decode_attn_static, kv_cache.py:1190-1201) when the appended slots are the
+ * rows' next positions, which is how the reference's decode step computes
+ * them (gqa_attention.py:174-190; kv_cache.py:1083-1093 and 1129-1146 write
+ * at lengths[i] and attend lengths[i] + 1 tokens).  Rows with context_lens[b] == 0 or
+ * > max_context_len append nothing.  The block holding a row's new token must
+ * not be read by another row of the same call.  Other arguments and the
+ * workspace as s8kv_decode_int8.
+ */
+int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                            int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                            int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                            int64_t num_blocks, int block_size, const int32_t* block_table,
+                            int64_t block_table_stride, const int32_t* context_lens, int max_context_len, float scale,
+                            void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Decode attention over the K8V3 cache (int8 K, 3-bit Lloyd-Max V dequantized
  * in-kernel).  Replaces superl8.attn_paged_decode_k8v3(q, k_cache, k_scale,
  * v_packed, v_norm, v_codebook, block_table, context_lens, block_size, *,

@@ -12,66 +12,16 @@ namespace s8kv {
 
 constexpr int kAppendWaves = 4;  // waves per workgroup
 
-template <int D>
-struct RowLayout {
-  static constexpr int E = D >= 64 ? D / 64 : 1;    // elements per lane
-  static constexpr int ACTIVE = D >= 64 ? 64 : D;   // lanes holding data
-};
-
-// Fixed-order fp32 Walsh-Hadamard transform of one D-row spread over the wave:
-// stages h = 1, 2, ..., D/2; the pair (i, i+h) with bit h of i clear becomes
-// (x[i] + x[i+h], x[i] - x[i+h]).
-template <int D>
-__device__ __forceinline__ void fwht_row(float (&x)[RowLayout<D>::E], int lane) {
-  constexpr int E = RowLayout<D>::E;
-#pragma unroll
-  for (int h = 1; h < D && h < 64; h <<= 1) {
-    const bool upper = (lane & h) != 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      float p = shfl_xor_f(x[j], h);
-      x[j] = upper ? (p - x[j]) : (x[j] + p);
-    }
-  }
-#pragma unroll
-  for (int hs = 1; hs < E; hs <<= 1) {  // h = 64*hs, in-lane
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      if ((j & hs) == 0) {
-        float a = x[j], b = x[j + hs];
-        x[j] = a + b;
-        x[j + hs] = a - b;
-      }
-    }
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void load_row_f16(const _Float16* p, float (&x)[RowLayout<D>::E], int lane) {
-  constexpr int E = RowLayout<D>::E;
-#pragma unroll
-  for (int j = 0; j < E; ++j) {
-    int e = lane + 64 * j;
-    x[j] = (lane < RowLayout<D>::ACTIVE) ? (float)p[e] : 0.0f;
-  }
-}
-
 // Per-row RTN int8 of the wave's row; writes D bytes at `byte_off` and the scale.
 template <int D>
 __device__ __forceinline__ void rtn_store_row(const float (&y)[RowLayout<D>::E], int lane, rsrc_t qbuf,
                                               uint32_t byte_off, rsrc_t sbuf, uint32_t scale_off) {
   constexpr int E = RowLayout<D>::E;
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(y[j]));
-  amax = wave_max(amax);
-  const float scale = amax / 127.0f;
+  int q[E];
+  const float scale = rtn_row<D>(y, q);
   if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-      int q = rtn_i8(y[j], scale);
-      bstore8((uint8_t)(int8_t)q, qbuf, byte_off + lane + 64 * j);
-    }
+    for (int j = 0; j < E; ++j) bstore8((uint8_t)(int8_t)q[j], qbuf, byte_off + lane + 64 * j);
   }
   if (lane == 0) bstore32(__builtin_bit_cast(uint32_t, scale), sbuf, scale_off);
 }

@@ -102,6 +102,14 @@ struct DecodeArgs {
   float* ws_ml;         // [Hkv][slots][G][2]  (max, sum) of each segment
   float* ws_acc;        // [Hkv][slots][G][D]  unnormalized output of each segment
   int* ws_desc;         // [batch][2]  first and last slice of each split row, -1 if not split
+  // fused append (decode_kernel<D, false, true>): row b's new token, at position
+  // context_lens[b] - 1, is quantized and written by the workgroup that holds
+  // the row's last tile, which attends over it from registers
+  const _Float16* k_new;  // [batch][Hkv][D] fp16, unit stride on D
+  const _Float16* v_new;
+  int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
+  float rot_norm;         // fp32(1/sqrt(D)): the K rotation's normalisation
+  int smem_new;           // LDS byte offset of the new token's rows: fp16 K, fp16 V, int8 K, int8 V, two scales
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -147,9 +155,14 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
-// Context length of row b from the LDS copy of the first kLensLds rows.
+// Context length of row b (clamped to [0, max_context_len]) from the LDS copy
+// of the first kLensLds rows' context_lens entries.
 __device__ __forceinline__ int lens_at(const DecodeArgs& a, const int* lens_lds, int b) {
-  return b < kLensLds ? lens_lds[b] : row_len(a, b);
+  return b < kLensLds ? max(0, min(lens_lds[b], a.max_context_len)) : row_len(a, b);
+}
+// The unclamped context_lens entry of row b.
+__device__ __forceinline__ int raw_len_at(const DecodeArgs& a, const int* lens_lds, int b) {
+  return b < kLensLds ? lens_lds[b] : a.context_lens[b];
 }
 
 // Stream length of all rows (every wave computes it; no barrier).
@@ -201,9 +214,11 @@ struct TileIO {
   float4_t vs[2][C::NB];
 };
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool FUSE>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
+  static_assert(!(FUSE && K8V3), "the fused append covers the int8 layout");
+  constexpr int E = RowLayout<D>::E;
   // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids][context lengths]
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
@@ -218,7 +233,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // ---- context lengths -> LDS (one global round trip for the whole prologue) ----
-  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = row_len(a, i);
+  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
   __syncthreads();
 
   // ---- this workgroup's slice [lo, hi) of the token stream ----
@@ -312,7 +327,19 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // sub-split's block ids, issued early so their latency overlaps other work.
   half8_t qraw[C::KCH / 8];
   int btv[kBtRegs];
+  _Float16 knr[E], vnr[E];  // fused append: row rb's new K and V (RowLayout lanes)
   auto prefetch_segment = [&](int rb, int s0) {
+    if constexpr (FUSE) {
+      const int lane_o = opaque_int(threadIdx.x) & 63;
+      const _Float16* kp = a.k_new + (int64_t)rb * a.kn_stride_b + (int64_t)h * a.kn_stride_h;
+      const _Float16* vp = a.v_new + (int64_t)rb * a.vn_stride_b + (int64_t)h * a.vn_stride_h;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const bool on = lane_o < RowLayout<D>::ACTIVE;
+        knr[e] = on ? kp[lane_o + 64 * e] : (_Float16)0.0f;
+        vnr[e] = on ? vp[lane_o + 64 * e] : (_Float16)0.0f;
+      }
+    }
     const int tid_o = opaque_int(threadIdx.x);
     const int cl = tid_o & 15, gl = (tid_o & 63) >> 4;
     const _Float16* qp =
@@ -411,6 +438,25 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
           const _Float16 qh = (_Float16)val;
           qhi[m][e] = qh;
           qlo[m][e] = (_Float16)(val - (float)qh);
+        }
+      }
+    }
+
+    // fused append: the wave that will process the row's last tile keeps the
+    // new token's fp16 rows in LDS until that tile (its registers are needed
+    // by the tile loop)
+    const int raw_len = raw_len_at(a, lens_lds, b);
+    const bool app_seg = FUSE && raw_len >= 1 && raw_len <= a.max_context_len && s1 == padL;
+    if constexpr (FUSE) {
+      const int u_last = s0 + ((s1 - 1 - s0) / kSubTokens) * kSubTokens;
+      if (app_seg && wave == ((padL - kTile - u_last) / kTile) % kDecWaves) {
+        _Float16* nf = reinterpret_cast<_Float16*>(smem + a.smem_new);
+        if (lane < RowLayout<D>::ACTIVE) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            nf[lane + 64 * e] = knr[e];
+            nf[D + lane + 64 * e] = vnr[e];
+          }
         }
       }
     }
@@ -526,6 +572,39 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         constexpr bool PREFETCH = decltype(prefetch_tag)::value;
         const int tn = tb + kTile * kDecWaves;
         uint32_t rn = 0;
+
+        // 0. fused append: the row's last tile takes the new token's values
+        // from the LDS rows the appending wave wrote (the loads may predate
+        // the cache store)
+        if constexpr (FUSE && MASKED) {
+          if (app_seg && tb == padL - kTile) {
+            const int r = last - tb;  // tile row of the new token
+            const char* nk = smem + a.smem_new + 4 * D;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              if (16 * s + c == r) {
+#pragma unroll
+                for (int w = 0; w < C::KCH / 4; ++w)
+                  io.k[s][w] = *reinterpret_cast<const uint32_t*>(nk + g * C::KCH + 4 * w);
+              }
+            }
+#pragma unroll
+            for (int jj = 0; jj < C::VLOADS; ++jj)
+              if (jj * RPI + lane / LPR == r) io.v[jj] = *reinterpret_cast<const u32x4_t*>(nk + D + (lane % LPR) * 16);
+            const float nks = reinterpret_cast<const float*>(nk + 2 * D)[0];
+            const float nvs = reinterpret_cast<const float*>(nk + 2 * D)[1];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                if (16 * s + 4 * g + i == r) {
+                  io.ks[s][i] = nks;
+                  io.vs[s][0][i] = nvs;
+                }
+              }
+            }
+          }
+        }
 
         // 1. V tile -> LDS (int8 rows, or K8V3 codes expanded to fp16 rows)
         if constexpr (!K8V3) {
@@ -672,6 +751,42 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
           process(tb, std::false_type{}, std::true_type{});
           tb += kTile * kDecWaves;
+        }
+        if constexpr (FUSE) {
+          if (app_seg && tb == padL - kTile) {  // the row's last tile: append its new token first
+            // (the append kernel's arithmetic; runs while the tile's loads are in flight)
+            const _Float16* nf = reinterpret_cast<const _Float16*>(smem + a.smem_new);
+            float x[E], y[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {  // lanes past a short row hold zeros (they enter the absmax)
+              const bool on = lane < RowLayout<D>::ACTIVE;
+              x[e] = on ? (float)nf[lane + 64 * e] : 0.0f;
+              y[e] = on ? (float)nf[D + lane + 64 * e] : 0.0f;
+            }
+            fwht_row<D>(x, lane);
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = (float)(_Float16)materialize(x[e] * a.rot_norm);
+            int qk[E], qv[E];
+            const float sk = rtn_row<D>(x, qk);
+            const float sv = rtn_row<D>(y, qv);
+            const uint32_t nrow = tile_in_block ? tile_row0(tb) + (uint32_t)(last - tb) : row_of(last);
+            char* nq = smem + a.smem_new + 4 * D;  // int8 K row, int8 V row, K scale, V scale
+            if (lane < RowLayout<D>::ACTIVE) {
+#pragma unroll
+              for (int e = 0; e < E; ++e) {
+                bstore8((uint8_t)(int8_t)qk[e], kc, nrow * (uint32_t)D + lane + 64 * e);
+                bstore8((uint8_t)(int8_t)qv[e], vc, nrow * (uint32_t)D + lane + 64 * e);
+                nq[lane + 64 * e] = (char)qk[e];
+                nq[D + lane + 64 * e] = (char)qv[e];
+              }
+            }
+            if (lane == 0) {
+              bstore32(__builtin_bit_cast(uint32_t, sk), ks, nrow * 4u);
+              bstore32(__builtin_bit_cast(uint32_t, sv), vs, nrow * 4u);
+              reinterpret_cast<float*>(nq + 2 * D)[0] = sk;
+              reinterpret_cast<float*>(nq + 2 * D)[1] = sv;
+            }
+          }
         }
         process(tb, std::true_type{}, std::false_type{});
       }
@@ -855,23 +970,25 @@ static int plan_wg_per_head(int num_kv_heads, int resident_per_cu) {
   return w < 1 ? 1 : (w > cap ? cap : w);
 }
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool FUSE>
 static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
+  constexpr int kNewBytes = FUSE ? 6 * D + 16 : 0;  // fused append: fp16 K and V rows, int8 K and V rows, scales
   const auto smem_main_for = [](int group) {
     const int merge = kDecWaves * (group * D + 32) * 4;
     return ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
   };
   a.smem_main = smem_main_for(a.group);
-  const int smem = a.smem_main + (kMaxSubBlocks + kLensLds) * 4;
+  a.smem_new = a.smem_main + (kMaxSubBlocks + kLensLds) * 4;
+  const int smem = a.smem_new + kNewBytes;
   // Resident workgroups per CU at this LDS size (depends on the GQA group),
   // queried once per group size.
   static int resident_by_group[17] = {};
   static bool lds_raised = false;
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3, FUSE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            smem_main_for(16) + (kMaxSubBlocks + kLensLds) * 4) != hipSuccess) {
+                            smem_main_for(16) + (kMaxSubBlocks + kLensLds) * 4 + kNewBytes) != hipSuccess) {
       set_error("s8kv_decode: cannot raise the dynamic LDS limit");
       return S8KV_ERR_LAUNCH;
     }
@@ -880,7 +997,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   int& resident = resident_by_group[a.group];
   if (resident == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3>, 64 * kDecWaves, smem) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3, FUSE>, 64 * kDecWaves, smem) != hipSuccess ||
         n <= 0)
       n = 2;
     resident = n < kMaxResidentPerCU ? n : kMaxResidentPerCU;
@@ -895,9 +1012,9 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.wg_per_head * a.num_kv_heads), mgrid(a.num_kv_heads, a.batch);
   hipEvent_t* ev = timing_slot(stream);
   if (ev) {  // events stamped with the kernels' own start and end times
-    hipExtLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
+    hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, K8V3>), grid, dim3(64 * kDecWaves), smem, stream, a);
+    hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, a);
   }
   int rc = check_launch("s8kv_decode");
   if (rc == S8KV_OK) {
@@ -916,7 +1033,7 @@ static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int
   return (int64_t)num_q_heads * (batch + wph) * (head_dim + 2) * 4 + (int64_t)batch * 8;
 }
 
-static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                          int64_t num_blocks, int block_size, int max_context_len, float scale, void* workspace,
                          int64_t workspace_bytes_given, void* stream) {
   S8KV_REQUIRE(batch >= 0, S8KV_ERR_INVALID, "decode: batch < 0");
@@ -936,6 +1053,7 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
                "decode: batch * max_context_len too large");
   S8KV_REQUIRE(a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.block_table && a.context_lens && a.out,
                S8KV_ERR_INVALID, "decode: null pointer argument");
+  S8KV_REQUIRE(!fuse || (a.k_new && a.v_new), S8KV_ERR_INVALID, "decode_append: null k_new / v_new");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "decode: per-layer cache exceeds 4 GiB");
   a.batch = batch;
@@ -955,6 +1073,7 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
   a.max_context_len = max_context_len;
   a.q_vec = ((uintptr_t)a.q % 16 == 0) && (a.q_stride_b % 8 == 0) && (a.q_stride_h % 8 == 0);
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
+  a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
   const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
   S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
                "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes_given);
@@ -963,11 +1082,21 @@ static int decode_common(DecodeArgs& a, bool k8v3, int batch, int num_q_heads, i
   a.ws_acc = a.ws_ml + partials * 2;
   a.ws_desc = reinterpret_cast<int*>(a.ws_acc + partials * head_dim);
   hipStream_t s = (hipStream_t)stream;
+  if (fuse) {
+    if (k8v3) return S8KV_ERR_UNSUPPORTED;
+    switch (head_dim) {
+      case 32: return launch_decode<32, false, true>(a, s);
+      case 64: return launch_decode<64, false, true>(a, s);
+      case 128: return launch_decode<128, false, true>(a, s);
+      case 256: return launch_decode<256, false, true>(a, s);
+    }
+    return S8KV_ERR_UNSUPPORTED;
+  }
   switch (head_dim) {
-    case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false>(a, s);
-    case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false>(a, s);
-    case 128: return k8v3 ? launch_decode<128, true>(a, s) : launch_decode<128, false>(a, s);
-    case 256: return k8v3 ? launch_decode<256, true>(a, s) : launch_decode<256, false>(a, s);
+    case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false, false>(a, s);
+    case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false, false>(a, s);
+    case 128: return k8v3 ? launch_decode<128, true, false>(a, s) : launch_decode<128, false, false>(a, s);
+    case 256: return k8v3 ? launch_decode<256, true, false>(a, s) : launch_decode<256, false, false>(a, s);
   }
   return S8KV_ERR_UNSUPPORTED;
 }
@@ -1026,8 +1155,35 @@ extern "C" int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int n
   a.bt_stride = block_table_stride;
   a.context_lens = context_lens;
   a.out = (_Float16*)out;
-  return decode_common(a, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size, max_context_len,
-                       scale, workspace, workspace_bytes, stream);
+  return decode_common(a, false, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                                       int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                                       int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int8_t* v_cache,
+                                       float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                       int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                       float scale, void* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  a.k_new = (const _Float16*)k_new;
+  a.v_new = (const _Float16*)v_new;
+  a.kn_stride_b = k_new_stride_b;
+  a.kn_stride_h = k_new_stride_h;
+  a.vn_stride_b = v_new_stride_b;
+  a.vn_stride_h = v_new_stride_h;
+  return decode_common(a, false, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1048,6 +1204,6 @@ extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int n
   a.bt_stride = block_table_stride;
   a.context_lens = context_lens;
   a.out = (_Float16*)out;
-  return decode_common(a, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size, max_context_len,
-                       scale, workspace, workspace_bytes, stream);
+  return decode_common(a, true, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
 }

@@ -125,6 +125,69 @@ __device__ __forceinline__ int rtn_i8(float y, float scale) {
   return (int)q;
 }
 
+// ---------------------------------------------------------------------------
+// One (token, head) row spread over a wave: lane l holds elements l, l+64, ...
+// (rows shorter than 64 use the first D lanes).
+// ---------------------------------------------------------------------------
+template <int D>
+struct RowLayout {
+  static constexpr int E = D >= 64 ? D / 64 : 1;    // elements per lane
+  static constexpr int ACTIVE = D >= 64 ? 64 : D;   // lanes holding data
+};
+
+// Fixed-order fp32 Walsh-Hadamard transform of one D-row spread over the wave:
+// stages h = 1, 2, ..., D/2; the pair (i, i+h) with bit h of i clear becomes
+// (x[i] + x[i+h], x[i] - x[i+h]).
+template <int D>
+__device__ __forceinline__ void fwht_row(float (&x)[RowLayout<D>::E], int lane) {
+  constexpr int E = RowLayout<D>::E;
+#pragma unroll
+  for (int h = 1; h < D && h < 64; h <<= 1) {
+    const bool upper = (lane & h) != 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      float p = shfl_xor_f(x[j], h);
+      x[j] = upper ? (p - x[j]) : (x[j] + p);
+    }
+  }
+#pragma unroll
+  for (int hs = 1; hs < E; hs <<= 1) {  // h = 64*hs, in-lane
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      if ((j & hs) == 0) {
+        float a = x[j], b = x[j + hs];
+        x[j] = a + b;
+        x[j + hs] = a - b;
+      }
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void load_row_f16(const _Float16* p, float (&x)[RowLayout<D>::E], int lane) {
+  constexpr int E = RowLayout<D>::E;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    int e = lane + 64 * j;
+    x[j] = (lane < RowLayout<D>::ACTIVE) ? (float)p[e] : 0.0f;
+  }
+}
+
+// Per-row RTN int8 of the wave's row (lane layout of RowLayout): scale =
+// absmax/127 over the wave, codes rint(y/scale) clamped to +-127.
+template <int D>
+__device__ __forceinline__ float rtn_row(const float (&y)[RowLayout<D>::E], int (&q)[RowLayout<D>::E]) {
+  constexpr int E = RowLayout<D>::E;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(y[j]));
+  amax = wave_max(amax);
+  const float scale = amax / 127.0f;
+#pragma unroll
+  for (int j = 0; j < E; ++j) q[j] = rtn_i8(y[j], scale);
+  return scale;
+}
+
 // Spread the low 4 bits of x into bit 0 of each byte.
 __device__ __forceinline__ uint32_t spread4(uint32_t x) {
   return ((x & 0xFu) * 0x00204081u) & 0x01010101u;

@@ -23,6 +23,7 @@ __all__ = [
     "quantize_kv_write_paged_k8v3",
     "attn_paged_decode_cached",
     "attn_paged_decode_k8v3",
+    "attn_paged_decode_append",
     "decode_workspace_bytes",
     "attn_paged_verify",
     "copy_blocks",
@@ -206,6 +207,48 @@ def attn_paged_decode_cached(q, k_cache, k_scale, v_cache, v_scale, block_table,
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
     _lib.check(rc, "attn_paged_decode_cached")
+    return out
+
+
+def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale, block_table, context_lens,
+                             block_size, *, max_context_len, scale):
+    """One decode step of a layer in one launch: append row b's new token at
+    position ``context_lens[b] - 1`` of its block table, then attend over
+    positions ``0 .. context_lens[b] - 1``.
+
+    Same cache bytes as ``quantize_kv_write_paged`` at those slots followed by
+    ``attn_paged_decode_cached`` (the pair ``write_decode_static`` +
+    ``decode_attn_static`` runs, kv_cache.py:1103-1116 and 1190-1201), and the
+    same output.  ``k_new``, ``v_new``: fp16 ``[B, Hkv, D]``.  Rows with
+    ``context_lens[b] == 0`` or ``> max_context_len`` append nothing.  The
+    block receiving a row's new token must not be read by another row of the
+    same call (a block being appended to is owned by its sequence)."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_new", k_new, torch.float16, dev)
+    _on_gpu("v_new", v_new, torch.float16, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
+    k_new = _tokens_view(k_new, "k_new", hkv, d)
+    v_new = _tokens_view(v_new, "v_new", hkv, d)
+    _require(k_new.shape[0] == b and v_new.shape[0] == b, f"k_new and v_new must be [{b}, {hkv}, {d}]")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_append_int8(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_new.data_ptr(), k_new.stride(0), k_new.stride(1), v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+        bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_append")
     return out
 
 
