@@ -133,20 +133,43 @@ __device__ __forceinline__ int slot_first(int c, int W, int classes) { return (c
 __device__ __forceinline__ float slot_weight(int c, int classes, int skew_permille) {
   return classes > 1 ? 1.0f + 0.001f * (float)(skew_permille * (classes - 1 - 2 * c) / (classes - 1)) : 1.0f;
 }
-// Stream position where workgroup j's slice starts (0 <= j < W).
-__device__ __forceinline__ int slice_start(int j, int total, int W, int ncls, int skew_permille) {
+// The slice layout is computed across lanes, lane c describing class c (at
+// most 8 classes): every wave of every workgroup computes it, and scalar code
+// doing the same would queue on the CU's one scalar unit.
+struct SliceLayout {
+  int f0, f1;   // lane c: workgroups [f0, f1) are in class c (f0 = f1 = W past the last class)
+  int sz;       // lane c: slice length of class c
+  int start;    // lane c: stream position of class c's first slice
+};
+__device__ __forceinline__ SliceLayout slice_layout(int total, int W, int ncls, int skew_permille, int lane) {
   const int classes = max(1, min(ncls, min(W, kMaxResidentPerCU)));
-  float wsum = 0.0f;
-  for (int c = 0; c < classes; ++c)
-    wsum += (float)(slot_first(c + 1, W, classes) - slot_first(c, W, classes)) * slot_weight(c, classes, skew_permille);
+  const bool act = lane < classes;
+  SliceLayout s;
+  s.f0 = act ? slot_first(lane, W, classes) : W;
+  s.f1 = act ? slot_first(lane + 1, W, classes) : W;
+  const float wt = act ? slot_weight(lane, classes, skew_permille) : 0.0f;
+  float ws = (float)(s.f1 - s.f0) * wt;  // lanes 0..7 sum in a fixed tree order
+  ws += shfl_xor_f(ws, 1);
+  ws += shfl_xor_f(ws, 2);
+  ws += shfl_xor_f(ws, 4);
+  const float wsum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), 0));
   const float unit = (float)total / wsum;
-  int pos = 0;
-  for (int c = 0; c < classes; ++c) {
-    const int n = min(j, slot_first(c + 1, W, classes)) - slot_first(c, W, classes);
-    if (n <= 0) break;
-    pos += n * max(kTile, padded32((int)ceilf(unit * slot_weight(c, classes, skew_permille))));
+  s.sz = act ? max(kTile, padded32((int)ceilf(unit * wt))) : 0;
+  const int span = (s.f1 - s.f0) * s.sz;
+  int incl = span;
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
   }
-  return pos;
+  s.start = incl - span;
+  return s;
+}
+// Stream position where workgroup j's slice starts (0 <= j < W).
+__device__ __forceinline__ int slice_start(const SliceLayout& s, int j) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(s.f0 <= j && j < s.f1);
+  const int cl = m ? (int)__builtin_ctzll(m) : 0;
+  return __builtin_amdgcn_readlane(s.start + (j - s.f0) * s.sz, cl);
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -246,10 +269,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         if (h == 0 && tid == 0) a.ws_desc[2 * b] = -1;
       }
   }
-  const int lo = slice_start(j, total, a.wg_per_head, a.slot_classes, a.slot_skew);
+  const SliceLayout sl = slice_layout(total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
+  const int lo = slice_start(sl, j);
   if (lo >= total) return;
-  const int hi =
-      j + 1 >= a.wg_per_head ? total : min(total, slice_start(j + 1, total, a.wg_per_head, a.slot_classes, a.slot_skew));
+  const int hi = j + 1 >= a.wg_per_head ? total : min(total, slice_start(sl, j + 1));
 
   // ---- first row whose stream range holds lo: wave-level prefix scan ----
   int b = 0, pb = 0;  // row, and the start of its stream range
