@@ -63,6 +63,39 @@ def test_prefill_decode_flow(v_quant, block_size):
     assert np.abs(v16.float().cpu().numpy() - rv.astype(np.float32)).max() <= 1e-3 * max(1.0, np.abs(rv).max())
 
 
+@pytest.mark.parametrize("v_quant", ["int8", "lloydmax3"])
+def test_decode_step_equals_write_then_attend(v_quant):
+    """decode_step (one launch for int8) leaves the same cache and returns the
+    same output as write_decode followed by decode_attn."""
+    g = torch.Generator(device=DEV).manual_seed(3)
+    hq, hkv, d, bs = 16, 4, 128, 16
+    caches = [PagedKVCache(1, 4, hkv, 1024, d, device=DEV, block_size=bs, v_quant=v_quant) for _ in range(2)]
+    lens = [300, 0, 47, 512]
+    for c in caches:
+        slots = [c.alloc() for _ in lens]
+        c.ensure_capacity(slots, [n + 1 for n in lens])
+    g2 = torch.Generator(device=DEV).manual_seed(4)
+    for s, n in zip(slots, lens):
+        if n == 0:
+            continue
+        k = torch.randn(1, hkv, n, d, generator=g2, device=DEV).half()
+        v = torch.randn(1, hkv, n, d, generator=g2, device=DEV).half()
+        for c in caches:
+            c.write_prefill(0, k, v, slot=s)
+    kn = torch.randn(len(lens), hkv, d, generator=g, device=DEV).half()
+    vn = torch.randn(len(lens), hkv, d, generator=g, device=DEV).half()
+    q = torch.randn(len(lens), hq, 1, d, generator=g, device=DEV).half()
+    scale = 1.0 / math.sqrt(d)
+    caches[0].write_decode(0, slots, lens, kn, vn)
+    ref = caches[0].decode_attn(0, q, slots, lens, scale=scale)
+    out = caches[1].decode_step(0, q, kn, vn, slots, lens, scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    names = ("k_cache", "k_scale", "v_cache", "v_scale") if v_quant == "int8" else ("k_cache", "k_scale", "v_packed", "v_norm")
+    for name in names:
+        assert torch.equal(getattr(caches[0], name), getattr(caches[1], name)), name
+
+
 def test_chunked_prefill_positions_and_verify():
     g = torch.Generator(device=DEV).manual_seed(1)
     hq, hkv, d, bs = 8, 2, 128, 16
