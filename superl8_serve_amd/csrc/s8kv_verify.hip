@@ -33,6 +33,10 @@ constexpr int kSubKeys = 2048;                 // block ids staged in LDS per 20
 constexpr int kMaxSubBlocks = kSubKeys / 4 + 2;  // block_size >= 4
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kMaxSlack = 8.0f;
+// Running max before any key: finite, so exp2(score - max) is 0 for a masked
+// score (-inf) and never NaN, with no test per score; any real score exceeds
+// it by more than kMaxSlack, which makes the first visible tile rescale (by 0).
+constexpr float kMaxInit = -1.0e30f;
 
 template <int D>
 struct Cfg {
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     }
   }
 
-  float m_run = kNegInf;
+  float m_run = kMaxInit;
   float l_run = 0.0f;
   float4_t acc[C::NPV];
 #pragma unroll
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       mt = fmaxf(mt, shfl_xor_f(mt, 32));
       if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
         const float m_new = fmaxf(m_run, mt);
-        const float alpha = m_new == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
         for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
@@ -288,7 +292,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float x = pr[s][i];
-          const float e = x == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(x - m_run);
+          const float e = __builtin_amdgcn_exp2f(x - m_run);
           l_run += e;
           const float w = materialize(e * vsc[s][i]);  // one value for hi and lo
           const _Float16 wh = (_Float16)w;
