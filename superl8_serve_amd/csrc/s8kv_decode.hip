@@ -442,14 +442,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         }
       }
 #pragma unroll
-      for (int m = 16; m <= 32; m <<= 1) {
-        const bool upper = (lane & m) != 0;
+      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x16(x[i], lane);
 #pragma unroll
-        for (int i = 0; i < C::KCH; ++i) {
-          const float p = shfl_xor_f(x[i], m);
-          x[i] = upper ? (p - x[i]) : (x[i] + p);
-        }
-      }
+      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x32(x[i], lane);
 #pragma unroll
       for (int m = 0; m < C::NQK; ++m) {
 #pragma unroll
@@ -699,8 +694,8 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             mt = fmaxf(mt, x);
           }
         }
-        mt = fmaxf(mt, shfl_xor_f(mt, 16));
-        mt = fmaxf(mt, shfl_xor_f(mt, 32));
+        mt = max_x16(mt);
+        mt = max_x32(mt);
         if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
           const float m_new = fmaxf(m_run, mt);
           const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
@@ -828,9 +823,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     const int lane = tid & 63;
     const int c = lane & 15;
     const int g = lane >> 4;
-    float l_tot = l_run;
-    l_tot += shfl_xor_f(l_tot, 16);
-    l_tot += shfl_xor_f(l_tot, 32);
+    const float l_tot = sum_x32(sum_x16(l_run));
     __syncthreads();  // every wave is done with its V staging and the staged block ids
     float* mrg = reinterpret_cast<float*>(smem);
     const int wstride = G * D + 32;

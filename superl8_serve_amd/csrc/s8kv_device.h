@@ -65,6 +65,38 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
 }
 
+// Exchanges across lane ^ 16 and lane ^ 32 on the VALU (gfx950
+// v_permlane16_swap / v_permlane32_swap, both operands x): the two results
+// hold {x, x of lane ^ m} -- own value first in lanes with bit m clear,
+// partner first in lanes with bit m set.
+struct LanePair { float a, b; };
+__device__ __forceinline__ LanePair lane_pair16(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ LanePair lane_pair32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+// max / sum with the value of lane ^ 16 (or ^ 32); fmax and + are
+// commutative, so the result equals the shuffle-based form bit for bit.
+__device__ __forceinline__ float max_x16(float x) { const LanePair p = lane_pair16(x); return fmaxf(p.a, p.b); }
+__device__ __forceinline__ float max_x32(float x) { const LanePair p = lane_pair32(x); return fmaxf(p.a, p.b); }
+__device__ __forceinline__ float sum_x16(float x) { const LanePair p = lane_pair16(x); return p.a + p.b; }
+__device__ __forceinline__ float sum_x32(float x) { const LanePair p = lane_pair32(x); return p.a + p.b; }
+// Walsh-Hadamard butterfly across lane ^ 16 (^ 32): lanes with the bit clear
+// get x + partner, lanes with it set get partner - x.
+__device__ __forceinline__ float butterfly_x16(float x, int lane) {
+  const LanePair p = lane_pair16(x);
+  return (lane & 16) ? p.a - p.b : p.a + p.b;
+}
+__device__ __forceinline__ float butterfly_x32(float x, int lane) {
+  const LanePair p = lane_pair32(x);
+  return (lane & 32) ? p.a - p.b : p.a + p.b;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));

@@ -137,14 +137,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       }
     }
 #pragma unroll
-    for (int m = 16; m <= 32; m <<= 1) {
-      const bool upper = (lane & m) != 0;
+    for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x16(x[i], lane);
 #pragma unroll
-      for (int i = 0; i < C::KCH; ++i) {
-        const float pv = shfl_xor_f(x[i], m);
-        x[i] = upper ? (pv - x[i]) : (x[i] + pv);
-      }
-    }
+    for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x32(x[i], lane);
 #pragma unroll
     for (int m = 0; m < C::NQK; ++m) {
 #pragma unroll
@@ -276,8 +271,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           mt = fmaxf(mt, x);
         }
       }
-      mt = fmaxf(mt, shfl_xor_f(mt, 16));
-      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      mt = max_x16(mt);
+      mt = max_x32(mt);
       if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
         const float m_new = fmaxf(m_run, mt);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -347,9 +342,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   }
 
   // ---- normalize and write this wave's 16 rows ----
-  float l_tot = l_run;
-  l_tot += shfl_xor_f(l_tot, 16);
-  l_tot += shfl_xor_f(l_tot, 32);
+  const float l_tot = sum_x32(sum_x16(l_run));
   if (pos < a.max_queries && (r - pos * G) < G) {
     const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
     _Float16* op = a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
