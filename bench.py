@@ -400,10 +400,11 @@ K8V3_BATCH = 32
 K8V3_BYTES_PER_TOKEN_HEAD = D + 4 + D * 3 // 8 + 4 * (D // 128)  # 184 B
 
 
-def run_k8v3(steps: int, warmup: int) -> None:
+def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
     """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
     36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
-    needed, distinct storage per layer."""
+    needed, distinct storage per layer; one launch per layer
+    (attn_paged_decode_append_k8v3) unless `fused` is False."""
     import torch
 
     from oracle import kv_oracle as O
@@ -453,6 +454,11 @@ def run_k8v3(steps: int, warmup: int) -> None:
 
     def step():
         for layer in range(NUM_LAYERS):
+            if fused:
+                ops.attn_paged_decode_append_k8v3(q[layer], k_new[layer], v_new[layer], kc[layer], ks[layer],
+                                                  vp[layer], vn[layer], cb, btd, cl, BS, max_context_len=max_ctx,
+                                                  scale=scale)
+                continue
             ops.quantize_kv_write_paged_k8v3(k_new[layer], v_new[layer], kc[layer], ks[layer], vp[layer], vn[layer],
                                              cb, new_sm)
             ops.attn_paged_decode_k8v3(q[layer], kc[layer], ks[layer], vp[layer], vn[layer], cb, btd, cl, BS,
@@ -484,7 +490,9 @@ def run_k8v3(steps: int, warmup: int) -> None:
         "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20, seed 2)",
         "config": {"workload": "Qwen3-8B K8V3 decode step: 36 layers x (append 1 token/seq + decode)",
                    "batch": t, "sum_context_tokens": int(lens.sum()), "pool_blocks_per_layer": n_blocks,
-                   "bytes_per_step": step_b},
+                   "bytes_per_step": step_b,
+                   "append": "in the decode launch (attn_paged_decode_append_k8v3)" if fused
+                             else "separate kernel (quantize_kv_write_paged_k8v3)"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2)}))
 
 
@@ -555,7 +563,7 @@ def main():
         run_verify(args.workload, args.steps, args.warmup)
         return
     if args.workload == "k8v3":
-        run_k8v3(args.steps, args.warmup)
+        run_k8v3(args.steps, args.warmup, not args.separate_append)
         return
     if args.workload == "copy":
         run_copy(args.steps)

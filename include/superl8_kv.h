@@ -131,6 +131,24 @@ int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_k
                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * s8kv_decode_append_int8 for the K8V3 layout: the new token is written as
+ * s8kv_append_k8v3 writes it (int8 K, 3-bit Lloyd-Max V words and per-128
+ * block norms) at position context_lens[b] - 1, then the row attends as
+ * s8kv_decode_k8v3 does.  Replaces the reference's K8V3 write
+ * (_write_k_int8 + _write_v_lloydmax3, kv_cache.py:587-626) followed by
+ * attn_paged_decode_k8v3 (kv_cache.py:1167-1182).  head_dim 128 or 256,
+ * lloyd_block 128.
+ */
+int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                            int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                            int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int32_t* v_packed,
+                            float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                            int block_size, const int32_t* block_table, int64_t block_table_stride,
+                            const int32_t* context_lens, int max_context_len, float scale, void* out,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Decode attention over the K8V3 cache (int8 K, 3-bit Lloyd-Max V dequantized
  * in-kernel).  Replaces superl8.attn_paged_decode_k8v3(q, k_cache, k_scale,
  * v_packed, v_norm, v_codebook, block_table, context_lens, block_size, *,

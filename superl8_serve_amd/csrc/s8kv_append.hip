@@ -85,58 +85,11 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
     float cb[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
-    float norm[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      // Block nb holds elements 128nb + {lane, lane+64}: fold the halves, then
-      // butterflies 32..1 -- the order the CPU restatement uses.
-      float s = x[2 * nb] * x[2 * nb] + x[2 * nb + 1] * x[2 * nb + 1];
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) s = s + shfl_xor_f(s, m);
-      norm[nb] = __builtin_sqrtf(s);
-    }
-    uint32_t codes[E];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const float nrm = norm[j / 2];
-      const float u = nrm > 0.0f ? x[j] / nrm : 0.0f;
-      float best = fabsf(u - cb[0]);
-      uint32_t c = 0;
-#pragma unroll
-      for (int i = 1; i < 8; ++i) {
-        float d = fabsf(u - cb[i]);
-        if (d < best) {
-          best = d;
-          c = (uint32_t)i;
-        }
-      }
-      codes[j] = c;
-    }
-    // Bit-plane packing: element group g (32 elements) -> words 3g+b, bit i of
-    // word 3g+b = bit b of the code of element 32g+i.  Slot j of lanes 0..31
-    // is group 2j, of lanes 32..63 group 2j+1.
-    uint32_t words[WORDS];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-#pragma unroll
-      for (int b = 0; b < 3; ++b) {
-        uint64_t m = __ballot((codes[j] >> b) & 1u);
-        words[3 * (2 * j) + b] = (uint32_t)m;
-        words[3 * (2 * j + 1) + b] = (uint32_t)(m >> 32);
-      }
-    }
-    if (lane < WORDS) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int i = 0; i < WORDS; ++i) w = (lane == i) ? words[i] : w;
-      bstore32(w, vc, row * (uint32_t)(WORDS * 4) + lane * 4u);
-    }
-    if (lane < NB) {
-      float nv = norm[0];
-#pragma unroll
-      for (int nb = 1; nb < NB; ++nb) nv = (lane == nb) ? norm[nb] : nv;
-      bstore32(__builtin_bit_cast(uint32_t, nv), vs, row * (uint32_t)(NB * 4) + lane * 4u);
-    }
+    uint32_t w;
+    float nv;
+    lloydmax3_encode_row<D>(x, cb, lane, w, nv);
+    if (lane < WORDS) bstore32(w, vc, row * (uint32_t)(WORDS * 4) + lane * 4u);
+    if (lane < NB) bstore32(__builtin_bit_cast(uint32_t, nv), vs, row * (uint32_t)(NB * 4) + lane * 4u);
   }
 }
 

@@ -73,6 +73,13 @@ struct DecCfg {
   static constexpr int VSTAGE = kTile * VROW;                 // bytes per wave
   static constexpr int VLOADS = K8V3 ? (kTile * NG) / 64 : (kTile * D / 16) / 64;  // V loads per lane per tile
   static constexpr int SMEM_A = kDecWaves * VSTAGE;
+  // fused append: the new token's rows in LDS -- fp16 K and V (staged at the
+  // segment start), int8 K, then int8 V (int8) or packed V words (K8V3), then
+  // the K scale and the V scale (int8) or V norms (K8V3)
+  static constexpr int NEW_F16K = 0, NEW_F16V = 2 * D, NEW_I8K = 4 * D, NEW_V = 5 * D;
+  static constexpr int NEW_KS = K8V3 ? NEW_V + 4 * WORDS : NEW_V + D;
+  static constexpr int NEW_VS = NEW_KS + 4;
+  static constexpr int NEW_BYTES = (NEW_VS + 4 * NB + 15) / 16 * 16;
 };
 
 struct DecodeArgs {
@@ -109,7 +116,7 @@ struct DecodeArgs {
   const _Float16* v_new;
   int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
   float rot_norm;         // fp32(1/sqrt(D)): the K rotation's normalisation
-  int smem_new;           // LDS byte offset of the new token's rows: fp16 K, fp16 V, int8 K, int8 V, two scales
+  int smem_new;           // LDS byte offset of the new token's rows (DecCfg NEW_*)
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -240,7 +247,6 @@ struct TileIO {
 template <int D, bool K8V3, bool FUSE>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
-  static_assert(!(FUSE && K8V3), "the fused append covers the int8 layout");
   constexpr int E = RowLayout<D>::E;
   // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids][context lengths]
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -468,12 +474,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     if constexpr (FUSE) {
       const int u_last = s0 + ((s1 - 1 - s0) / kSubTokens) * kSubTokens;
       if (app_seg && wave == ((padL - kTile - u_last) / kTile) % kDecWaves) {
-        _Float16* nf = reinterpret_cast<_Float16*>(smem + a.smem_new);
+        _Float16* nf = reinterpret_cast<_Float16*>(smem + a.smem_new + C::NEW_F16K);
         if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
           for (int e = 0; e < E; ++e) {
             nf[lane + 64 * e] = knr[e];
-            nf[D + lane + 64 * e] = vnr[e];
+            nf[D + lane + 64 * e] = vnr[e];  // NEW_F16V = 2D bytes on
           }
         }
       }
@@ -597,27 +603,43 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         if constexpr (FUSE && MASKED) {
           if (app_seg && tb == padL - kTile) {
             const int r = last - tb;  // tile row of the new token
-            const char* nk = smem + a.smem_new + 4 * D;
+            const char* nn = smem + a.smem_new;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
               if (16 * s + c == r) {
 #pragma unroll
                 for (int w = 0; w < C::KCH / 4; ++w)
-                  io.k[s][w] = *reinterpret_cast<const uint32_t*>(nk + g * C::KCH + 4 * w);
+                  io.k[s][w] = *reinterpret_cast<const uint32_t*>(nn + C::NEW_I8K + g * C::KCH + 4 * w);
               }
             }
+            if constexpr (!K8V3) {
 #pragma unroll
-            for (int jj = 0; jj < C::VLOADS; ++jj)
-              if (jj * RPI + lane / LPR == r) io.v[jj] = *reinterpret_cast<const u32x4_t*>(nk + D + (lane % LPR) * 16);
-            const float nks = reinterpret_cast<const float*>(nk + 2 * D)[0];
-            const float nvs = reinterpret_cast<const float*>(nk + 2 * D)[1];
+              for (int jj = 0; jj < C::VLOADS; ++jj)
+                if (jj * RPI + lane / LPR == r)
+                  io.v[jj] = *reinterpret_cast<const u32x4_t*>(nn + C::NEW_V + (lane % LPR) * 16);
+            } else {
+              const uint32_t* nw = reinterpret_cast<const uint32_t*>(nn + C::NEW_V);
+#pragma unroll
+              for (int jj = 0; jj < C::VLOADS; ++jj) {
+                const int job = jj * 64 + lane;
+                if (job / C::NG == r) {
+                  const int gi = job % C::NG;
+                  io.v[jj].x = nw[3 * gi];
+                  io.v[jj].y = nw[3 * gi + 1];
+                  io.v[jj].z = nw[3 * gi + 2];
+                }
+              }
+            }
+            const float nks = *reinterpret_cast<const float*>(nn + C::NEW_KS);
+            const float* nvs = reinterpret_cast<const float*>(nn + C::NEW_VS);
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 if (16 * s + 4 * g + i == r) {
                   io.ks[s][i] = nks;
-                  io.vs[s][0][i] = nvs;
+#pragma unroll
+                  for (int nb = 0; nb < C::NB; ++nb) io.vs[s][nb][i] = nvs[nb];
                 }
               }
             }
@@ -773,7 +795,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         if constexpr (FUSE) {
           if (app_seg && tb == padL - kTile) {  // the row's last tile: append its new token first
             // (the append kernel's arithmetic; runs while the tile's loads are in flight)
-            const _Float16* nf = reinterpret_cast<const _Float16*>(smem + a.smem_new);
+            const _Float16* nf = reinterpret_cast<const _Float16*>(smem + a.smem_new + C::NEW_F16K);
             float x[E], y[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) {  // lanes past a short row hold zeros (they enter the absmax)
@@ -784,25 +806,50 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             fwht_row<D>(x, lane);
 #pragma unroll
             for (int e = 0; e < E; ++e) x[e] = (float)(_Float16)materialize(x[e] * a.rot_norm);
-            int qk[E], qv[E];
+            int qk[E];
             const float sk = rtn_row<D>(x, qk);
-            const float sv = rtn_row<D>(y, qv);
             const uint32_t nrow = tile_in_block ? tile_row0(tb) + (uint32_t)(last - tb) : row_of(last);
-            char* nq = smem + a.smem_new + 4 * D;  // int8 K row, int8 V row, K scale, V scale
+            char* nn = smem + a.smem_new;
             if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
               for (int e = 0; e < E; ++e) {
                 bstore8((uint8_t)(int8_t)qk[e], kc, nrow * (uint32_t)D + lane + 64 * e);
-                bstore8((uint8_t)(int8_t)qv[e], vc, nrow * (uint32_t)D + lane + 64 * e);
-                nq[lane + 64 * e] = (char)qk[e];
-                nq[D + lane + 64 * e] = (char)qv[e];
+                nn[C::NEW_I8K + lane + 64 * e] = (char)qk[e];
               }
             }
             if (lane == 0) {
               bstore32(__builtin_bit_cast(uint32_t, sk), ks, nrow * 4u);
-              bstore32(__builtin_bit_cast(uint32_t, sv), vs, nrow * 4u);
-              reinterpret_cast<float*>(nq + 2 * D)[0] = sk;
-              reinterpret_cast<float*>(nq + 2 * D)[1] = sv;
+              *reinterpret_cast<float*>(nn + C::NEW_KS) = sk;
+            }
+            if constexpr (!K8V3) {
+              int qv[E];
+              const float sv = rtn_row<D>(y, qv);
+              if (lane < RowLayout<D>::ACTIVE) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                  bstore8((uint8_t)(int8_t)qv[e], vc, nrow * (uint32_t)D + lane + 64 * e);
+                  nn[C::NEW_V + lane + 64 * e] = (char)qv[e];
+                }
+              }
+              if (lane == 0) {
+                bstore32(__builtin_bit_cast(uint32_t, sv), vs, nrow * 4u);
+                *reinterpret_cast<float*>(nn + C::NEW_VS) = sv;
+              }
+            } else {  // 3-bit Lloyd-Max V: packed words and per-128 block norms
+              float cb[8];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
+              uint32_t w;
+              float nv;
+              lloydmax3_encode_row<D>(y, cb, lane, w, nv);
+              if (lane < C::WORDS) {
+                bstore32(w, vc, nrow * (uint32_t)(C::WORDS * 4) + lane * 4u);
+                reinterpret_cast<uint32_t*>(nn + C::NEW_V)[lane] = w;
+              }
+              if (lane < C::NB) {
+                bstore32(__builtin_bit_cast(uint32_t, nv), vs, nrow * (uint32_t)(C::NB * 4) + lane * 4u);
+                reinterpret_cast<float*>(nn + C::NEW_VS)[lane] = nv;
+              }
             }
           }
         }
@@ -989,7 +1036,7 @@ static int plan_wg_per_head(int num_kv_heads, int resident_per_cu) {
 template <int D, bool K8V3, bool FUSE>
 static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
-  constexpr int kNewBytes = FUSE ? 6 * D + 16 : 0;  // fused append: fp16 K and V rows, int8 K and V rows, scales
+  constexpr int kNewBytes = FUSE ? C::NEW_BYTES : 0;  // fused append: the new token's rows
   const auto smem_main_for = [](int group) {
     const int merge = kDecWaves * (group * D + 32) * 4;
     return ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
@@ -1099,7 +1146,13 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   a.ws_desc = reinterpret_cast<int*>(a.ws_acc + partials * head_dim);
   hipStream_t s = (hipStream_t)stream;
   if (fuse) {
-    if (k8v3) return S8KV_ERR_UNSUPPORTED;
+    if (k8v3) {
+      switch (head_dim) {
+        case 128: return launch_decode<128, true, true>(a, s);
+        case 256: return launch_decode<256, true, true>(a, s);
+      }
+      return S8KV_ERR_UNSUPPORTED;
+    }
     switch (head_dim) {
       case 32: return launch_decode<32, false, true>(a, s);
       case 64: return launch_decode<64, false, true>(a, s);
@@ -1199,6 +1252,36 @@ extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads
   a.vn_stride_b = v_new_stride_b;
   a.vn_stride_h = v_new_stride_h;
   return decode_common(a, false, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                                       int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                                       int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int32_t* v_packed,
+                                       float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                       int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                       const int32_t* context_lens, int max_context_len, float scale, void* out,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "decode_append_k8v3: lloyd_block %d != 128", lloyd_block);
+  S8KV_REQUIRE(v_codebook != nullptr, S8KV_ERR_INVALID, "decode_append_k8v3: null codebook");
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_packed; a.v_scale = v_norm;
+  a.v_codebook = v_codebook;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  a.k_new = (const _Float16*)k_new;
+  a.v_new = (const _Float16*)v_new;
+  a.kn_stride_b = k_new_stride_b;
+  a.kn_stride_h = k_new_stride_h;
+  a.vn_stride_b = v_new_stride_b;
+  a.vn_stride_h = v_new_stride_h;
+  return decode_common(a, true, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, scale, workspace, workspace_bytes, stream);
 }
 

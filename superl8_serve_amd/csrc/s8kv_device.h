@@ -220,6 +220,69 @@ __device__ __forceinline__ float rtn_row(const float (&y)[RowLayout<D>::E], int 
   return scale;
 }
 
+// 3-bit Lloyd-Max encoding of one V row spread over the wave (RowLayout
+// lanes; head_dim 128 or 256, lloyd_block 128): per-128 block L2 norm (fp32
+// squares, fold the two halves, then butterflies 32..1, correctly rounded
+// sqrt), u = v / norm (0 for a zero norm), code = first index minimising
+// |u - c_j| in fp32, bit-plane words (word 3g+b holds bit b of the codes of
+// elements 32g..32g+31, element 32g+i at bit i).  Lane w < 3D/32 gets word w,
+// lane nb < D/128 gets norm nb.
+template <int D>
+__device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<D>::E], const float (&cb)[8], int lane,
+                                                      uint32_t& word_out, float& norm_out) {
+  constexpr int E = RowLayout<D>::E;
+  constexpr int NB = D / 128;
+  constexpr int WORDS = D / 32 * 3;
+  float norm[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    // Block nb holds elements 128nb + {lane, lane+64}: fold the halves, then
+    // butterflies 32..1 -- the order the CPU restatement uses.
+    float s = x[2 * nb] * x[2 * nb] + x[2 * nb + 1] * x[2 * nb + 1];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s = s + shfl_xor_f(s, m);
+    norm[nb] = __builtin_sqrtf(s);
+  }
+  uint32_t codes[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const float nrm = norm[j / 2];
+    const float u = nrm > 0.0f ? x[j] / nrm : 0.0f;
+    float best = fabsf(u - cb[0]);
+    uint32_t c = 0;
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      float d = fabsf(u - cb[i]);
+      if (d < best) {
+        best = d;
+        c = (uint32_t)i;
+      }
+    }
+    codes[j] = c;
+  }
+  // Bit-plane packing: element group g (32 elements) -> words 3g+b, bit i of
+  // word 3g+b = bit b of the code of element 32g+i.  Slot j of lanes 0..31
+  // is group 2j, of lanes 32..63 group 2j+1.
+  uint32_t words[WORDS];
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      uint64_t m = __ballot((codes[j] >> b) & 1u);
+      words[3 * (2 * j) + b] = (uint32_t)m;
+      words[3 * (2 * j + 1) + b] = (uint32_t)(m >> 32);
+    }
+  }
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < WORDS; ++i) w = (lane == i) ? words[i] : w;
+  float nv = norm[0];
+#pragma unroll
+  for (int nb = 1; nb < NB; ++nb) nv = (lane == nb) ? norm[nb] : nv;
+  word_out = w;
+  norm_out = nv;
+}
+
 // Spread the low 4 bits of x into bit 0 of each byte.
 __device__ __forceinline__ uint32_t spread4(uint32_t x) {
   return ((x & 0xFu) * 0x00204081u) & 0x01010101u;

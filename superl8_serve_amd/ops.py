@@ -24,6 +24,7 @@ __all__ = [
     "attn_paged_decode_cached",
     "attn_paged_decode_k8v3",
     "attn_paged_decode_append",
+    "attn_paged_decode_append_k8v3",
     "decode_workspace_bytes",
     "attn_paged_verify",
     "copy_blocks",
@@ -249,6 +250,47 @@ def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
     _lib.check(rc, "attn_paged_decode_append")
+    return out
+
+
+def attn_paged_decode_append_k8v3(q, k_new, v_new, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table,
+                                  context_lens, block_size, *, max_context_len, scale, lloyd_block: int = 128):
+    """``attn_paged_decode_append`` for the K8V3 layout: row b's new token is
+    written at position ``context_lens[b] - 1`` exactly as
+    ``quantize_kv_write_paged_k8v3`` writes it (int8 K; 3-bit Lloyd-Max V
+    words and block norms), then the row attends as ``attn_paged_decode_k8v3``
+    does -- one launch for the pair the reference runs as its K8V3 write
+    (kv_cache.py:587-626) and ``decode_attn_static`` (kv_cache.py:1167-1182)."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_new", k_new, torch.float16, dev)
+    _on_gpu("v_new", v_new, torch.float16, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_packed", v_packed, torch.int32, dev)
+    _on_gpu("v_norm", v_norm, torch.float32, dev)
+    _on_gpu("v_codebook", v_codebook, torch.float32, dev)
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_packed.shape) == (n, hkv, bs, d * 3 // 32) and v_packed.is_contiguous(),
+             "v_packed must be [N, Hkv, bs, D*3/32]")
+    _require(tuple(v_norm.shape) == (n, hkv, bs, d // lloyd_block) and v_norm.is_contiguous(),
+             "v_norm must be [N, Hkv, bs, D/lloyd_block]")
+    _require(v_codebook.numel() == 8 and v_codebook.is_contiguous(), "v_codebook must hold 8 contiguous entries")
+    k_new = _tokens_view(k_new, "k_new", hkv, d)
+    v_new = _tokens_view(v_new, "v_new", hkv, d)
+    _require(k_new.shape[0] == b and v_new.shape[0] == b, f"k_new and v_new must be [{b}, {hkv}, {d}]")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_append_k8v3(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_new.data_ptr(), k_new.stride(0), k_new.stride(1), v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
+        lloyd_block, n, bs, bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_append_k8v3")
     return out
 
 

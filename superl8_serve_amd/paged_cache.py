@@ -407,15 +407,17 @@ class PagedKVCache:
     def decode_step_static(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                            block_table: torch.Tensor, context_lens: torch.Tensor, max_context_len: int, *,
                            scale: float) -> torch.Tensor:
-        """``write_decode_static`` + ``decode_attn_static`` in one launch for the
-        int8 layout: row b's new token goes to position ``context_lens[b] - 1``
+        """``write_decode_static`` + ``decode_attn_static`` in one launch (int8
+        and K8V3 layouts): row b's new token goes to position ``context_lens[b] - 1``
         of its block table (where the reference's decode step writes it,
         kv_cache.py:1083-1093 with 1129-1146), then the row attends.  Same
         cache bytes and output as the two calls."""
-        if self.v_quant != "int8":
-            self.write_decode_static(layer, self._slot_mapping_from_table(block_table, context_lens), k_new, v_new)
-            return self.decode_attn_static(layer, q, block_table, context_lens, max_context_len, scale=scale)
         row = self._layer_row(layer)
+        if self.v_quant == "lloydmax3":
+            return ops.attn_paged_decode_append_k8v3(
+                q, k_new, v_new, self.k_cache[row], self.k_scale[row], self.v_packed[row], self.v_norm[row],
+                self.v_codebook[row], block_table, context_lens, self.block_size, max_context_len=max_context_len,
+                scale=scale)
         return ops.attn_paged_decode_append(q, k_new, v_new, self.k_cache[row], self.k_scale[row],
                                             self.v_cache[row], self.v_scale[row], block_table, context_lens,
                                             self.block_size, max_context_len=max_context_len, scale=scale)
@@ -428,14 +430,6 @@ class PagedKVCache:
         return self.decode_step_static(layer, q, k_new, v_new, self.block_table(slots),
                                        torch.tensor(ctx, dtype=torch.int32, device=self.device),
                                        max(ctx) if ctx else 0, scale=scale)
-
-    def _slot_mapping_from_table(self, block_table: torch.Tensor, context_lens: torch.Tensor) -> torch.Tensor:
-        """Flat slot of position ``context_lens[b] - 1`` of every row (-1 for
-        empty rows), computed on the device."""
-        pos = context_lens.to(torch.int64) - 1
-        blk = torch.gather(block_table.to(torch.int64), 1, (pos.clamp(min=0) // self.block_size)[:, None])[:, 0]
-        return torch.where(pos >= 0, blk * self.block_size + pos.clamp(min=0) % self.block_size,
-                           torch.full_like(pos, -1)).to(torch.int32)
 
     def verify_attn(self, layer: int, q: torch.Tensor, slots: list[int], prefix_lens: list[int], *, scale: float,
                     query_lens: list[int] | None = None, tree_mask: torch.Tensor | None = None) -> torch.Tensor:

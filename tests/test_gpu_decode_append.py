@@ -14,7 +14,7 @@ import torch
 
 from oracle import kv_oracle as O
 from superl8_serve_amd import ops
-from tests.kvcase import empty_int8_cache, make_case
+from tests.kvcase import empty_int8_cache, empty_k8v3_cache, make_case
 
 pytestmark = pytest.mark.gpu
 
@@ -156,3 +156,61 @@ def test_decode_append_graph_replays():
         assert np.array_equal(_np(out.float())[:, :, 0, :], eager)
     for a, b in zip((kc, ks, vc, vs), full):
         assert np.array_equal(_np(a).view(np.uint8), b.view(np.uint8))
+
+
+# ---------------------------------------------------------------------------
+# K8V3 layout (int8 K, 3-bit Lloyd-Max V)
+# ---------------------------------------------------------------------------
+
+CODEBOOK = O.gaussian_codebook(3, 128)
+
+
+def _split_k8v3(case):
+    ends = np.cumsum(case.lens)
+    last = ends - 1
+    has = case.lens > 0
+    keep = np.ones(int(ends[-1]) if len(ends) else 0, bool)
+    keep[last[has]] = False
+    pre = empty_k8v3_cache(case)
+    O.k8v3_write_paged(case.k[keep], case.v[keep], *pre, CODEBOOK, case.slots[keep])
+    full = empty_k8v3_cache(case)
+    O.k8v3_write_paged(case.k, case.v, *full, CODEBOOK, case.slots)
+    k_new = np.zeros((case.batch, case.num_kv_heads, case.head_dim), np.float16)
+    v_new = np.zeros_like(k_new)
+    k_new[has] = case.k[last[has]]
+    v_new[has] = case.v[last[has]]
+    slots = np.where(has, case.slots[np.minimum(last, len(case.slots) - 1)], -1).astype(np.int32)
+    return pre, full, k_new, v_new, slots
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,lens", [
+    (32, 8, 128, 256, "long"),                       # Qwen3-8B heads, 8k-32k-like rows (shortened)
+    (16, 8, 128, 16, [100, 17, 16, 15, 1, 0]),
+    (8, 2, 256, 16, [50, 129, 300]),                 # two Lloyd-Max blocks per row
+])
+def test_decode_append_k8v3_matches_append_then_decode(hq, hkv, d, bs, lens):
+    if lens == "long":
+        lens = np.random.default_rng(4).integers(1500, 6000, size=8).tolist()
+    case = make_case(3000 + hq + d + bs, len(lens), hq, hkv, d, bs, lens, outlier_channels=2 if d == 128 else 0)
+    max_ctx = int(case.lens.max())
+    pre, full, k_new, v_new, slots = _split_k8v3(case)
+    cb = _t(CODEBOOK)
+    q = _t(case.q)[:, :, None, :]
+    bt, cl = _t(case.block_table), _t(case.lens.astype(np.int32))
+    kc, ks, vp, vn = (_t(x) for x in pre)
+    got = ops.attn_paged_decode_append_k8v3(q, _t(k_new), _t(v_new), kc, ks, vp, vn, cb, bt, cl, case.block_size,
+                                            max_context_len=max_ctx, scale=case.scale)
+    torch.cuda.synchronize()
+    for a, b, name in zip((kc, ks, vp, vn), full, ("k_cache", "k_scale", "v_packed", "v_norm")):
+        assert np.array_equal(_np(a).view(np.uint8), b.view(np.uint8)), f"{name} differs from the oracle's append"
+    got = _np(got.float())[:, :, 0, :]
+    layer = O.LayerCache(*full[:2], v_packed=full[2], v_norm=full[3], v_codebook=CODEBOOK)
+    ref = O.paged_decode(case.q, layer, case.block_table, case.lens, case.scale)
+    mx, rel = O.attention_errors(got, ref)
+    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"k8v3 fused: max err {mx:.3e}, rel rms {rel:.3e}"
+    kc2, ks2, vp2, vn2 = (_t(x) for x in pre)
+    ops.quantize_kv_write_paged_k8v3(_t(k_new), _t(v_new), kc2, ks2, vp2, vn2, cb, _t(slots))
+    sep = ops.attn_paged_decode_k8v3(q, kc2, ks2, vp2, vn2, cb, bt, cl, case.block_size, max_context_len=max_ctx,
+                                     scale=case.scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, _np(sep.float())[:, :, 0, :]), "k8v3 fused differs from append + decode"
