@@ -509,7 +509,9 @@ def run_copy(steps: int) -> None:
     t = [torch.randint(-127, 128, (1, n, HKV, BS, D), dtype=torch.int8, device="cuda") for _ in range(2)]
     t += [torch.rand((1, n, HKV, BS), device="cuda") for _ in range(2)]
     perm = rng.permutation(n)
-    src, dst = perm[:1024].tolist(), perm[1024:2048].tolist()
+    # block ids already on the device, as a serving loop hands them over
+    src = torch.tensor(perm[:1024], dtype=torch.int32, device="cuda")
+    dst = torch.tensor(perm[1024:2048], dtype=torch.int32, device="cuda")
     ops.copy_blocks(t, src, dst)
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -1,6 +1,9 @@
 // Whole-block copy across every layer of the cache tensors (copy-on-write of a
 // shared prefix block, pool compaction).  Pure HBM streaming: each workgroup
-// moves one 4 KiB chunk of one (tensor, block pair, layer) with 16-byte loads.
+// moves one 8 KiB chunk of one (tensor, block pair, layer); every thread
+// issues its two 16-byte loads (4 KiB apart, so each instruction is one
+// contiguous 4 KiB span per workgroup) before its two non-temporal stores.
+// Two loads in flight per thread measured fastest (1, 4 and 8 are slower).
 #include "s8kv_device.h"
 #include "s8kv_host.h"
 
@@ -8,13 +11,16 @@ namespace s8kv {
 
 constexpr int kMaxCopyTensors = 8;
 constexpr int kCopyThreads = 256;
-constexpr int kCopyChunk = kCopyThreads * 16;
+constexpr int kCopyUnroll = 2;
+constexpr int kCopyStep = kCopyThreads * 16;            // bytes per load instruction of the workgroup
+constexpr int kCopyChunk = kCopyStep * kCopyUnroll;     // bytes per workgroup
 
 struct CopyArgs {
   char* base[kMaxCopyTensors];
   int64_t block_bytes[kMaxCopyTensors];
   int64_t layer_stride[kMaxCopyTensors];
   int chunk_begin[kMaxCopyTensors + 1];  // prefix sum of chunks per tensor
+  int vec16[kMaxCopyTensors];            // base, layer stride and block bytes all 16-byte aligned
   int num_tensors;
   int64_t num_blocks;
   const int32_t* src;
@@ -31,15 +37,28 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(CopyArgs a) {
   const int32_t db = a.dst[pair];
   if (sb < 0 || db < 0 || sb >= a.num_blocks || db >= a.num_blocks) return;
   const int64_t bb = a.block_bytes[t];
-  const int64_t off = (int64_t)(chunk_id - a.chunk_begin[t]) * kCopyChunk + (int64_t)threadIdx.x * 16;
-  if (off >= bb) return;
-  const char* s = a.base[t] + layer * a.layer_stride[t] + (int64_t)sb * bb + off;
-  char* d = a.base[t] + layer * a.layer_stride[t] + (int64_t)db * bb + off;
-  if ((bb & 15) == 0) {  // 16-byte aligned blocks: one vector move per thread
-    *reinterpret_cast<u32x4_t*>(d) = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(s));
+  const int64_t off0 = (int64_t)(chunk_id - a.chunk_begin[t]) * kCopyChunk + (int64_t)threadIdx.x * 16;
+  if (off0 >= bb) return;
+  const char* s = a.base[t] + layer * a.layer_stride[t] + (int64_t)sb * bb;
+  char* d = a.base[t] + layer * a.layer_stride[t] + (int64_t)db * bb;
+  if (a.vec16[t]) {  // 16-byte aligned blocks: vector moves, all loads in flight first
+    u32x4_t v[kCopyUnroll];
+#pragma unroll
+    for (int i = 0; i < kCopyUnroll; ++i) {
+      const int64_t off = off0 + (int64_t)i * kCopyStep;
+      if (off < bb) v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(s + off));
+    }
+#pragma unroll
+    for (int i = 0; i < kCopyUnroll; ++i) {
+      const int64_t off = off0 + (int64_t)i * kCopyStep;
+      if (off < bb) __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4_t*>(d + off));
+    }
   } else {
-    for (int64_t i = 0; i < 16 && i + 4 <= bb - off; i += 4)
-      *reinterpret_cast<uint32_t*>(d + i) = *reinterpret_cast<const uint32_t*>(s + i);
+    for (int i = 0; i < kCopyUnroll; ++i) {
+      const int64_t off = off0 + (int64_t)i * kCopyStep;
+      for (int64_t k = 0; k < 16 && off + k + 4 <= bb; k += 4)
+        *reinterpret_cast<uint32_t*>(d + off + k) = *reinterpret_cast<const uint32_t*>(s + off + k);
+    }
   }
 }
 
@@ -73,6 +92,8 @@ extern "C" int s8kv_copy_blocks(int num_tensors, void* const* tensor_ptrs, const
     a.base[i] = (char*)tensor_ptrs[i];
     a.block_bytes[i] = block_bytes[i];
     a.layer_stride[i] = layer_stride_bytes[i];
+    a.vec16[i] = ((reinterpret_cast<uintptr_t>(tensor_ptrs[i]) | (uintptr_t)layer_stride_bytes[i] |
+                   (uintptr_t)block_bytes[i]) & 15) == 0;
     a.chunk_begin[i] = chunks;
     chunks += (int)((block_bytes[i] + kCopyChunk - 1) / kCopyChunk);
   }

@@ -323,6 +323,28 @@ def test_copy_blocks_odd_block_bytes():
     assert np.array_equal(_np(g), x)
 
 
+def test_copy_blocks_multi_chunk_and_unaligned_base():
+    """10,560-byte blocks (two workgroup chunks, the second partial), once in
+    a 16-byte aligned tensor (vector path) and once in a contiguous view that
+    starts 4 bytes into its storage (word path)."""
+    rng = np.random.default_rng(7)
+    shape = (2, 7, 5, 33, 64)
+    x = rng.integers(-128, 128, shape).astype(np.int8)
+    src, dst = [6, 1, 3], [0, 5, 2]
+    ref = x.copy()
+    O.copy_blocks([ref], src, dst)
+    g = _t(x)
+    ops.copy_blocks([g], src, dst)
+    assert np.array_equal(_np(g), ref)
+    buf = torch.zeros(x.size + 4, dtype=torch.int8, device=DEV)
+    v = buf[4:].view(shape)
+    assert v.is_contiguous() and v.data_ptr() % 16 == 4
+    v.copy_(torch.from_numpy(x).to(DEV))
+    ops.copy_blocks([v], src, dst)
+    assert np.array_equal(_np(v), ref)
+    assert int(buf[:4].abs().sum()) == 0
+
+
 # ---------------------------------------------------------------------------
 # HIP graph capture
 # ---------------------------------------------------------------------------
