@@ -155,9 +155,10 @@ def make_step(w, fused: bool):
 
 
 def time_decode_kernel(w, reps: int, fused: bool) -> dict:
-    """Average durations of the decode attention kernel and of its merge
-    kernel, from HIP events the library records on the launch stream around
-    each kernel (s8kv_timing_begin/end), over `reps` eager passes of the 36
+    """Average duration of the decode attention kernel (which also combines
+    the partials of rows split across workgroups), from HIP events the library
+    records on the launch stream around each launch (s8kv_timing_begin/end),
+    over `reps` eager passes of the 36
     decode calls (the one-launch step when `fused`: its append rewrites the
     same bytes).  A preceding spin kernel keeps the GPU ahead of the host so
     host launch latency never enters an interval."""
@@ -185,7 +186,7 @@ def time_decode_kernel(w, reps: int, fused: bool) -> dict:
     _lib.check(lib.s8kv_timing_end(ctypes.byref(n), ctypes.byref(dk), ctypes.byref(mk)), "s8kv_timing_end")
     torch.cuda.synchronize()
     launches = max(n.value, 1)
-    return {"decode_s": dk.value * 1e-3 / launches, "merge_s": mk.value * 1e-3 / launches, "launches": n.value}
+    return {"decode_s": dk.value * 1e-3 / launches, "launches": n.value}
 
 
 def cpu_baseline(lens: np.ndarray, bt_np: np.ndarray, layers: int) -> dict:
@@ -535,7 +536,8 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=NUM_LAYERS, help="layers in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
-    ap.add_argument("--kernel-reps", type=int, default=3, help="event-timed decode passes over the 36 layers")
+    ap.add_argument("--kernel-reps", type=int, default=3,
+                    help="eager event-timed decode passes over the 36 layers (0 = skip, one-launch step only)")
     ap.add_argument("--separate-append", action="store_true",
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
@@ -587,19 +589,32 @@ def main():
     for _ in range(args.warmup):
         graph.replay()
     torch.cuda.synchronize()
+    # HIP events on the replay stream bracket the timed replays as well
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record()
     for _ in range(args.steps):
         graph.replay()
+    ev1.record()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt / max(args.steps, 1) * 1e3
+    ev_launch_s = ev0.elapsed_time(ev1) * 1e-3 / (max(args.steps, 1) * NUM_LAYERS)
 
     b = step_bytes(w["lens"])
     value = b["step"] / (ms * 1e-3) / 1e9
-    kt = time_decode_kernel(w, args.kernel_reps, fused)
-    dec_s = kt["decode_s"]
+    # eager per-launch timing: required for the two-call step, a cross-check otherwise
+    kt = (time_decode_kernel(w, args.kernel_reps, fused) if args.kernel_reps > 0 or not fused
+          else {"decode_s": None, "launches": 0})
     kernel = "decode_kernel<128, int8, fused append>" if fused else "decode_kernel<128, int8>"
     kernel_bytes = b["fused_layer"] if fused else b["decode_layer"]
+    # The one-launch step graph holds exactly NUM_LAYERS decode_kernel launches
+    # and nothing else, so the events around the timed replays give the
+    # kernel's average launch duration over the timed region (gaps between the
+    # back-to-back launches included).  The two-call step also runs the append
+    # kernel, so there the library's per-launch events over eager passes time
+    # the decode kernel alone.
+    dec_s = ev_launch_s if fused else kt["decode_s"]
     achieved = kernel_bytes / dec_s / 1e9
     traffic = None
     if args.traffic_json and os.path.exists(args.traffic_json):
@@ -635,7 +650,10 @@ def main():
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "avg_launch_us": round(dec_s * 1e6, 2), "algorithmic_bytes_per_launch": kernel_bytes,
-            "merge_kernel_avg_us": round(kt["merge_s"] * 1e6, 2), "timed_launches": kt["launches"],
+            "avg_launch_from": ("HIP events around the timed graph replays / launches" if fused
+                                else "library HIP events per eager launch"),
+            "timed_launches": args.steps * NUM_LAYERS if fused else kt["launches"],
+            "eager_avg_launch_us": round(kt["decode_s"] * 1e6, 2) if kt["decode_s"] else None,
         },
     }
     if args.cpu_layers > 0:

@@ -71,9 +71,11 @@ int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens, int num_k
 /*
  * Bytes of scratch device memory the decode entry points need for this
  * geometry on the current device (partial softmax states of rows split across
- * workgroups).  Depends only on its arguments and the device's compute-unit
- * count, so a caller can size the workspace once per graph bucket;
- * max_context_len does not change it.  The workspace needs no initialisation
+ * workgroups, and one 8-byte arrival counter per (KV head, row)).  Depends
+ * only on its arguments and the device's compute-unit count, so a caller can
+ * size the workspace once per graph bucket; max_context_len does not change
+ * it.  The workspace must be 8-byte aligned; it needs no initialisation (each
+ * launch tags its counters, and the last arrival of a row clears its word),
  * and calls that overlap on one workspace race.
  */
 int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -93,7 +95,7 @@ int64_t s8kv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
  * ceil(context_lens[b]/block_size) entries.  context_lens: int32 [batch].
  * max_context_len >= max(context_lens) bounds the block-table width read; a
  * row whose context_lens entry exceeds it is truncated to max_context_len
- * tokens.  A row with context length 0 yields zeros.
+ * tokens.  A row with context length 0 yields zeros.  max_context_len < 2^28.
  * out: fp16 [batch, num_q_heads, head_dim] contiguous.
  * Row b, head h attends tokens [0, context_lens[b]) of KV head
  * h / (num_q_heads / num_kv_heads) with softmax scale `scale`, applying the
@@ -193,10 +195,10 @@ int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads
 /*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
- * graph capture launches its two kernels with HIP events stamped with each
+ * graph capture launches its kernel with HIP events stamped with the
  * kernel's start and end; s8kv_timing_end() waits for them and returns the
- * number of decode calls and the summed durations (ms) of the attention
- * kernel and of the merge kernel.
+ * number of decode calls and the summed kernel durations (ms).  merge_ms is
+ * always 0: rows split across workgroups are combined inside the kernel.
  * Used by the benchmark to time the attention kernel on its own stream.
  */
 int s8kv_timing_begin(void);

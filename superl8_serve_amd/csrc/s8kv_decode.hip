@@ -7,7 +7,8 @@
 // never leave part of the GPU idle.  A slice may end inside one row and start
 // the next; the part of a row inside one slice is a "segment".  A row covered
 // by a single segment is written directly, otherwise every segment writes a
-// (max, sum, acc) partial and merge_kernel combines them.  Each row also
+// (max, sum, acc) partial and the workgroup whose segment completes the row
+// (see "Arrival counters" below) combines them.  Each row also
 // occupies `ghost` stream tokens that are not processed: they charge the fixed
 // cost of a segment (q set-up, merge) to the slice that holds it.  A
 // segment's set-up loads (q, first block ids) are issued before the previous
@@ -31,10 +32,25 @@
 //         with the gfx950 transpose reads ds_read_b64_tr_b8 (int8) /
 //         ds_read_b64_tr_b16 (K8V3 codes expanded to fp16 in LDS).
 // The next tile's loads are issued while the current one computes.
-// (Combining partials in the last-arriving workgroup would need agent-scope
-// release/acquire fences, which on this multi-XCD part write back and
-// invalidate the whole L2 per workgroup -- far costlier than a second launch.)
+//
+// Arrival counters: the partials of a split row are stored with agent-scope
+// (L2-bypassing, `sc1`) stores; after every wave has waited for its stores,
+// one lane adds the segment's length to the row's counter word with an
+// agent-scope compare-and-swap, and the workgroup that brings the count to the
+// row's padded length reads the partials back with agent-scope loads and
+// writes the row.  Only the data exchanged goes through the coherence point:
+// agent-scope release/acquire fences would write back and invalidate the
+// whole L2 of the XCD instead.  A counter word holds a 40-bit tag of the
+// launch and a 24-bit count of 32-token units; a word whose tag is not this
+// launch's counts as zero, so the workspace needs no initialisation (a stale
+// word matches a launch's tag with probability 2^-40), and the last arrival
+// writes the word back to zero, so a graph replaying the launch with the same
+// tag starts from zero too.
 #include <stdlib.h>
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
 
 #include <array>
 #include <type_traits>
@@ -108,7 +124,8 @@ struct DecodeArgs {
   _Float16* out;
   float* ws_ml;         // [Hkv][slots][G][2]  (max, sum) of each segment
   float* ws_acc;        // [Hkv][slots][G][D]  unnormalized output of each segment
-  int* ws_desc;         // [batch][2]  first and last slice of each split row, -1 if not split
+  unsigned long long* ws_cnt;  // [Hkv][batch] arrival counters: tag << 24 | 32-token units done
+  unsigned long long tag;      // this launch's 40-bit tag (non-zero)
   // fused append (decode_kernel<D, false, true>): row b's new token, at position
   // context_lens[b] - 1, is quantized and written by the workgroup that holds
   // the row's last tile, which attends over it from registers
@@ -142,7 +159,14 @@ __device__ __forceinline__ float slot_weight(int c, int classes, int skew_permil
 }
 // The slice layout is computed across lanes, lane c describing class c (at
 // most 8 classes): every wave of every workgroup computes it, and scalar code
-// doing the same would queue on the CU's one scalar unit.
+// doing the same would queue on the CU's one scalar unit.  Its cross-lane
+// steps are swizzles and DPP row shifts, which need no lane-address
+// registers, so the copy recomputed for a merge shares nothing with the
+// prologue's.
+template <int M>
+__device__ __forceinline__ float swz_xor_f(float v) {  // lane ^ M, M < 32 (ds_swizzle bit mode)
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (M << 10)));
+}
 struct SliceLayout {
   int f0, f1;   // lane c: workgroups [f0, f1) are in class c (f0 = f1 = W past the last class)
   int sz;       // lane c: slice length of class c
@@ -156,19 +180,17 @@ __device__ __forceinline__ SliceLayout slice_layout(int total, int W, int ncls, 
   s.f1 = act ? slot_first(lane + 1, W, classes) : W;
   const float wt = act ? slot_weight(lane, classes, skew_permille) : 0.0f;
   float ws = (float)(s.f1 - s.f0) * wt;  // lanes 0..7 sum in a fixed tree order
-  ws += shfl_xor_f(ws, 1);
-  ws += shfl_xor_f(ws, 2);
-  ws += shfl_xor_f(ws, 4);
+  ws += swz_xor_f<1>(ws);
+  ws += swz_xor_f<2>(ws);
+  ws += swz_xor_f<4>(ws);
   const float wsum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), 0));
   const float unit = (float)total / wsum;
   s.sz = act ? max(kTile, padded32((int)ceilf(unit * wt))) : 0;
   const int span = (s.f1 - s.f0) * s.sz;
-  int incl = span;
-#pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
-    const int t = __shfl_up(incl, off);
-    if (lane >= off) incl += t;
-  }
+  int incl = span;  // inclusive scan over lanes 0..7 (DPP row_shr: lanes below `off` read 0)
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, false);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, false);
   s.start = incl - span;
   return s;
 }
@@ -177,6 +199,38 @@ __device__ __forceinline__ int slice_start(const SliceLayout& s, int j) {
   const uint64_t m = __builtin_amdgcn_ballot_w64(s.f0 <= j && j < s.f1);
   const int cl = m ? (int)__builtin_ctzll(m) : 0;
   return __builtin_amdgcn_readlane(s.start + (j - s.f0) * s.sz, cl);
+}
+// The workgroup whose slice holds stream position p (0 <= p < stream total):
+// the largest j with slice_start(j) <= p.  Class starts increase with the
+// class and the class spans cover the stream, so the last class starting at
+// or before p holds it.
+__device__ __forceinline__ int slice_of(const SliceLayout& s, int p) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(s.f0 < s.f1 && s.start <= p);
+  const int cl = m ? 63 - (int)__builtin_clzll(m) : 0;
+  const int k = min((p - s.start) / max(s.sz, 1), s.f1 - s.f0 - 1);
+  return __builtin_amdgcn_readlane(s.f0 + k, cl);
+}
+
+// One segment of a split row has stored its partial: add its `units` (32-token
+// units) to the row's counter word; true for the arrival that completes the
+// row's `total` units, which also writes the word back to zero.  Every failed
+// exchange means another segment's add went in, so the loop ends.
+__device__ __forceinline__ bool arrive(unsigned long long* cp, unsigned long long tag, uint32_t units, uint32_t total) {
+  unsigned long long old = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const uint32_t done = (old >> 24) == tag ? (uint32_t)(old & 0xFFFFFFu) : 0u;
+    const uint32_t now = done + units;
+    const unsigned long long nw = now == total ? 0ull : (tag << 24) | now;
+    if (__hip_atomic_compare_exchange_weak(cp, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT))
+      return now == total;
+  }
+}
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -272,7 +326,6 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       if (lens_at(a, lens_lds, b) == 0) {
         for (int i = tid; i < G * D; i += 64 * kDecWaves)
           a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
-        if (h == 0 && tid == 0) a.ws_desc[2 * b] = -1;
       }
   }
   const SliceLayout sl = slice_layout(total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
@@ -889,17 +942,6 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     __syncthreads();
     store_prefetched_bt();  // bt_lds is free: every wave left its tile loop
     const int64_t slot = ((int64_t)h * a.slots + (j + b)) * G;  // (row, slice) -> unique slot j + b
-    // the merge kernel learns the slices of a split row from these: first and
-    // last slice, or -1 for a row finished here (stream positions are the same
-    // for every head, so head 0 writes them)
-    if (h == 0 && tid == 0) {
-      if (whole_row) {
-        a.ws_desc[2 * b] = -1;
-      } else {
-        if (s0 == 0) a.ws_desc[2 * b] = j;
-        if (s1 == padL) a.ws_desc[2 * b + 1] = j;
-      }
-    }
     for (int i = tid; i < G * D; i += 64 * kDecWaves) {
       const int cc = i / D, d = i - cc * D;
       float M = kNegInf;
@@ -917,10 +959,58 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       if (whole_row) {
         a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
       } else {
-        a.ws_acc[(slot + cc) * D + d] = num;
+        store_agent(&a.ws_acc[(slot + cc) * D + d], num);
         if (d == 0) {
-          a.ws_ml[(slot + cc) * 2] = M;
-          a.ws_ml[(slot + cc) * 2 + 1] = den;
+          store_agent(&a.ws_ml[(slot + cc) * 2], M);
+          store_agent(&a.ws_ml[(slot + cc) * 2 + 1], den);
+        }
+      }
+    }
+    if (!whole_row) {
+      // ---- arrival: the segment completing the row combines its partials ----
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have reached the coherence point
+      __syncthreads();
+      __shared__ int completes_row;
+      if (tid == 0)
+        completes_row = arrive(a.ws_cnt + (int64_t)h * a.batch + b, a.tag, (uint32_t)(s1 - s0) >> 5,
+                               (uint32_t)padL >> 5);
+      __syncthreads();
+      if (completes_row) {
+        // slices jf..jl hold the row's segments; their partials are at slots j + b
+        // (recomputed here from opaque copies of its inputs, so that no part of
+        // it is hoisted from the prologue and kept live across the tile loop)
+        const SliceLayout sm = slice_layout(opaque_int(total), opaque_int(a.wg_per_head), opaque_int(a.slot_classes),
+                                            opaque_int(a.slot_skew), opaque_int(threadIdx.x) & 63);
+        const int jf = slice_of(sm, rs);
+        const int jl = slice_of(sm, rs + padL - 1);
+        for (int i = tid; i < G * D; i += 64 * kDecWaves) {
+          const int cc = i / D, d = i - cc * D;
+          float M = kNegInf, num = 0.0f, den = 0.0f;
+          for (int j0 = jf; j0 <= jl; j0 += 4) {  // four partials' loads in flight at a time
+            float ms[4], ls[4], xs[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int jj = min(j0 + u, jl);
+              const int64_t pi = ((int64_t)h * a.slots + jj + b) * G + cc;
+              ms[u] = j0 + u <= jl ? load_agent(&a.ws_ml[pi * 2]) : kNegInf;
+              ls[u] = load_agent(&a.ws_ml[pi * 2 + 1]);
+              xs[u] = load_agent(&a.ws_acc[pi * D + d]);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              if (ms[u] == kNegInf) continue;  // past jl, or a segment that saw no token
+              if (ms[u] > M) {
+                const float f = __builtin_amdgcn_exp2f(M - ms[u]);  // 0 while M = -inf
+                num *= f;
+                den *= f;
+                M = ms[u];
+              }
+              const float f = __builtin_amdgcn_exp2f(ms[u] - M);
+              num += f * xs[u];
+              den += f * ls[u];
+            }
+          }
+          a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
         }
       }
     }
@@ -932,59 +1022,16 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   }
 }
 
-// Combine the segments of (row b, KV head h): decode_kernel recorded the
-// first and last slice of every split row (-1 for rows it finished); the
-// partials of slices j_first..j_last are at slots j + b and are read four at a
-// time.
-template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int jf = a.ws_desc[2 * b];
-  if (jf < 0) return;
-  const int jl = a.ws_desc[2 * b + 1];
-  const int G = a.group;
-  for (int i = threadIdx.x; i < G * D; i += 256) {
-    const int cc = i / D, d = i - cc * D;
-    float M = kNegInf, num = 0.0f, den = 0.0f;
-    for (int j0 = jf; j0 <= jl; j0 += 4) {
-      float ms[4], ls[4], xs[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int jj = min(j0 + u, jl);
-        const int64_t pi = ((int64_t)h * a.slots + jj + b) * G + cc;
-        ms[u] = j0 + u <= jl ? a.ws_ml[pi * 2] : kNegInf;
-        ls[u] = a.ws_ml[pi * 2 + 1];
-        xs[u] = a.ws_acc[pi * D + d];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (ms[u] == kNegInf) continue;  // past jl, or a segment that saw no token
-        if (ms[u] > M) {
-          const float f = __builtin_amdgcn_exp2f(M - ms[u]);  // 0 while M = -inf
-          num *= f;
-          den *= f;
-          M = ms[u];
-        }
-        const float f = __builtin_amdgcn_exp2f(ms[u] - M);
-        num += f * xs[u];
-        den += f * ls[u];
-      }
-    }
-    a.out[((int64_t)b * a.num_q_heads + h * G + cc) * D + d] = (_Float16)(den > 0.0f ? num / den : 0.0f);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
 // Kernel timing (diagnostics): while enabled, every decode call launches its
-// two kernels with HIP events stamped with each kernel's start and end time
+// kernel with HIP events stamped with the kernel's start and end time
 // (hipExtLaunchKernelGGL).  Calls under graph capture are not timed.
 struct TimingState {
   bool on = false;
-  std::vector<std::array<hipEvent_t, 4>> events;
+  std::vector<std::array<hipEvent_t, 2>> events;
   size_t used = 0;
 };
 static TimingState g_timing;
@@ -994,7 +1041,7 @@ static hipEvent_t* timing_slot(hipStream_t stream) {
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
   if (g_timing.used == g_timing.events.size()) {
-    std::array<hipEvent_t, 4> e{};
+    std::array<hipEvent_t, 2> e{};
     for (auto& x : e)
       if (hipEventCreate(&x) != hipSuccess) return nullptr;
     g_timing.events.push_back(e);
@@ -1072,28 +1119,42 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   if (const char* env = getenv("S8KV_DECODE_SLOT_SKEW")) a.slot_skew = atoi(env);
   if (const char* env = getenv("S8KV_DECODE_GHOST")) a.ghost = (atoi(env) < 0 ? 0 : atoi(env) + 31) / 32 * 32;
   a.slots = a.batch + a.wg_per_head;
-  const dim3 grid(a.wg_per_head * a.num_kv_heads), mgrid(a.num_kv_heads, a.batch);
+  const dim3 grid(a.wg_per_head * a.num_kv_heads);
   hipEvent_t* ev = timing_slot(stream);
-  if (ev) {  // events stamped with the kernels' own start and end times
+  if (ev) {  // events stamped with the kernel's own start and end times
     hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
   } else {
     hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, a);
   }
-  int rc = check_launch("s8kv_decode");
-  if (rc == S8KV_OK) {
-    if (ev) {
-      hipExtLaunchKernelGGL((merge_kernel<D>), mgrid, dim3(256), 0, stream, ev[2], ev[3], 0, a);
-    } else {
-      hipLaunchKernelGGL((merge_kernel<D>), mgrid, dim3(256), 0, stream, a);
-    }
-    rc = check_launch("s8kv_decode(merge)");
-  }
-  return rc;
+  return check_launch("s8kv_decode");
 }
 
+// Workspace: (max, sum) and unnormalised output partials of every (q head,
+// slot), then the arrival counters of every (KV head, row).  The partials'
+// size is a multiple of 8 bytes (head_dim + 2 is even), so the counters are
+// 8-byte aligned when the workspace is.
+static int64_t partial_count(int batch, int num_q_heads, int num_kv_heads) {
+  return (int64_t)num_q_heads * (batch + max_wg_per_head(num_kv_heads));  // (q head, slot) pairs
+}
 static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim) {
-  const int64_t wph = max_wg_per_head(num_kv_heads);
-  return (int64_t)num_q_heads * (batch + wph) * (head_dim + 2) * 4 + (int64_t)batch * 8;
+  return partial_count(batch, num_q_heads, num_kv_heads) * (head_dim + 2) * 4 + (int64_t)num_kv_heads * batch * 8;
+}
+
+// A fresh 40-bit launch tag (never zero): a per-process sequence, seeded from
+// the clock and the process id, through the splitmix64 finaliser.
+static unsigned long long next_launch_tag() {
+  static std::atomic<unsigned long long> seq{0};
+  static const unsigned long long seed =
+      (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull ^
+      ((unsigned long long)getpid() << 32);
+  for (;;) {
+    unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (seq.fetch_add(1) + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    z &= (1ull << 40) - 1;
+    if (z != 0) return z;
+  }
 }
 
 static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1112,6 +1173,8 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
                "decode: block_size %d must be a power of two >= 4", block_size);
   S8KV_REQUIRE(num_blocks > 0, S8KV_ERR_INVALID, "decode: num_blocks must be > 0");
   S8KV_REQUIRE(max_context_len >= 0, S8KV_ERR_INVALID, "decode: max_context_len < 0");
+  S8KV_REQUIRE(max_context_len < (1 << 28), S8KV_ERR_UNSUPPORTED, "decode: max_context_len %d >= 2^28",
+               max_context_len);
   S8KV_REQUIRE((int64_t)batch * (max_context_len + 31) < (int64_t(1) << 31), S8KV_ERR_UNSUPPORTED,
                "decode: batch * max_context_len too large");
   S8KV_REQUIRE(a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.block_table && a.context_lens && a.out,
@@ -1140,10 +1203,12 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
   S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
                "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes_given);
-  const int64_t partials = (int64_t)num_q_heads * (batch + max_wg_per_head(num_kv_heads));  // (head, slot) pairs
+  S8KV_REQUIRE((uintptr_t)workspace % 8 == 0, S8KV_ERR_WORKSPACE, "decode: workspace not 8-byte aligned");
+  const int64_t partials = partial_count(batch, num_q_heads, num_kv_heads);
   a.ws_ml = reinterpret_cast<float*>(workspace);
   a.ws_acc = a.ws_ml + partials * 2;
-  a.ws_desc = reinterpret_cast<int*>(a.ws_acc + partials * head_dim);
+  a.ws_cnt = reinterpret_cast<unsigned long long*>(a.ws_acc + partials * head_dim);
+  a.tag = next_launch_tag();
   hipStream_t s = (hipStream_t)stream;
   if (fuse) {
     if (k8v3) {
@@ -1182,22 +1247,20 @@ extern "C" int s8kv_timing_begin(void) {
 
 extern "C" int s8kv_timing_end(int* launches, double* decode_ms, double* merge_ms) {
   g_timing.on = false;
-  double dk = 0.0, mk = 0.0;
+  double dk = 0.0;
   for (size_t i = 0; i < g_timing.used; ++i) {
     auto& e = g_timing.events[i];
-    if (hipEventSynchronize(e[3]) != hipSuccess) {
+    if (hipEventSynchronize(e[1]) != hipSuccess) {
       set_error("s8kv_timing_end: event synchronize failed");
       return S8KV_ERR_LAUNCH;
     }
-    float a = 0.f, b = 0.f;
+    float a = 0.f;
     hipEventElapsedTime(&a, e[0], e[1]);
-    hipEventElapsedTime(&b, e[2], e[3]);
     dk += a;
-    mk += b;
   }
   if (launches) *launches = (int)g_timing.used;
   if (decode_ms) *decode_ms = dk;
-  if (merge_ms) *merge_ms = mk;
+  if (merge_ms) *merge_ms = 0.0;  // the merge runs inside the decode kernel
   g_timing.used = 0;
   return S8KV_OK;
 }
