@@ -233,9 +233,17 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+// Inclusive prefix sum over the 64 lanes of a wave in DPP steps (VALU, no
+// LDS round trips): shifts by 1, 2, 4, 8 within each 16-lane row (lanes
+// shifted in from outside the row read 0), then lane 15 of rows 0 and 2 is
+// added to rows 1 and 3, and lane 31 to rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
   return v;
 }
 
@@ -249,14 +257,10 @@ __device__ __forceinline__ int raw_len_at(const DecodeArgs& a, const int* lens_l
   return b < kLensLds ? lens_lds[b] : a.context_lens[b];
 }
 
-// Stream length of all rows (every wave computes it; no barrier).
-__device__ __forceinline__ int stream_total(const DecodeArgs& a, const int* lens_lds, int lane) {
-  int t = 0;
-  for (int c0 = 0; c0 < a.batch; c0 += 64) {
-    const int r = c0 + lane;
-    t += wave_sum_i(r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0);
-  }
-  return __builtin_amdgcn_readfirstlane(t);
+// Stream length of rows c0 + lane (0 past the batch).
+__device__ __forceinline__ int row_stream_len(const DecodeArgs& a, const int* lens_lds, int c0, int lane) {
+  const int r = c0 + lane;
+  return r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0;
 }
 
 // Position of tile token tt (0..31) in the LDS-staged V tile: lane group g's
@@ -319,42 +323,46 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
   __syncthreads();
 
+  // ---- stream positions: prefix of the rows' stream lengths (every wave) ----
+  const int v0 = row_stream_len(a, lens_lds, 0, lane);
+  const int incl0 = wave_incl_scan(v0);  // rows 0..63
+  int total = __builtin_amdgcn_readlane(incl0, 63);
+  for (int c0 = 64; c0 < a.batch; c0 += 64)
+    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len(a, lens_lds, c0, lane)), 63);
+  total = __builtin_amdgcn_readfirstlane(total);
+
   // ---- this workgroup's slice [lo, hi) of the token stream ----
-  const int total = stream_total(a, lens_lds, lane);
   if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
-    for (int b = 0; b < a.batch; ++b)
-      if (lens_at(a, lens_lds, b) == 0) {
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      uint64_t m = __builtin_amdgcn_ballot_w64(c0 + lane < a.batch && lens_at(a, lens_lds, c0 + lane) == 0);
+      while (m != 0) {
+        const int b = c0 + (int)__builtin_ctzll(m);
+        m &= m - 1;
         for (int i = tid; i < G * D; i += 64 * kDecWaves)
           a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
       }
+    }
   }
   const SliceLayout sl = slice_layout(total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
   const int lo = slice_start(sl, j);
   if (lo >= total) return;
   const int hi = j + 1 >= a.wg_per_head ? total : min(total, slice_start(sl, j + 1));
 
-  // ---- first row whose stream range holds lo: wave-level prefix scan ----
+  // ---- first row whose stream range holds lo ----
   int b = 0, pb = 0;  // row, and the start of its stream range
   {
     int carry = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
-      const int r = c0 + lane;
-      const int v = r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0;
-      int incl = v;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-      }
-      incl += carry;
+      const int v = c0 == 0 ? v0 : row_stream_len(a, lens_lds, c0, lane);
+      const int incl = (c0 == 0 ? incl0 : wave_incl_scan(v)) + carry;
       const uint64_t m = __builtin_amdgcn_ballot_w64(incl > lo);
       if (m != 0) {
-        const int f = __builtin_ctzll(m);
+        const int f = (int)__builtin_ctzll(m);
         b = c0 + f;
-        pb = __shfl(incl - v, f);
+        pb = __builtin_amdgcn_readlane(incl - v, f);
         break;
       }
-      carry = __shfl(incl, 63);
+      carry = __builtin_amdgcn_readlane(incl, 63);
     }
   }
   b = __builtin_amdgcn_readfirstlane(b);
