@@ -73,6 +73,7 @@ constexpr int kMaxResidentPerCU = 8;                     // bound used to size t
 constexpr int kLensLds = 1024;                           // context lengths kept in LDS (rows beyond: global reads)
 constexpr int kGhostTokens = 256;                        // stream tokens charged per row start
 constexpr int kSlotSkewPermille = 200;                   // slice weight skew across residency slots
+constexpr int kQHeadsPerWave = 4;                        // q heads a wave rotates (group <= 16, 4 waves)
 
 template <int D, bool K8V3>
 struct DecCfg {
@@ -89,6 +90,7 @@ struct DecCfg {
   static constexpr int VSTAGE = kTile * VROW;                 // bytes per wave
   static constexpr int VLOADS = K8V3 ? (kTile * NG) / 64 : (kTile * D / 16) / 64;  // V loads per lane per tile
   static constexpr int SMEM_A = kDecWaves * VSTAGE;
+  static constexpr int SMEM_Q = (SMEM_A + 15) / 16 * 16;   // rotated q (hi, lo) [2][G][D] fp16, after the V staging
   // fused append: the new token's rows in LDS -- fp16 K and V (staged at the
   // segment start), int8 K, then int8 V (int8) or packed V words (K8V3), then
   // the K scale and the V scale (int8) or V norms (K8V3)
@@ -114,7 +116,6 @@ struct DecodeArgs {
   int bs_log2;
   int max_context_len;  // every row is clamped to it (block-table rows hold this many tokens)
   int smem_main;        // LDS bytes before the staged block ids (V staging, then the merge)
-  int q_vec;            // q rows are 16-byte aligned: load them with 16-byte loads
   int wg_per_head;      // workgroups per KV head (slices of the token stream)
   int slots;            // partial slots per head: batch + wg_per_head
   int ghost;            // stream tokens charged per row for its fixed costs (multiple of 32)
@@ -306,7 +307,8 @@ template <int D, bool K8V3, bool FUSE>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<D, K8V3>;
   constexpr int E = RowLayout<D>::E;
-  // LDS: [V staging of the 4 waves, reused for the cross-wave merge][block ids][context lengths]
+  // LDS: [V staging of the 4 waves | rotated q; the cross-wave merge reuses both][block ids]
+  //      [context lengths][fused append: the new token's rows]
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
   int* lens_lds = bt_lds + kMaxSubBlocks;
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // Set-up loads of a segment that starts at token 0 of row rb (or at s0 for
   // the slice's first row): the lane's raw q fragment and the first
   // sub-split's block ids, issued early so their latency overlaps other work.
-  half8_t qraw[C::KCH / 8];
+  _Float16 qraw[kQHeadsPerWave][E];
   int btv[kBtRegs];
   _Float16 knr[E], vnr[E];  // fused append: row rb's new K and V (RowLayout lanes)
   auto prefetch_segment = [&](int rb, int s0) {
@@ -430,23 +432,17 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         vnr[e] = on ? vp[lane_o + 64 * e] : (_Float16)0.0f;
       }
     }
+    // q of this wave's heads c = wave + 4k (lane l: dims l + 64e), the heads
+    // the wave rotates for the whole workgroup
     const int tid_o = opaque_int(threadIdx.x);
-    const int cl = tid_o & 15, gl = (tid_o & 63) >> 4;
-    const _Float16* qp =
-        a.q + (int64_t)rb * a.q_stride_b + (int64_t)(h * G + (cl < G ? cl : 0)) * a.q_stride_h + gl * C::KCH;
-    if (a.q_vec) {
+    const int lane_q = tid_o & 63;
 #pragma unroll
-      for (int i = 0; i < C::KCH / 8; ++i)
-        qraw[i] = (cl < G) ? *reinterpret_cast<const half8_t*>(qp + 8 * i) : half8_t{};
-    } else {  // unaligned q view: element loads, 8 in flight at a time (rare path)
+    for (int k = 0; k < kQHeadsPerWave; ++k) {
+      const int cq = wave + kDecWaves * k;
+      const _Float16* qp = a.q + (int64_t)rb * a.q_stride_b + (int64_t)(h * G + (cq < G ? cq : 0)) * a.q_stride_h;
 #pragma unroll
-      for (int i = 0; i < C::KCH / 8; ++i) {
-        half8_t t;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t[e] = (cl < G) ? qp[8 * i + e] : (_Float16)0.0f;
-        qraw[i] = t;
-        asm volatile("" : "+v"(qraw[i]));
-      }
+      for (int e = 0; e < E; ++e)
+        qraw[k][e] = (cq < G && lane_q < RowLayout<D>::ACTIVE) ? qp[lane_q + 64 * e] : (_Float16)0.0f;
     }
     const int fb = s0 >> bs_log2;
     const int32_t* bt_row = a.block_table + (int64_t)rb * a.bt_stride + fb;
@@ -487,44 +483,40 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     const int last = L - 1;
     const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
 
-    // q: lane (c, g) holds dims [g*KCH, (g+1)*KCH) of head c; fp32 FWHT with
-    // in-lane stages h < KCH and two cross-lane stages (lane ^ 16, lane ^ 32)
-    half8_t qhi[C::NQK], qlo[C::NQK];
-    {
-      float x[C::KCH];
+    // q: each wave rotates the heads c = wave + 4k of the group (lane l holds
+    // dims l + 64e: the append's fp32 FWHT, stages h = 1 .. D/2 in order),
+    // splits the scaled values into fp16 hi + lo and publishes them in LDS;
+    // then every wave takes its MFMA B fragments (lane (c, g): dims
+    // g*KCH + 8m .. +8 of head c).
+    _Float16* qs = reinterpret_cast<_Float16*>(smem + C::SMEM_Q);  // [hi, lo][G][D]
 #pragma unroll
-      for (int i = 0; i < C::KCH / 8; ++i) {
+    for (int k = 0; k < kQHeadsPerWave; ++k) {
+      const int cq = wave + kDecWaves * k;
+      if (cq < G) {
+        float x[E];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)qraw[i][e];
-      }
+        for (int e = 0; e < E; ++e) x[e] = (float)qraw[k][e];
+        fwht_row<D>(x, lane);
+        if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
-      for (int hs = 1; hs < C::KCH; hs <<= 1) {
-#pragma unroll
-        for (int i = 0; i < C::KCH; ++i) {
-          if ((i & hs) == 0) {
-            const float x0 = x[i], x1 = x[i + hs];
-            x[i] = x0 + x1;
-            x[i + hs] = x0 - x1;
+          for (int e = 0; e < E; ++e) {
+            // (materialized: hi and lo must both come from this one fp32 value;
+            // a fused fp16(x*s) for the lo term can differ from fp16(val) by one
+            // ulp, which would leave hi + lo off by 2^-11)
+            const float val = materialize(x[e] * a.qscale);
+            const _Float16 qh = (_Float16)val;
+            qs[cq * D + lane + 64 * e] = qh;
+            qs[(G + cq) * D + lane + 64 * e] = (_Float16)(val - (float)qh);
           }
         }
       }
+    }
+    __syncthreads();  // every head of q published
+    half8_t qhi[C::NQK], qlo[C::NQK];
 #pragma unroll
-      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x16(x[i], lane);
-#pragma unroll
-      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x32(x[i], lane);
-#pragma unroll
-      for (int m = 0; m < C::NQK; ++m) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // (materialized: hi and lo must both come from this one fp32 value;
-          // a fused fp16(x*s) for the lo term can differ from fp16(val) by one
-          // ulp, which would leave hi + lo off by 2^-11)
-          const float val = materialize(x[8 * m + e] * a.qscale);
-          const _Float16 qh = (_Float16)val;
-          qhi[m][e] = qh;
-          qlo[m][e] = (_Float16)(val - (float)qh);
-        }
-      }
+    for (int m = 0; m < C::NQK; ++m) {
+      qhi[m] = c < G ? *reinterpret_cast<const half8_t*>(qs + c * D + g * C::KCH + 8 * m) : half8_t{};
+      qlo[m] = c < G ? *reinterpret_cast<const half8_t*>(qs + (G + c) * D + g * C::KCH + 8 * m) : half8_t{};
     }
 
     // fused append: the wave that will process the row's last tile keeps the
@@ -1092,9 +1084,10 @@ template <int D, bool K8V3, bool FUSE>
 static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
   constexpr int kNewBytes = FUSE ? C::NEW_BYTES : 0;  // fused append: the new token's rows
-  const auto smem_main_for = [](int group) {
+  const auto smem_main_for = [](int group) {  // V staging + rotated q, or the cross-wave merge
     const int merge = kDecWaves * (group * D + 32) * 4;
-    return ((C::SMEM_A > merge ? C::SMEM_A : merge) + 15) / 16 * 16;
+    const int stage_q = C::SMEM_Q + 4 * group * D;
+    return ((stage_q > merge ? stage_q : merge) + 15) / 16 * 16;
   };
   a.smem_main = smem_main_for(a.group);
   a.smem_new = a.smem_main + (kMaxSubBlocks + kLensLds) * 4;
@@ -1205,7 +1198,6 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   }
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  a.q_vec = ((uintptr_t)a.q % 16 == 0) && (a.q_stride_b % 8 == 0) && (a.q_stride_h % 8 == 0);
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
   const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);

@@ -97,6 +97,29 @@ __device__ __forceinline__ float butterfly_x32(float x, int lane) {
   return (lane & 32) ? p.a - p.b : p.a + p.b;
 }
 
+// Walsh-Hadamard butterfly across lane ^ M on the VALU or the LDS swizzle
+// unit (no lane-address registers): M = 1, 2 DPP quad permutes, M = 4 an LDS
+// swizzle, M = 8 a DPP row rotate by 8, M = 16, 32 the permlane swaps.
+// Lanes with bit M clear get x + partner, lanes with it set partner - x.
+template <int M>
+__device__ __forceinline__ float butterfly_xor(float x, int lane) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane xor 1..32");
+  if constexpr (M == 16) {
+    return butterfly_x16(x, lane);
+  } else if constexpr (M == 32) {
+    return butterfly_x32(x, lane);
+  } else {
+    const int u = __builtin_bit_cast(int, x);
+    int pu;
+    if constexpr (M == 1) pu = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) pu = __builtin_amdgcn_mov_dpp(u, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) pu = __builtin_amdgcn_ds_swizzle(u, 0x1F | (4 << 10));     // bit mode, xor 4
+    else pu = __builtin_amdgcn_mov_dpp(u, 0x128, 0xF, 0xF, false);                        // row_ror:8
+    const float p = __builtin_bit_cast(float, pu);
+    return (lane & M) ? p - x : x + p;
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
@@ -170,18 +193,22 @@ struct RowLayout {
 // Fixed-order fp32 Walsh-Hadamard transform of one D-row spread over the wave:
 // stages h = 1, 2, ..., D/2; the pair (i, i+h) with bit h of i clear becomes
 // (x[i] + x[i+h], x[i] - x[i+h]).
+template <int D, int H>
+__device__ __forceinline__ void fwht_lane_stage(float (&x)[RowLayout<D>::E], int lane) {
+  if constexpr (H < D && H < 64) {
+#pragma unroll
+    for (int j = 0; j < RowLayout<D>::E; ++j) x[j] = butterfly_xor<H>(x[j], lane);
+  }
+}
 template <int D>
 __device__ __forceinline__ void fwht_row(float (&x)[RowLayout<D>::E], int lane) {
   constexpr int E = RowLayout<D>::E;
-#pragma unroll
-  for (int h = 1; h < D && h < 64; h <<= 1) {
-    const bool upper = (lane & h) != 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-      float p = shfl_xor_f(x[j], h);
-      x[j] = upper ? (p - x[j]) : (x[j] + p);
-    }
-  }
+  fwht_lane_stage<D, 1>(x, lane);  // h = 1 .. 32: across lanes
+  fwht_lane_stage<D, 2>(x, lane);
+  fwht_lane_stage<D, 4>(x, lane);
+  fwht_lane_stage<D, 8>(x, lane);
+  fwht_lane_stage<D, 16>(x, lane);
+  fwht_lane_stage<D, 32>(x, lane);
 #pragma unroll
   for (int hs = 1; hs < E; hs <<= 1) {  // h = 64*hs, in-lane
 #pragma unroll
