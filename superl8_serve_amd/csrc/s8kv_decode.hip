@@ -350,25 +350,29 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   if (lo >= total) return;
   const int hi = j + 1 >= a.wg_per_head ? total : min(total, slice_start(sl, j + 1));
 
-  // ---- first row whose stream range holds lo ----
-  int b = 0, pb = 0;  // row, and the start of its stream range
-  {
+  // The row whose stream range holds position pos (< total), and the start of
+  // that range.
+  auto find_row = [&](int pos, int& rb, int& rpb) {
+    rb = 0;
+    rpb = 0;
     int carry = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
       const int v = c0 == 0 ? v0 : row_stream_len(a, lens_lds, c0, lane);
       const int incl = (c0 == 0 ? incl0 : wave_incl_scan(v)) + carry;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(incl > lo);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(incl > pos);
       if (m != 0) {
         const int f = (int)__builtin_ctzll(m);
-        b = c0 + f;
-        pb = __builtin_amdgcn_readlane(incl - v, f);
+        rb = c0 + f;
+        rpb = __builtin_amdgcn_readlane(incl - v, f);
         break;
       }
       carry = __builtin_amdgcn_readlane(incl, 63);
     }
-  }
-  b = __builtin_amdgcn_readfirstlane(b);
-  pb = __builtin_amdgcn_readfirstlane(pb);
+    rb = __builtin_amdgcn_readfirstlane(rb);
+    rpb = __builtin_amdgcn_readfirstlane(rpb);
+  };
+  int b, pb;  // row, and the start of its stream range
+  find_row(lo, b, pb);
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
@@ -463,10 +467,31 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
   int L = find_segment(b, pb);
   if (L == 0) return;
+  // Segment order: when the slice's last segment is split by the slice end
+  // (its row continues in the next slice) and is not its first segment, it
+  // is processed first, then the segments from the first one on, stopping
+  // before its row.  Both parts of a row shared by two slices are then
+  // processed early in their slices, so the row's combine happens while
+  // other workgroups stream, not in the kernel's tail.
+  const int b_first = b, pb_first = pb, L_first = L;
+  int b_stop = a.batch;  // rows from here on are left to the reordered segment
+  bool reordered = false;
+  {
+    int bl, pbl;
+    find_row(hi - 1, bl, pbl);
+    const int Ll = bl > b ? __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, bl)) : 0;
+    if (Ll > 0 && pbl + a.ghost < hi && pbl + a.ghost + padded32(Ll) > hi) {
+      b = bl;
+      pb = pbl;
+      L = Ll;
+      b_stop = bl;
+      reordered = true;
+    }
+  }
   prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
   store_prefetched_bt();
 
-  // ---- segments: rows overlapping [lo, hi), in order ----
+  // ---- segments: rows overlapping [lo, hi) ----
   for (;;) {
     __syncthreads();  // staged block ids visible; the previous merge is done with LDS
     // per-lane values of this segment's q set-up and merge, from an opaque
@@ -911,11 +936,21 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     }
 
     // ---- next segment: its set-up loads overlap this segment's merge ----
-    int nb = b + 1, npb = pb + stream_len(a, L);
-    const int nL = find_segment(nb, npb);
+    int nb, npb, nL;
+    if (reordered) {  // the reordered last segment is done: continue from the first
+      nb = b_first;
+      npb = pb_first;
+      nL = L_first;
+      reordered = false;
+    } else {
+      nb = b + 1;
+      npb = pb + stream_len(a, L);
+      nL = find_segment(nb, npb);
+      if (nb >= b_stop) nL = 0;
+    }
     // (unconditional, from a valid row when there is no next segment: values
     // set on only one path would stay live across the tile loop)
-    prefetch_segment(nL != 0 ? nb : b, 0);
+    prefetch_segment(nL != 0 ? nb : b, nL != 0 ? max(lo, npb + a.ghost) - (npb + a.ghost) : 0);
 
     // ---- merge the waves of the workgroup in LDS ----
     {
