@@ -13,8 +13,9 @@
 // cost of a segment (q set-up, merge) to the slice that holds it.  A
 // segment's set-up loads (q, first block ids) are issued before the previous
 // segment's merge so their latency hides behind it.  Workgroup id
-// wg = j * Hkv + h, so the round-robin deal of workgroups to the 8 XCDs gives
-// every XCD the same share of every head.
+// wg = j * Hkv + h: the round-robin deal of workgroups to the 8 XCDs gives
+// every XCD the same number of equal-work workgroups (with Hkv = 8, all of
+// head h's on XCD h, whose L2 then holds that head's block table and q).
 //
 // Inside a segment the 4 waves of the workgroup take 32-token tiles in turn
 // (tiles w, w+4, ...) and keep an online softmax for the G = Hq/Hkv query heads
