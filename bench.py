@@ -497,6 +497,49 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2)}))
 
 
+def run_append(steps: int, warmup: int) -> None:
+    """Prefill append: 64 sequences x 2048 new tokens (131,072 tokens) of
+    Qwen3-8B K/V (8 KV heads, head_dim 128, fp16) quantized into a paged int8
+    cache (block 256) by one quantize_kv_write_paged call, as one layer of
+    the reference's write_prefill_varlen does; each sequence's slots are
+    contiguous over blocks dealt from a seeded permutation of the pool.  The
+    inputs (537 MB) exceed the 256 MB Infinity Cache, so every call reads
+    them from HBM."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    seqs, per_seq = 64, 2048
+    T = seqs * per_seq
+    nblk = per_seq // BS
+    pool = seqs * nblk + 64
+    perm = np.random.default_rng(7).permutation(pool)
+    off = np.arange(per_seq)
+    slots = np.concatenate([perm[s * nblk + off // BS] * BS + off % BS for s in range(seqs)]).astype(np.int32)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    k = torch.randn((T, HKV, D), device="cuda", generator=gen).half()
+    v = torch.randn((T, HKV, D), device="cuda", generator=gen).half()
+    kc = torch.zeros((pool, HKV, BS, D), dtype=torch.int8, device="cuda")
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((pool, HKV, BS), dtype=torch.float32, device="cuda")
+    vs = torch.zeros_like(ks)
+    sm = torch.from_numpy(slots).cuda()
+    for _ in range(max(warmup, 1)):
+        ops.quantize_kv_write_paged(k, v, kc, ks, vc, vs, sm)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(steps):
+        ops.quantize_kv_write_paged(k, v, kc, ks, vc, vs, sm)
+    en.record()
+    torch.cuda.synchronize()
+    sec = st.elapsed_time(en) * 1e-3 / steps
+    moved = T * HKV * (2 * D * 2 + 2 * D + 2 * 4)  # fp16 K, V in; int8 K, V and two fp32 scales out
+    print(json.dumps({"metric": "prefill append GB/s (fp16 K/V in, int8 + scales out), 131,072 tokens x 8 KV heads",
+                      "value": round(moved / sec / 1e9, 1), "unit": "GB/s", "us_per_call": round(sec * 1e6, 1),
+                      "bytes_per_call": moved, "pct_of_hbm_peak": round(100 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
+
+
 def run_copy(steps: int) -> None:
     """copy_blocks over a 4096-block synthetic pool (Qwen3-8B int8 block: K, V,
     two scale tensors; 1 layer): 1024 random source blocks moved to 1024 other
@@ -542,9 +585,10 @@ def main():
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy", "append"], default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
-                         "attention; k8v3: the K8V3 decode step (batch 32, 8k-32k); copy: copy_blocks")
+                         "attention; k8v3: the K8V3 decode step (batch 32, 8k-32k); copy: copy_blocks; "
+                         "append: prefill append of 131,072 tokens")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -571,6 +615,9 @@ def main():
         return
     if args.workload == "copy":
         run_copy(args.steps)
+        return
+    if args.workload == "append":
+        run_append(args.steps, args.warmup)
         return
 
     device = "cuda"

@@ -66,18 +66,20 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
   const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
 
-  // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
-  float x[E];
+  // both rows' loads in flight together
+  float x[E], y[E];
   load_row_f16<D>(a.k + t * a.k_stride_t + h * a.k_stride_h, x, lane);
+  load_row_f16<D>(a.v + t * a.v_stride_t + h * a.v_stride_h, y, lane);
+
+  // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
   fwht_row<D>(x, lane);
 #pragma unroll
   for (int j = 0; j < E; ++j) x[j] = (float)(_Float16)materialize(x[j] * a.rot_norm);
   rtn_store_row<D>(x, lane, kc, row * (uint32_t)D, ks, row * 4u);
 
   // ---- V ----
-  load_row_f16<D>(a.v + t * a.v_stride_t + h * a.v_stride_h, x, lane);
   if constexpr (!K8V3) {
-    rtn_store_row<D>(x, lane, vc, row * (uint32_t)D, vs, row * 4u);
+    rtn_store_row<D>(y, lane, vc, row * (uint32_t)D, vs, row * 4u);
   } else {
     static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
     constexpr int NB = D / 128;   // Lloyd-Max blocks per row (lloyd_block = 128)
@@ -87,16 +89,149 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
     for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
     uint32_t w;
     float nv;
-    lloydmax3_encode_row<D>(x, cb, lane, w, nv);
+    lloydmax3_encode_row<D>(y, cb, lane, w, nv);
     if (lane < WORDS) bstore32(w, vc, row * (uint32_t)(WORDS * 4) + lane * 4u);
     if (lane < NB) bstore32(__builtin_bit_cast(uint32_t, nv), vs, row * (uint32_t)(NB * 4) + lane * 4u);
   }
+}
+
+// int8 append with several rows per wave: a row's D values sit on LPR = D/16
+// consecutive lanes, 16 consecutive values per lane, so each lane moves a row
+// part with two 16-byte loads and one 16-byte store per tensor and the
+// per-row work (slot lookup, addresses, reductions) is shared by 64/LPR rows
+// per instruction.  The K rotation runs the FWHT stages h = 1, 2, 4, 8
+// in-lane and h = 16 .. D/2 as lane ^ (h/16) butterflies: the stage order and
+// arithmetic of fwht_row, so the bytes equal the one-row-per-wave kernel's.
+// Needs 16-byte aligned K and V rows.
+template <int D>
+__device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, int li, rsrc_t qbuf,
+                                               uint32_t byte_off, rsrc_t sbuf, uint32_t scale_off) {
+  constexpr int LPR = D / 16;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(y[i]));
+  if constexpr (LPR > 1) amax = fmaxf(amax, xor_partner<1>(amax));
+  if constexpr (LPR > 2) amax = fmaxf(amax, xor_partner<2>(amax));
+  if constexpr (LPR > 4) amax = fmaxf(amax, xor_partner<4>(amax));
+  if constexpr (LPR > 8) amax = fmaxf(amax, xor_partner<8>(amax));
+  const float scale = amax / 127.0f;
+  const float rscale = 1.0f / scale;  // (inf for a zero row: rtn_i8_recip returns 0 there)
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v |= ((uint32_t)rtn_i8_recip(y[4 * k + i], scale, rscale) & 0xFFu) << (8 * i);
+    w[k] = v;
+  }
+  if (live) {
+    bstore128(u32x4_t{w[0], w[1], w[2], w[3]}, qbuf, byte_off);
+    if (li == 0) bstore32(__builtin_bit_cast(uint32_t, scale), sbuf, scale_off);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendArgs a) {
+  constexpr int LPR = D / 16;  // lanes per row
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int li = lane % LPR;
+  const int64_t row_id = ((int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  bool live = row_id < a.num_tokens * a.num_kv_heads;
+  int64_t t = 0;
+  int h = 0;
+  uint32_t row = 0;
+  if (live) {
+    t = row_id / a.num_kv_heads;
+    h = (int)(row_id - t * a.num_kv_heads);
+    const int32_t slot = a.slot_mapping[t];
+    const uint32_t blk = (uint32_t)slot >> a.block_size_log2;
+    live = slot >= 0 && (int64_t)blk < a.num_blocks;  // negative slots and slots outside the pool are skipped
+    row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) +
+          ((uint32_t)slot & ((1u << a.block_size_log2) - 1u));
+  }
+  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
+  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
+
+  // both row parts' loads in flight together
+  float x[16], y[16];
+  {
+    half8_t k0{}, k1{}, v0{}, v1{};
+    if (live) {
+      const _Float16* kp = a.k + t * a.k_stride_t + h * a.k_stride_h + li * 16;
+      const _Float16* vp = a.v + t * a.v_stride_t + h * a.v_stride_h + li * 16;
+      k0 = *reinterpret_cast<const half8_t*>(kp);
+      k1 = *reinterpret_cast<const half8_t*>(kp + 8);
+      v0 = *reinterpret_cast<const half8_t*>(vp);
+      v1 = *reinterpret_cast<const half8_t*>(vp + 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[i] = (float)k0[i];
+      x[8 + i] = (float)k1[i];
+      y[i] = (float)v0[i];
+      y[8 + i] = (float)v1[i];
+    }
+  }
+
+  // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
+#pragma unroll
+  for (int hs = 1; hs < 16; hs <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if ((i & hs) == 0) {
+        const float p0 = x[i], p1 = x[i + hs];
+        x[i] = p0 + p1;
+        x[i + hs] = p0 - p1;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (LPR > 1) x[i] = butterfly_xor<1>(x[i], lane);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (LPR > 2) x[i] = butterfly_xor<2>(x[i], lane);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (LPR > 4) x[i] = butterfly_xor<4>(x[i], lane);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (LPR > 8) x[i] = butterfly_xor<8>(x[i], lane);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = (float)(_Float16)materialize(x[i] * a.rot_norm);
+  rows_rtn_store<D>(x, live, li, kc, row * (uint32_t)D + (uint32_t)li * 16u, ks, row * 4u);
+
+  // ---- V: RTN ----
+  rows_rtn_store<D>(y, live, li, vc, row * (uint32_t)D + (uint32_t)li * 16u, vs, row * 4u);
 }
 
 template <bool K8V3>
 static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) {
   const int64_t rows = a.num_tokens * a.num_kv_heads;
   if (rows == 0) return S8KV_OK;
+  const bool rows16 = ((uintptr_t)a.k % 16 == 0) && ((uintptr_t)a.v % 16 == 0) && a.k_stride_t % 8 == 0 &&
+                      a.k_stride_h % 8 == 0 && a.v_stride_t % 8 == 0 && a.v_stride_h % 8 == 0;
+  if (!K8V3 && rows16) {  // several rows per wave
+    const int rows_per_wg = kAppendWaves * 64 / (head_dim / 16);
+    const int64_t grid = (rows + rows_per_wg - 1) / rows_per_wg;
+    S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);
+    dim3 g((unsigned)grid), b(64 * kAppendWaves);
+    switch (head_dim) {
+      case 32: hipLaunchKernelGGL((append_rows_kernel<32>), g, b, 0, stream, a); break;
+      case 64: hipLaunchKernelGGL((append_rows_kernel<64>), g, b, 0, stream, a); break;
+      case 128: hipLaunchKernelGGL((append_rows_kernel<128>), g, b, 0, stream, a); break;
+      case 256: hipLaunchKernelGGL((append_rows_kernel<256>), g, b, 0, stream, a); break;
+      default: return S8KV_ERR_UNSUPPORTED;
+    }
+    return check_launch("s8kv_append_int8");
+  }
   const int64_t grid = (rows + kAppendWaves - 1) / kAppendWaves;
   S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);
   dim3 g((unsigned)grid), b(64 * kAppendWaves);

@@ -102,6 +102,17 @@ __device__ __forceinline__ float butterfly_x32(float x, int lane) {
 // swizzle, M = 8 a DPP row rotate by 8, M = 16, 32 the permlane swaps.
 // Lanes with bit M clear get x + partner, lanes with it set partner - x.
 template <int M>
+__device__ __forceinline__ float xor_partner(float x) {  // the value of lane ^ M, M = 1, 2, 4, 8
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "lane xor 1..8");
+  const int u = __builtin_bit_cast(int, x);
+  int pu;
+  if constexpr (M == 1) pu = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
+  else if constexpr (M == 2) pu = __builtin_amdgcn_mov_dpp(u, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  else if constexpr (M == 4) pu = __builtin_amdgcn_ds_swizzle(u, 0x1F | (4 << 10));     // bit mode, xor 4
+  else pu = __builtin_amdgcn_mov_dpp(u, 0x128, 0xF, 0xF, false);                        // row_ror:8
+  return __builtin_bit_cast(float, pu);
+}
+template <int M>
 __device__ __forceinline__ float butterfly_xor(float x, int lane) {
   static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane xor 1..32");
   if constexpr (M == 16) {
@@ -109,13 +120,7 @@ __device__ __forceinline__ float butterfly_xor(float x, int lane) {
   } else if constexpr (M == 32) {
     return butterfly_x32(x, lane);
   } else {
-    const int u = __builtin_bit_cast(int, x);
-    int pu;
-    if constexpr (M == 1) pu = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
-    else if constexpr (M == 2) pu = __builtin_amdgcn_mov_dpp(u, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-    else if constexpr (M == 4) pu = __builtin_amdgcn_ds_swizzle(u, 0x1F | (4 << 10));     // bit mode, xor 4
-    else pu = __builtin_amdgcn_mov_dpp(u, 0x128, 0xF, 0xF, false);                        // row_ror:8
-    const float p = __builtin_bit_cast(float, pu);
+    const float p = xor_partner<M>(x);
     return (lane & M) ? p - x : x + p;
   }
 }
@@ -176,6 +181,22 @@ __device__ __forceinline__ int opaque_int(int x) {
 __device__ __forceinline__ int rtn_i8(float y, float scale) {
   if (!(scale > 0.0f)) return 0;
   float q = __builtin_rintf(y / scale);
+  q = fminf(127.0f, fmaxf(-127.0f, q));
+  return (int)q;
+}
+
+// rtn_i8 with the quotient from a per-row reciprocal: rscale = 1 / scale
+// (IEEE), q0 = RN(y * rscale), the residual y - q0 * scale exactly by FMA, and
+// one FMA correction q0 + residual * rscale (Markstein's division).  For the
+// append's operands -- y an fp16 value and scale = RN(m / 127) for an fp16
+// absmax m >= |y| -- the corrected quotient equals the IEEE quotient y / scale
+// for every such pair (an exhaustive check over all 1.0e9 of them), so the
+// codes equal rtn_i8's.
+__device__ __forceinline__ int rtn_i8_recip(float y, float scale, float rscale) {
+  if (!(scale > 0.0f)) return 0;
+  const float q0 = materialize(y * rscale);
+  const float r = __builtin_fmaf(-q0, scale, y);
+  float q = __builtin_rintf(__builtin_fmaf(r, rscale, q0));
   q = fminf(127.0f, fmaxf(-127.0f, q));
   return (int)q;
 }

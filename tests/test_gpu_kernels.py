@@ -106,6 +106,36 @@ def test_append_int8_special_rows():
         assert np.array_equal(_np(a), b)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+def test_append_int8_input_views(d):
+    """The same tokens written from contiguous K/V (several rows per wave),
+    from K/V slices of a fused qkv projection output (strided, 16-byte aligned
+    rows: several rows per wave) and from views 2 bytes off alignment (one row
+    per wave): every cache byte equals the oracle's."""
+    hq, hkv, bs = 4, 2, 16
+    case = make_case(40 + d, 3, hq, hkv, d, bs, [37, 16, 70])
+    ref = oracle_fill_int8(case)
+    t = case.k.shape[0]
+    qkv = torch.zeros((t, (hq + 2 * hkv) * d), dtype=torch.float16, device=DEV)
+    qkv[:, hq * d:(hq + hkv) * d] = _t(case.k).reshape(t, hkv * d)
+    qkv[:, (hq + hkv) * d:] = _t(case.v).reshape(t, hkv * d)
+    k_slice = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v_slice = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    flat = torch.zeros(2 * t * hkv * d + 1, dtype=torch.float16, device=DEV)
+    k_odd = flat[1:1 + t * hkv * d].view(t, hkv, d)
+    v_odd = flat[1 + t * hkv * d:].view(t, hkv, d)
+    k_odd.copy_(_t(case.k))
+    v_odd.copy_(_t(case.v))
+    assert k_slice.stride(0) == (hq + 2 * hkv) * d and k_odd.data_ptr() % 16 == 2
+    for name, (kk, vv) in {"contiguous": (_t(case.k), _t(case.v)), "qkv slices": (k_slice, v_slice),
+                           "unaligned": (k_odd, v_odd)}.items():
+        kc, ks, vc, vs = _gpu_int8_cache(case)
+        ops.quantize_kv_write_paged(kk, vv, kc, ks, vc, vs, _t(case.slots))
+        torch.cuda.synchronize()
+        for what, g, r in zip(("k_cache", "k_scale", "v_cache", "v_scale"), (kc, ks, vc, vs), ref):
+            assert np.array_equal(_np(g).view(np.uint8), r.view(np.uint8)), f"{name}: {what} differs"
+
+
 def test_append_negative_slot_skipped():
     case = make_case(3, 2, 4, 2, 128, 16, [20, 5])
     slots = case.slots.copy()
