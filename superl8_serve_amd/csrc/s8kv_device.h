@@ -254,7 +254,8 @@ __device__ __forceinline__ void load_row_f16(const _Float16* p, float (&x)[RowLa
 }
 
 // Per-row RTN int8 of the wave's row (lane layout of RowLayout): scale =
-// absmax/127 over the wave, codes rint(y/scale) clamped to +-127.
+// absmax/127 over the wave, codes rint(y/scale) clamped to +-127 (y must be
+// fp16 values: the quotient comes from rtn_i8_recip).
 template <int D>
 __device__ __forceinline__ float rtn_row(const float (&y)[RowLayout<D>::E], int (&q)[RowLayout<D>::E]) {
   constexpr int E = RowLayout<D>::E;
@@ -263,8 +264,9 @@ __device__ __forceinline__ float rtn_row(const float (&y)[RowLayout<D>::E], int 
   for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(y[j]));
   amax = wave_max(amax);
   const float scale = amax / 127.0f;
+  const float rscale = 1.0f / scale;
 #pragma unroll
-  for (int j = 0; j < E; ++j) q[j] = rtn_i8(y[j], scale);
+  for (int j = 0; j < E; ++j) q[j] = rtn_i8_recip(y[j], scale, rscale);
   return scale;
 }
 
