@@ -408,8 +408,8 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
     (attn_paged_decode_append_k8v3) unless `fused` is False."""
     import torch
 
-    from oracle import kv_oracle as O
     from superl8_serve_amd import ops
+    from superl8_serve_amd.codebook import gaussian_codebook
 
     dev = "cuda"
     rng = np.random.default_rng(2)
@@ -429,7 +429,7 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
     ks = torch.ones(shape[:4], dtype=torch.float32, device=dev)
     vp = torch.zeros(shape[:4] + (D * 3 // 32,), dtype=torch.int32, device=dev)
     vn = torch.zeros(shape[:4] + (D // 128,), dtype=torch.float32, device=dev)
-    cb = torch.from_numpy(O.gaussian_codebook(3, 128)).to(dev)
+    cb = torch.from_numpy(gaussian_codebook(3, 128)).to(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(2)
     chunk = 65536
@@ -497,14 +497,14 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2)}))
 
 
-def run_append(steps: int, warmup: int) -> None:
+def run_append(steps: int, warmup: int, k8v3: bool = False) -> None:
     """Prefill append: 64 sequences x 2048 new tokens (131,072 tokens) of
-    Qwen3-8B K/V (8 KV heads, head_dim 128, fp16) quantized into a paged int8
-    cache (block 256) by one quantize_kv_write_paged call, as one layer of
-    the reference's write_prefill_varlen does; each sequence's slots are
-    contiguous over blocks dealt from a seeded permutation of the pool.  The
-    inputs (537 MB) exceed the 256 MB Infinity Cache, so every call reads
-    them from HBM."""
+    Qwen3-8B K/V (8 KV heads, head_dim 128, fp16) quantized into a paged
+    cache (block 256) by one quantize_kv_write_paged call (K8V3:
+    quantize_kv_write_paged_k8v3), as one layer of the reference's
+    write_prefill_varlen does; each sequence's slots are contiguous over
+    blocks dealt from a seeded permutation of the pool.  The inputs (537 MB)
+    exceed the 256 MB Infinity Cache, so every call reads them from HBM."""
     import torch
 
     from superl8_serve_amd import ops
@@ -520,22 +520,40 @@ def run_append(steps: int, warmup: int) -> None:
     k = torch.randn((T, HKV, D), device="cuda", generator=gen).half()
     v = torch.randn((T, HKV, D), device="cuda", generator=gen).half()
     kc = torch.zeros((pool, HKV, BS, D), dtype=torch.int8, device="cuda")
-    vc = torch.zeros_like(kc)
     ks = torch.zeros((pool, HKV, BS), dtype=torch.float32, device="cuda")
-    vs = torch.zeros_like(ks)
     sm = torch.from_numpy(slots).cuda()
+    if k8v3:
+        from superl8_serve_amd.codebook import gaussian_codebook
+
+        vc = torch.zeros((pool, HKV, BS, D * 3 // 32), dtype=torch.int32, device="cuda")
+        vs = torch.zeros((pool, HKV, BS, D // 128), dtype=torch.float32, device="cuda")
+        cb = torch.from_numpy(gaussian_codebook(3, 128)).cuda()
+
+        def call():
+            ops.quantize_kv_write_paged_k8v3(k, v, kc, ks, vc, vs, cb, sm)
+
+        out_bytes = D + 4 + D * 3 // 8 + 4 * (D // 128)  # int8 K + scale, packed 3-bit V + norms
+    else:
+        vc = torch.zeros_like(kc)
+        vs = torch.zeros_like(ks)
+
+        def call():
+            ops.quantize_kv_write_paged(k, v, kc, ks, vc, vs, sm)
+
+        out_bytes = 2 * D + 2 * 4  # int8 K, V and two fp32 scales
     for _ in range(max(warmup, 1)):
-        ops.quantize_kv_write_paged(k, v, kc, ks, vc, vs, sm)
+        call()
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     st.record()
     for _ in range(steps):
-        ops.quantize_kv_write_paged(k, v, kc, ks, vc, vs, sm)
+        call()
     en.record()
     torch.cuda.synchronize()
     sec = st.elapsed_time(en) * 1e-3 / steps
-    moved = T * HKV * (2 * D * 2 + 2 * D + 2 * 4)  # fp16 K, V in; int8 K, V and two fp32 scales out
-    print(json.dumps({"metric": "prefill append GB/s (fp16 K/V in, int8 + scales out), 131,072 tokens x 8 KV heads",
+    moved = T * HKV * (2 * D * 2 + out_bytes)  # fp16 K, V in; the cache bytes out
+    fmt = "k8v3: int8 K + 3-bit V" if k8v3 else "int8 + scales"
+    print(json.dumps({"metric": f"prefill append GB/s (fp16 K/V in, {fmt} out), 131,072 tokens x 8 KV heads",
                       "value": round(moved / sec / 1e9, 1), "unit": "GB/s", "us_per_call": round(sec * 1e6, 1),
                       "bytes_per_call": moved, "pct_of_hbm_peak": round(100 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
 
@@ -585,10 +603,11 @@ def main():
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy", "append"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy", "append", "append_k8v3"],
+                    default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
                          "attention; k8v3: the K8V3 decode step (batch 32, 8k-32k); copy: copy_blocks; "
-                         "append: prefill append of 131,072 tokens")
+                         "append / append_k8v3: prefill append of 131,072 tokens")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -616,8 +635,8 @@ def main():
     if args.workload == "copy":
         run_copy(args.steps)
         return
-    if args.workload == "append":
-        run_append(args.steps, args.warmup)
+    if args.workload in ("append", "append_k8v3"):
+        run_append(args.steps, args.warmup, k8v3=args.workload == "append_k8v3")
         return
 
     device = "cuda"

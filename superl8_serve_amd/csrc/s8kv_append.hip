@@ -130,7 +130,62 @@ __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, 
   }
 }
 
+// 3-bit Lloyd-Max V of the lane's 16 values (head_dim 128 or 256, blocks of
+// 128 = 8 lanes): the block's L2 norm adds the fp32 squares in the order of
+// lloydmax3_encode_row (halves folded at h = 64, 32, 16 across lanes ^ 4,
+// ^ 2, ^ 1, then h = 8 .. 1 in-lane), correctly rounded sqrt; u = v / norm
+// (0 for a zero norm); code = first index minimising |u - c_j|.  Lanes 2g
+// and 2g + 1 hold elements 32g .. 32g + 31: each builds 16 bits of the three
+// bit-plane words 3g + b, and the even lane stores them.
 template <int D>
+__device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool live, int li, const float (&cb)[8],
+                                                     rsrc_t vbuf, uint32_t word_off, rsrc_t nbuf, uint32_t norm_off) {
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = x[i] * x[i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<4>(s[i]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<2>(s[i]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<1>(s[i]);
+#pragma unroll
+  for (int h = 8; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int i = 0; i < h; ++i) s[i] = s[i] + s[i + h];
+  }
+  const float nrm = __builtin_sqrtf(s[0]);
+  uint32_t pw[3] = {0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float u = nrm > 0.0f ? x[i] / nrm : 0.0f;
+    float best = fabsf(u - cb[0]);
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+      const float d = fabsf(u - cb[j]);
+      if (d < best) {
+        best = d;
+        c = (uint32_t)j;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 3; ++b) pw[b] |= ((c >> b) & 1u) << i;
+  }
+  uint32_t w[3];
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    const uint32_t odd = (uint32_t)__builtin_amdgcn_mov_dpp((int)pw[b], 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    w[b] = pw[b] | (odd << 16);
+  }
+  if (live && (li & 1) == 0) {
+#pragma unroll
+    for (int b = 0; b < 3; ++b) bstore32(w[b], vbuf, word_off + (uint32_t)(li / 2) * 12u + 4u * b);
+  }
+  if (live && (li & 7) == 0) bstore32(__builtin_bit_cast(uint32_t, nrm), nbuf, norm_off + (uint32_t)(li / 8) * 4u);
+}
+
+template <int D, bool K8V3>
 __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendArgs a) {
   constexpr int LPR = D / 16;  // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave
@@ -208,8 +263,16 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendAr
   for (int i = 0; i < 16; ++i) x[i] = (float)(_Float16)materialize(x[i] * a.rot_norm);
   rows_rtn_store<D>(x, live, li, kc, row * (uint32_t)D + (uint32_t)li * 16u, ks, row * 4u);
 
-  // ---- V: RTN ----
-  rows_rtn_store<D>(y, live, li, vc, row * (uint32_t)D + (uint32_t)li * 16u, vs, row * 4u);
+  // ---- V: RTN, or 3-bit Lloyd-Max ----
+  if constexpr (!K8V3) {
+    rows_rtn_store<D>(y, live, li, vc, row * (uint32_t)D + (uint32_t)li * 16u, vs, row * 4u);
+  } else {
+    static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
+    float cb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
+    rows_lloydmax3_store<D>(y, live, li, cb, vc, row * (uint32_t)(D / 32 * 3 * 4), vs, row * (uint32_t)(D / 128 * 4));
+  }
 }
 
 template <bool K8V3>
@@ -218,19 +281,23 @@ static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) 
   if (rows == 0) return S8KV_OK;
   const bool rows16 = ((uintptr_t)a.k % 16 == 0) && ((uintptr_t)a.v % 16 == 0) && a.k_stride_t % 8 == 0 &&
                       a.k_stride_h % 8 == 0 && a.v_stride_t % 8 == 0 && a.v_stride_h % 8 == 0;
-  if (!K8V3 && rows16) {  // several rows per wave
+  if (rows16) {  // several rows per wave
     const int rows_per_wg = kAppendWaves * 64 / (head_dim / 16);
     const int64_t grid = (rows + rows_per_wg - 1) / rows_per_wg;
     S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);
     dim3 g((unsigned)grid), b(64 * kAppendWaves);
     switch (head_dim) {
-      case 32: hipLaunchKernelGGL((append_rows_kernel<32>), g, b, 0, stream, a); break;
-      case 64: hipLaunchKernelGGL((append_rows_kernel<64>), g, b, 0, stream, a); break;
-      case 128: hipLaunchKernelGGL((append_rows_kernel<128>), g, b, 0, stream, a); break;
-      case 256: hipLaunchKernelGGL((append_rows_kernel<256>), g, b, 0, stream, a); break;
+      case 32:
+        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<32, false>), g, b, 0, stream, a); break; }
+        return S8KV_ERR_UNSUPPORTED;
+      case 64:
+        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<64, false>), g, b, 0, stream, a); break; }
+        return S8KV_ERR_UNSUPPORTED;
+      case 128: hipLaunchKernelGGL((append_rows_kernel<128, K8V3>), g, b, 0, stream, a); break;
+      case 256: hipLaunchKernelGGL((append_rows_kernel<256, K8V3>), g, b, 0, stream, a); break;
       default: return S8KV_ERR_UNSUPPORTED;
     }
-    return check_launch("s8kv_append_int8");
+    return check_launch(K8V3 ? "s8kv_append_k8v3" : "s8kv_append_int8");
   }
   const int64_t grid = (rows + kAppendWaves - 1) / kAppendWaves;
   S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);

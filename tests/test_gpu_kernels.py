@@ -162,6 +162,27 @@ def test_append_k8v3_bitexact(d, bs, lens):
         assert np.array_equal(got.view(np.uint8), b.view(np.uint8)), f"{name} differs"
 
 
+@pytest.mark.parametrize("d", [128, 256])
+def test_append_k8v3_input_views(d):
+    """K8V3 writes from 16-byte aligned rows (several rows per wave) and from
+    views 2 bytes off alignment (one row per wave): both equal the oracle."""
+    hkv, bs = 2, 16
+    case = make_case(50 + d, 3, 4, hkv, d, bs, [37, 16, 70], outlier_channels=2)
+    ref = oracle_fill_k8v3(case, CODEBOOK)
+    t = case.k.shape[0]
+    flat = torch.zeros(2 * t * hkv * d + 1, dtype=torch.float16, device=DEV)
+    k_odd = flat[1:1 + t * hkv * d].view(t, hkv, d)
+    v_odd = flat[1 + t * hkv * d:].view(t, hkv, d)
+    k_odd.copy_(_t(case.k))
+    v_odd.copy_(_t(case.v))
+    for name, (kk, vv) in {"aligned": (_t(case.k), _t(case.v)), "unaligned": (k_odd, v_odd)}.items():
+        g = _gpu_k8v3_cache(case)
+        ops.quantize_kv_write_paged_k8v3(kk, vv, *g, _t(CODEBOOK), _t(case.slots))
+        torch.cuda.synchronize()
+        for what, a, b in zip(("k_cache", "k_scale", "v_packed", "v_norm"), g, ref):
+            assert np.array_equal(_np(a).view(np.uint8), b.view(np.uint8)), f"{name}: {what} differs"
+
+
 def test_append_k8v3_zero_and_tie_rows():
     d, hkv, bs = 128, 1, 4
     rows = [np.zeros(d), np.ones(d), np.r_[np.ones(64), -np.ones(64)], np.linspace(-3, 3, d)]
