@@ -213,27 +213,6 @@ __device__ __forceinline__ int slice_of(const SliceLayout& s, int p) {
   return __builtin_amdgcn_readlane(s.f0 + k, cl);
 }
 
-// One segment of a split row has stored its partial: add its `units` (32-token
-// units) to the row's counter word; true for the arrival that completes the
-// row's `total` units, which also writes the word back to zero.  Every failed
-// exchange means another segment's add went in, so the loop ends.
-__device__ __forceinline__ bool arrive(unsigned long long* cp, unsigned long long tag, uint32_t units, uint32_t total) {
-  unsigned long long old = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (;;) {
-    const uint32_t done = (old >> 24) == tag ? (uint32_t)(old & 0xFFFFFFu) : 0u;
-    const uint32_t now = done + units;
-    const unsigned long long nw = now == total ? 0ull : (tag << 24) | now;
-    if (__hip_atomic_compare_exchange_weak(cp, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT))
-      return now == total;
-  }
-}
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Inclusive prefix sum over the 64 lanes of a wave in DPP steps (VALU, no
 // LDS round trips): shifts by 1, 2, 4, 8 within each 16-lane row (lanes
@@ -1085,19 +1064,6 @@ static hipEvent_t* timing_slot(hipStream_t stream) {
   return g_timing.events[g_timing.used++].data();
 }
 
-// Compute units of the current device (cached per device id).
-static int device_cus() {
-  constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  if (dev >= 0 && dev < kMaxDevices && cached[dev] > 0) return cached[dev];
-  int cus = 256;
-  int v = 0;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-  if (dev >= 0 && dev < kMaxDevices) cached[dev] = cus;
-  return cus;
-}
 
 // Workgroups per KV head: about the number the GPU keeps resident, split
 // evenly over the heads.  S8KV_DECODE_WG_PER_HEAD overrides it (clamped to
@@ -1177,22 +1143,6 @@ static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int
   return partial_count(batch, num_q_heads, num_kv_heads) * (head_dim + 2) * 4 + (int64_t)num_kv_heads * batch * 8;
 }
 
-// A fresh 40-bit launch tag (never zero): a per-process sequence, seeded from
-// the clock and the process id, through the splitmix64 finaliser.
-static unsigned long long next_launch_tag() {
-  static std::atomic<unsigned long long> seq{0};
-  static const unsigned long long seed =
-      (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull ^
-      ((unsigned long long)getpid() << 32);
-  for (;;) {
-    unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (seq.fetch_add(1) + 1);
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    z ^= z >> 31;
-    z &= (1ull << 40) - 1;
-    if (z != 0) return z;
-  }
-}
 
 static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                          int64_t num_blocks, int block_size, int max_context_len, float scale, void* workspace,

@@ -339,3 +339,29 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
 }
 
 }  // namespace s8kv
+
+// Arrival at a counter word shared by the workgroups that each stored one
+// partial of the same output: add `units` to the word; true for the arrival
+// that completes `total` units, which also writes the word back to zero.  The
+// word holds this launch's 40-bit tag above a 24-bit count; a word with
+// another tag counts as zero.  Every failed
+// exchange means another segment's add went in, so the loop ends.
+__device__ __forceinline__ bool arrive(unsigned long long* cp, unsigned long long tag, uint32_t units, uint32_t total) {
+  unsigned long long old = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const uint32_t done = (old >> 24) == tag ? (uint32_t)(old & 0xFFFFFFu) : 0u;
+    const uint32_t now = done + units;
+    const unsigned long long nw = now == total ? 0ull : (tag << 24) | now;
+    if (__hip_atomic_compare_exchange_weak(cp, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT))
+      return now == total;
+  }
+}
+// Agent-scope (coherence point, L2-bypassing) float store and load.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+

@@ -12,6 +12,12 @@ namespace s8kv {
 
 void set_error(const char* fmt, ...);
 
+// A fresh 40-bit launch tag (never zero) for arrival counters.
+unsigned long long next_launch_tag();
+
+// Compute units of the current device (cached per device id).
+int device_cus();
+
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
 inline int log2i(int64_t x) {
