@@ -115,14 +115,12 @@ __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, 
   if constexpr (LPR > 4) amax = fmaxf(amax, xor_partner<4>(amax));
   if constexpr (LPR > 8) amax = fmaxf(amax, xor_partner<8>(amax));
   const float scale = amax / 127.0f;
-  const float rscale = 1.0f / scale;  // (inf for a zero row: rtn_i8_recip returns 0 there)
+  const float rscale = rtn_rscale(scale);
   uint32_t w[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    uint32_t v = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v |= ((uint32_t)rtn_i8_recip(y[4 * k + i], scale, rscale) & 0xFFu) << (8 * i);
-    w[k] = v;
+    w[k] = pack_low_bytes(rtn_i8_biased(y[4 * k], scale, rscale), rtn_i8_biased(y[4 * k + 1], scale, rscale),
+                          rtn_i8_biased(y[4 * k + 2], scale, rscale), rtn_i8_biased(y[4 * k + 3], scale, rscale));
   }
   if (live) {
     bstore128(u32x4_t{w[0], w[1], w[2], w[3]}, qbuf, byte_off);
@@ -134,9 +132,12 @@ __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, 
 // 128 = 8 lanes): the block's L2 norm adds the fp32 squares in the order of
 // lloydmax3_encode_row (halves folded at h = 64, 32, 16 across lanes ^ 4,
 // ^ 2, ^ 1, then h = 8 .. 1 in-lane), correctly rounded sqrt; u = v / norm
-// (0 for a zero norm); code = first index minimising |u - c_j|.  Lanes 2g
-// and 2g + 1 hold elements 32g .. 32g + 31: each builds 16 bits of the three
-// bit-plane words 3g + b, and the even lane stores them.
+// (0 for a zero norm) as the Markstein quotient from the block's reciprocal,
+// which equals the IEEE quotient for an fp16 v and any fp32 norm (checked for
+// every pair of significands); code = first index minimising |u - c_j|, by
+// lloyd3_search when the codebook allows it, else by the sequential scan.
+// Lanes 2g and 2g + 1 hold elements 32g .. 32g + 31: each builds 16 bits of
+// the three bit-plane words 3g + b, and the even lane stores them.
 template <int D>
 __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool live, int li, const float (&cb)[8],
                                                      rsrc_t vbuf, uint32_t word_off, rsrc_t nbuf, uint32_t norm_off) {
@@ -155,22 +156,41 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
     for (int i = 0; i < h; ++i) s[i] = s[i] + s[i + h];
   }
   const float nrm = __builtin_sqrtf(s[0]);
-  uint32_t pw[3] = {0u, 0u, 0u};
+  const float rn = rtn_rscale(nrm);  // 1 / norm, 0 for a zero norm (then u = 0)
+  float u[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const float u = nrm > 0.0f ? x[i] / nrm : 0.0f;
-    float best = fabsf(u - cb[0]);
-    uint32_t c = 0;
+    const float q0 = materialize(x[i] * rn);
+    const float r = __builtin_fmaf(-q0, nrm, x[i]);
+    u[i] = __builtin_fmaf(r, rn, q0);
+  }
+  // bit i of pw[b] = bit b of element i's code (elements shifted in from 15 down)
+  uint32_t pw[3] = {0u, 0u, 0u};
+  if (lloyd3_search_ok(cb)) {
 #pragma unroll
-    for (int j = 1; j < 8; ++j) {
-      const float d = fabsf(u - cb[j]);
-      if (d < best) {
-        best = d;
-        c = (uint32_t)j;
-      }
+    for (int i = 15; i >= 0; --i) {
+      bool b2, b1, b0;
+      lloyd3_search(u[i], cb, b2, b1, b0);
+      pw[0] = (pw[0] << 1) | (uint32_t)b0;
+      pw[1] = (pw[1] << 1) | (uint32_t)b1;
+      pw[2] = (pw[2] << 1) | (uint32_t)b2;
     }
+  } else {
 #pragma unroll
-    for (int b = 0; b < 3; ++b) pw[b] |= ((c >> b) & 1u) << i;
+    for (int i = 0; i < 16; ++i) {
+      float best = fabsf(u[i] - cb[0]);
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 1; j < 8; ++j) {
+        const float d = fabsf(u[i] - cb[j]);
+        if (d < best) {
+          best = d;
+          c = (uint32_t)j;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 3; ++b) pw[b] |= ((c >> b) & 1u) << i;
+    }
   }
   uint32_t w[3];
 #pragma unroll

@@ -87,14 +87,16 @@ __device__ __forceinline__ float max_x32(float x) { const LanePair p = lane_pair
 __device__ __forceinline__ float sum_x16(float x) { const LanePair p = lane_pair16(x); return p.a + p.b; }
 __device__ __forceinline__ float sum_x32(float x) { const LanePair p = lane_pair32(x); return p.a + p.b; }
 // Walsh-Hadamard butterfly across lane ^ 16 (^ 32): lanes with the bit clear
-// get x + partner, lanes with it set get partner - x.
+// get x + partner, lanes with it set get partner - x.  One FMA with a per-lane
+// sign: fma(+1, b, a) = RN(a + b) and fma(-1, b, a) = RN(a - b), signed zeros
+// included, so the result equals the add / subtract pair bit for bit.
 __device__ __forceinline__ float butterfly_x16(float x, int lane) {
   const LanePair p = lane_pair16(x);
-  return (lane & 16) ? p.a - p.b : p.a + p.b;
+  return __builtin_fmaf((lane & 16) ? -1.0f : 1.0f, p.b, p.a);
 }
 __device__ __forceinline__ float butterfly_x32(float x, int lane) {
   const LanePair p = lane_pair32(x);
-  return (lane & 32) ? p.a - p.b : p.a + p.b;
+  return __builtin_fmaf((lane & 32) ? -1.0f : 1.0f, p.b, p.a);
 }
 
 // Walsh-Hadamard butterfly across lane ^ M on the VALU or the LDS swizzle
@@ -121,7 +123,7 @@ __device__ __forceinline__ float butterfly_xor(float x, int lane) {
     return butterfly_x32(x, lane);
   } else {
     const float p = xor_partner<M>(x);
-    return (lane & M) ? p - x : x + p;
+    return __builtin_fmaf((lane & M) ? -1.0f : 1.0f, x, p);  // x + p, or p - x
   }
 }
 
@@ -185,20 +187,40 @@ __device__ __forceinline__ int rtn_i8(float y, float scale) {
   return (int)q;
 }
 
-// rtn_i8 with the quotient from a per-row reciprocal: rscale = 1 / scale
-// (IEEE), q0 = RN(y * rscale), the residual y - q0 * scale exactly by FMA, and
-// one FMA correction q0 + residual * rscale (Markstein's division).  For the
-// append's operands -- y an fp16 value and scale = RN(m / 127) for an fp16
-// absmax m >= |y| -- the corrected quotient equals the IEEE quotient y / scale
-// for every such pair (an exhaustive check over all 1.0e9 of them), so the
-// codes equal rtn_i8's.
-__device__ __forceinline__ int rtn_i8_recip(float y, float scale, float rscale) {
-  if (!(scale > 0.0f)) return 0;
+// 1.5 * 2^23: adding it to a |t| < 2^22 rounds t half-even to an integer n
+// (the fp32 spacing there is 1) and leaves n in the low bits of the sum's
+// encoding, kRoundMagicBits + n; its low byte is n as an int8.
+constexpr float kRoundMagic = 12582912.0f;
+constexpr uint32_t kRoundMagicBits = 0x4B400000u;
+
+// The reciprocal rtn_i8_recip takes: 1 / scale (IEEE), or 0 for a zero scale
+// (an all-zero row), which makes every quotient of that row 0 without a
+// per-element test.
+__device__ __forceinline__ float rtn_rscale(float scale) { return scale > 0.0f ? 1.0f / scale : 0.0f; }
+
+// rtn_i8 with the quotient from a per-row reciprocal: rscale = rtn_rscale(scale),
+// q0 = RN(y * rscale), the residual y - q0 * scale exactly by FMA, and one FMA
+// correction q0 + residual * rscale (Markstein's division).  For the append's
+// operands -- y an fp16 value and scale = RN(m / 127) for an fp16 absmax
+// m >= |y| -- the corrected quotient equals the IEEE quotient y / scale for
+// every such pair and rounds to an integer in [-127, 127] (an exhaustive check
+// over all 1.0e9 of them), so the codes equal rtn_i8's without its clamp.
+// Returns kRoundMagicBits + code (rtn_i8_biased; low byte = the int8) or the
+// code.  A NaN quotient (a row holding inf or NaN) gives code 0.
+__device__ __forceinline__ uint32_t rtn_i8_biased(float y, float scale, float rscale) {
   const float q0 = materialize(y * rscale);
   const float r = __builtin_fmaf(-q0, scale, y);
-  float q = __builtin_rintf(__builtin_fmaf(r, rscale, q0));
-  q = fminf(127.0f, fmaxf(-127.0f, q));
-  return (int)q;
+  return __builtin_bit_cast(uint32_t, __builtin_fmaf(r, rscale, q0) + kRoundMagic);
+}
+__device__ __forceinline__ int rtn_i8_recip(float y, float scale, float rscale) {
+  return (int)(rtn_i8_biased(y, scale, rscale) - kRoundMagicBits);
+}
+
+// Low bytes of four words, in order, as one word (three byte permutes).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0C0C0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // ---------------------------------------------------------------------------
@@ -264,10 +286,38 @@ __device__ __forceinline__ float rtn_row(const float (&y)[RowLayout<D>::E], int 
   for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(y[j]));
   amax = wave_max(amax);
   const float scale = amax / 127.0f;
-  const float rscale = 1.0f / scale;
+  const float rscale = rtn_rscale(scale);
 #pragma unroll
   for (int j = 0; j < E; ++j) q[j] = rtn_i8_recip(y[j], scale, rscale);
   return scale;
+}
+
+// Codebooks for which lloyd3_search returns the first index minimising
+// fl|u - c_j| for every |u| <= 1 (u = v / norm with norm >= |v|), or a NaN u
+// (index 0, as the sequential scan): finite, c_0 >= -4, c_7 <= 4, ascending
+// with neighbours at least 2^-19 apart.  Then for c_{j-1} < c_j <= u the
+// exact distances differ by more than 2^-20 while each rounds by at most
+// 2^-22, so the fp32 distances fall strictly up to the last c_j <= u and do
+// not fall after the first minimum: "entry j is strictly nearer than entry
+// j - 1" holds exactly for j = 1 .. m (m the first minimising index) and
+// fails above m, so m is found by a binary search over j.
+__device__ __forceinline__ bool lloyd3_search_ok(const float (&cb)[8]) {
+  bool ok = cb[0] >= -4.0f && cb[7] <= 4.0f;
+#pragma unroll
+  for (int j = 1; j < 8; ++j) ok = ok && (cb[j] - cb[j - 1] >= 0x1p-19f);
+  return ok;
+}
+
+// The bits of m for an 8-entry codebook accepted by lloyd3_search_ok: three
+// tests of "entry j strictly nearer than entry j - 1" at j = 4, 4 b2 + 2 and
+// 4 b2 + 2 b1 + 1, with the same fp32 distances as the sequential scan.
+__device__ __forceinline__ void lloyd3_search(float u, const float (&cb)[8], bool& b2, bool& b1, bool& b0) {
+  b2 = fabsf(u - cb[4]) < fabsf(u - cb[3]);
+  const float c62 = b2 ? cb[6] : cb[2], c51 = b2 ? cb[5] : cb[1];
+  const float c73 = b2 ? cb[7] : cb[3], c40 = b2 ? cb[4] : cb[0];
+  b1 = fabsf(u - c62) < fabsf(u - c51);
+  const float hi = b1 ? c73 : c51, lo = b1 ? c62 : c40;
+  b0 = fabsf(u - hi) < fabsf(u - lo);
 }
 
 // 3-bit Lloyd-Max encoding of one V row spread over the wave (RowLayout

@@ -183,6 +183,36 @@ def test_append_k8v3_input_views(d):
             assert np.array_equal(_np(a).view(np.uint8), b.view(np.uint8)), f"{name}: {what} differs"
 
 
+@pytest.mark.parametrize("kind", ["permuted", "wide", "repeated"])
+def test_append_k8v3_codebook_outside_search_condition(kind):
+    """Codebooks the three-comparison search does not accept (not ascending,
+    entries beyond +-4, a repeated entry) take the sequential scan: the bytes
+    still equal the oracle's first-minimum codes, from aligned and unaligned
+    inputs."""
+    cb = CODEBOOK.copy()
+    if kind == "permuted":
+        cb = cb[[3, 0, 6, 1, 7, 2, 5, 4]]
+    elif kind == "wide":
+        cb = (cb * 40.0).astype(np.float32)
+    else:
+        cb[5] = cb[4]
+    d, hkv, bs = 128, 2, 16
+    case = make_case(77, 2, 4, hkv, d, bs, [40, 9], outlier_channels=2)
+    ref = oracle_fill_k8v3(case, cb)
+    t = case.k.shape[0]
+    flat = torch.zeros(2 * t * hkv * d + 1, dtype=torch.float16, device=DEV)
+    k_odd = flat[1:1 + t * hkv * d].view(t, hkv, d)
+    v_odd = flat[1 + t * hkv * d:].view(t, hkv, d)
+    k_odd.copy_(_t(case.k))
+    v_odd.copy_(_t(case.v))
+    for name, (kk, vv) in {"aligned": (_t(case.k), _t(case.v)), "unaligned": (k_odd, v_odd)}.items():
+        g = _gpu_k8v3_cache(case)
+        ops.quantize_kv_write_paged_k8v3(kk, vv, *g, _t(cb), _t(case.slots))
+        torch.cuda.synchronize()
+        for what, a, b in zip(("k_cache", "k_scale", "v_packed", "v_norm"), g, ref):
+            assert np.array_equal(_np(a).view(np.uint8), b.view(np.uint8)), f"{kind} {name}: {what} differs"
+
+
 def test_append_k8v3_zero_and_tie_rows():
     d, hkv, bs = 128, 1, 4
     rows = [np.zeros(d), np.ones(d), np.r_[np.ones(64), -np.ones(64)], np.linspace(-3, 3, d)]
