@@ -211,15 +211,15 @@ def l2_norm_blocks(x: np.ndarray, block_size: int) -> np.ndarray:
     """Per-block fp32 L2 norm over the last axis.
 
     CHOICE (fixed reduction order, matched by the GPU): squares in fp32 (exact
-    for fp16 inputs), then repeatedly add the upper half onto the lower half
-    (``s[:h] + s[h:]``) until one element is left, then a correctly rounded
-    fp32 sqrt."""
+    for fp16 inputs), then a pairwise tree over neighbours: repeatedly add
+    each even-indexed partial sum to the odd one after it
+    (``s[0::2] + s[1::2]``) until one element is left, then a correctly
+    rounded fp32 sqrt."""
     xf = np.asarray(x, dtype=F32)
     d = xf.shape[-1]
     s = (xf * xf).reshape(*xf.shape[:-1], d // block_size, block_size)
     while s.shape[-1] > 1:
-        h = s.shape[-1] // 2
-        s = s[..., :h] + s[..., h:]
+        s = s[..., 0::2] + s[..., 1::2]
     return np.sqrt(s[..., 0]).astype(F32)
 
 

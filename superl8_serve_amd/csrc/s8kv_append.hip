@@ -128,10 +128,19 @@ __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, 
   }
 }
 
+// 2 w + b in one add with carry-in (the lanes' b as a wave mask).
+__device__ __forceinline__ uint32_t shift_in_bit(uint32_t w, bool b) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(b);
+  uint32_t r;
+  uint64_t carry_out;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(w), "s"(m));
+  return r;
+}
+
 // 3-bit Lloyd-Max V of the lane's 16 values (head_dim 128 or 256, blocks of
 // 128 = 8 lanes): the block's L2 norm adds the fp32 squares in the order of
-// lloydmax3_encode_row (halves folded at h = 64, 32, 16 across lanes ^ 4,
-// ^ 2, ^ 1, then h = 8 .. 1 in-lane), correctly rounded sqrt; u = v / norm
+// lloydmax3_encode_row (a pairwise tree over neighbours: levels h = 1 .. 8
+// in-lane, h = 16, 32, 64 across lanes ^ 1, ^ 2, ^ 4), correctly rounded sqrt; u = v / norm
 // (0 for a zero norm) as the Markstein quotient from the block's reciprocal,
 // which equals the IEEE quotient for an fp16 v and any fp32 norm (checked for
 // every pair of significands); code = first index minimising |u - c_j|, by
@@ -145,17 +154,15 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
 #pragma unroll
   for (int i = 0; i < 16; ++i) s[i] = x[i] * x[i];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<4>(s[i]);
+  for (int h = 1; h < 16; h <<= 1) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<2>(s[i]);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = s[i] + xor_partner<1>(s[i]);
-#pragma unroll
-  for (int h = 8; h >= 1; h >>= 1) {
-#pragma unroll
-    for (int i = 0; i < h; ++i) s[i] = s[i] + s[i + h];
+    for (int i = 0; i < 16; i += 2 * h) s[i] = s[i] + s[i + h];
   }
-  const float nrm = __builtin_sqrtf(s[0]);
+  float t = s[0];  // the lane's 16 elements; partners hold the neighbouring groups
+  t = t + xor_partner<1>(t);
+  t = t + xor_partner<2>(t);
+  t = t + xor_partner<4>(t);
+  const float nrm = __builtin_sqrtf(t);
   const float rn = rtn_rscale(nrm);  // 1 / norm, 0 for a zero norm (then u = 0)
   float u[16];
 #pragma unroll
@@ -171,9 +178,9 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
     for (int i = 15; i >= 0; --i) {
       bool b2, b1, b0;
       lloyd3_search(u[i], cb, b2, b1, b0);
-      pw[0] = (pw[0] << 1) | (uint32_t)b0;
-      pw[1] = (pw[1] << 1) | (uint32_t)b1;
-      pw[2] = (pw[2] << 1) | (uint32_t)b2;
+      pw[0] = shift_in_bit(pw[0], b0);
+      pw[1] = shift_in_bit(pw[1], b1);
+      pw[2] = shift_in_bit(pw[2], b2);
     }
   } else {
 #pragma unroll

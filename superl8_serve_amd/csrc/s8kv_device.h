@@ -322,8 +322,8 @@ __device__ __forceinline__ void lloyd3_search(float u, const float (&cb)[8], boo
 
 // 3-bit Lloyd-Max encoding of one V row spread over the wave (RowLayout
 // lanes; head_dim 128 or 256, lloyd_block 128): per-128 block L2 norm (fp32
-// squares, fold the two halves, then butterflies 32..1, correctly rounded
-// sqrt), u = v / norm (0 for a zero norm), code = first index minimising
+// squares summed by a pairwise tree over neighbours -- butterflies 1..32 on
+// each half, then the two halves -- correctly rounded sqrt), u = v / norm (0 for a zero norm), code = first index minimising
 // |u - c_j| in fp32, bit-plane words (word 3g+b holds bit b of the codes of
 // elements 32g..32g+31, element 32g+i at bit i).  Lane w < 3D/32 gets word w,
 // lane nb < D/128 gets norm nb.
@@ -336,12 +336,17 @@ __device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<
   float norm[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    // Block nb holds elements 128nb + {lane, lane+64}: fold the halves, then
-    // butterflies 32..1 -- the order the CPU restatement uses.
-    float s = x[2 * nb] * x[2 * nb] + x[2 * nb + 1] * x[2 * nb + 1];
+    // Block nb holds elements 128nb + {lane, lane+64}: the tree's levels
+    // h = 1 .. 32 are butterflies within each half (lane l gets its group's
+    // two partial sums added in either order -- the same fp32 value), h = 64
+    // adds the halves -- the order the CPU restatement uses.
+    float s0 = x[2 * nb] * x[2 * nb], s1 = x[2 * nb + 1] * x[2 * nb + 1];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s = s + shfl_xor_f(s, m);
-    norm[nb] = __builtin_sqrtf(s);
+    for (int m = 1; m <= 32; m <<= 1) {
+      s0 = s0 + shfl_xor_f(s0, m);
+      s1 = s1 + shfl_xor_f(s1, m);
+    }
+    norm[nb] = __builtin_sqrtf(s0 + s1);
   }
   uint32_t codes[E];
 #pragma unroll

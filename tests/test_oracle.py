@@ -205,6 +205,24 @@ def test_l2_norm_blocks():
     assert n.dtype == np.float32 and np.allclose(n, ref, rtol=2e-7)
 
 
+def test_l2_norm_blocks_summation_order():
+    """The squares are added by a pairwise tree over neighbours.  With 4096
+    at index 0 and ones at 64..127 every partial sum of that tree is exact
+    (2^24 + 64), while folding halves (s[:h] + s[h:]) absorbs two of the ones
+    into 2^24 by ties to even (2^24 + 62) and a left-to-right scan all of them
+    (2^24): three different fp32 norms."""
+    x = np.zeros((1, 128), np.float16)
+    x[0, 0] = 4096.0
+    x[0, 64:] = 1.0
+    n = O.l2_norm_blocks(x, 128)[0, 0]
+    want = np.float32(math.sqrt(2.0 ** 24 + 64))
+    assert n == want
+    assert want != np.float32(math.sqrt(2.0 ** 24 + 62)) and want != np.float32(4096.0)
+    # the same block in the second half of a 256-wide row, after a zero block
+    y = np.concatenate([np.zeros((1, 128), np.float16), x], axis=1)
+    assert O.l2_norm_blocks(y, 128)[0].tolist() == [0.0, float(want)]
+
+
 def test_quantize_lloydmax_is_nearest_codeword():
     rng = np.random.default_rng(5)
     cb = O.gaussian_codebook()
