@@ -193,6 +193,24 @@ int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads
                      int max_context_len, float scale, void* out, void* stream);
 
 /*
+ * s8kv_verify_int8 over the K8V3 cache (int8 K, 3-bit Lloyd-Max V): the
+ * one-launch form of the reference's chain verify on a k8v3 cache, which runs
+ * S sequential decodes that dispatch to attn_paged_decode_k8v3
+ * (gqa_attention.py:259-277, kv_cache.py:1168-1188), and of its k8v3 chunked
+ * prefill (read_dense, kv_cache.py:1233-1299, then attn_int8_fwd).  V is
+ * codebook[code] * block norm; v_packed int32 [num_blocks, Hkv, bs, 3*D/32],
+ * v_norm fp32 [num_blocks, Hkv, bs, D/128], v_codebook fp32 [8].  Other
+ * arguments as s8kv_verify_int8; head_dim 128 or 256 and lloyd_block 128
+ * (the reference's own k8v3 gate, kv_cache.py:691-701).
+ */
+int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
+                     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s, const int8_t* k_cache,
+                     const float* k_scale, const int32_t* v_packed, const float* v_norm, const float* v_codebook,
+                     int lloyd_block, int64_t num_blocks, int block_size, const int32_t* block_table,
+                     int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                     const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its kernel with HIP events stamped with the

@@ -263,17 +263,6 @@ __device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&d
   }
 }
 
-// fp16 lookup of 4 three-bit codes held as bytes of `sel` through the byte
-// tables (lo/hi bytes of the 8 fp16 codebook entries).
-__device__ __forceinline__ u32x2_t cb_lookup4(uint32_t sel, uint32_t lo03, uint32_t lo47, uint32_t hi03, uint32_t hi47) {
-  uint32_t lo = __builtin_amdgcn_perm(lo47, lo03, sel);
-  uint32_t hi = __builtin_amdgcn_perm(hi47, hi03, sel);
-  u32x2_t r;
-  r.x = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-  r.y = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-  return r;
-}
-
 template <int D, bool K8V3>
 struct TileIO {
   using C = DecCfg<D, K8V3>;
@@ -724,13 +713,13 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
               {
                 const int i = 4 * q4;
                 const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-                const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+                const u32x2_t r = codebook_lookup4(sel, tlo03, tlo47, thi03, thi47);
                 o.x = r.x; o.y = r.y;
               }
               {
                 const int i = 4 * q4 + 4;
                 const uint32_t sel = spread4(w0 >> i) | (spread4(w1 >> i) << 1) | (spread4(w2 >> i) << 2);
-                const u32x2_t r = cb_lookup4(sel, tlo03, tlo47, thi03, thi47);
+                const u32x2_t r = codebook_lookup4(sel, tlo03, tlo47, thi03, thi47);
                 o.z = r.x; o.w = r.y;
               }
               *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;

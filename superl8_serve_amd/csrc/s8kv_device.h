@@ -393,6 +393,18 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
   return ((x & 0xFu) * 0x00204081u) & 0x01010101u;
 }
 
+// fp16 lookup of 4 three-bit codes held as bytes of `sel` through byte tables
+// (lo / hi bytes of the 8 fp16 codebook entries: entries 0..3 and 4..7).
+__device__ __forceinline__ u32x2_t codebook_lookup4(uint32_t sel, uint32_t lo03, uint32_t lo47, uint32_t hi03,
+                                                    uint32_t hi47) {
+  const uint32_t lo = __builtin_amdgcn_perm(lo47, lo03, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(hi47, hi03, sel);
+  u32x2_t r;
+  r.x = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  r.y = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  return r;
+}
+
 }  // namespace s8kv
 
 // Arrival at a counter word shared by the workgroups that each stored one

@@ -1,4 +1,4 @@
-// Multi-query verify attention over the paged int8 cache: tree verify (each
+// Multi-query verify attention over the paged int8 or K8V3 cache: tree verify (each
 // draft query sees the prefix plus its ancestors in the draft tree) and
 // chunked prefill / chain verify (query s sees the prefix plus drafts 0..s).
 //
@@ -6,8 +6,9 @@
 // (sequence, KV head) pair -- row r is query position r / G of q head
 // h*G + r % G -- and streams the pair's keys in 32-key tiles.  Each tile's K
 // and V rows are loaded once per workgroup, converted int8 -> fp16 (exact) on
-// the way into LDS (double-buffered), and shared by the 4 waves; a wave owns 16
-// query rows, the 16 columns of its MFMA tiles:
+// the way into LDS (double-buffered), and shared by the 4 waves (K8V3: V's
+// 3-bit codes become the fp16 codebook entries, as in the decode kernel); a
+// wave owns 16 query rows, the 16 columns of its MFMA tiles:
 //   QK  : S^T[key][row] on MFMA 16x16x32 f16, A = K rows from LDS, B = the
 //         rotated, pre-scaled q split into fp16 hi + lo (two MFMAs).
 //   mask: keys below the prefix are visible to every row; draft key i is
@@ -15,7 +16,7 @@
 //         tree mask is set (tree).
 //   softmax: online, log2 domain, lazy max (as the decode kernel).
 //   PV  : O^T[dim][row] on MFMA, A = V^T via ds_read_b64_tr_b16 from LDS,
-//         B = P * v_scale as fp16 hi + lo.
+//         B = P * v_scale (K8V3: P * the key's block norm) as fp16 hi + lo.
 // Rows past a sequence's query count are written as zeros.
 #include <type_traits>
 
@@ -38,7 +39,7 @@ constexpr float kMaxSlack = 8.0f;
 // it by more than kMaxSlack, which makes the first visible tile rescale (by 0).
 constexpr float kMaxInit = -1.0e30f;
 
-template <int D>
+template <int D, bool K8V3>
 struct Cfg {
   static constexpr int KCH = D / 4;      // dims per lane per key row (MFMA A / B chunk of the lane group)
   static constexpr int NQK = D / 32;     // QK MFMAs per 16-key subtile
@@ -47,9 +48,15 @@ struct Cfg {
   static constexpr int VROW = 2 * D + 32;  // LDS pitch of an fp16 V row (bytes)
   static constexpr int KBYTES = kTile * KROW;
   static constexpr int VBYTES = kTile * VROW;
-  static constexpr int BUF = KBYTES + VBYTES + 2 * kTile * 4;  // K, V, k_scale, v_scale
+  static constexpr int NB = K8V3 ? D / 128 : 1;  // V scales per key: the int8 row scale, or K8V3 block norms
+  static constexpr int NG = D / 32;              // K8V3: 32-value code groups per key (3 packed words each)
+  static constexpr int WORDS = 3 * NG;           // K8V3: packed words per key
+  static constexpr int SBYTES = (1 + NB) * kTile * 4;  // k_scale, then the V scales of each block
+  static constexpr int BUF = KBYTES + VBYTES + SBYTES;
   static constexpr int CHUNKS = kTile * D / 16;                 // 16-byte int8 chunks per K (or V) tile
   static constexpr int LOADS = (CHUNKS + kThreads - 1) / kThreads;
+  static constexpr int VJOBS = kTile * NG;                       // K8V3: code groups per tile
+  static_assert(!K8V3 || VJOBS <= kThreads, "one K8V3 code group per thread");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
 };
 
@@ -59,9 +66,10 @@ struct VerifyArgs {
   int batch, num_q_heads, num_kv_heads, group, max_queries;
   const void* k_cache;
   const float* k_scale;
-  const void* v_cache;
-  const float* v_scale;
-  uint32_t kc_bytes, ks_bytes;
+  const void* v_cache;        // int8 V, or K8V3 packed code words
+  const float* v_scale;       // int8 V scales, or K8V3 block norms
+  const float* v_codebook;    // K8V3: fp32 [8]
+  uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
   const int32_t* block_table;
   int64_t bt_stride;
   const int32_t* prefix_lens;
@@ -78,9 +86,9 @@ struct VerifyArgs {
 // transpose-read rows (keys 4g..4g+3 and 16+4g..16+4g+3) are rows 8g..8g+7.
 __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-template <int D>
+template <int D, bool K8V3>
 __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
-  using C = Cfg<D>;
+  using C = Cfg<D, K8V3>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
 
@@ -161,9 +169,20 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
-  const rsrc_t vc = make_rsrc(a.v_cache, a.kc_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
-  const rsrc_t vs = make_rsrc(a.v_scale, a.ks_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
+  // K8V3 codebook byte tables (fp16 of the fp32 codebook; the decode kernel's)
+  uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
+  if constexpr (K8V3) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
+      const uint32_t lw = hb & 0xFFu, hw = hb >> 8;
+      if (i < 4) { tlo03 |= lw << (8 * i); thi03 |= hw << (8 * i); }
+      else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
+    }
+  }
   const int bs_log2 = a.bs_log2;
   const uint32_t bsm = (1u << bs_log2) - 1u;
   const uint32_t hkv = (uint32_t)a.num_kv_heads;
@@ -184,7 +203,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)kk & bsm);
     };
 
-    // ---- cooperative tile load: int8 K/V chunks and scales -> registers ----
+    // ---- cooperative tile load: int8 K/V chunks (K8V3: a code group's three
+    // words per thread) and scales -> registers ----
     struct TileRegs {
       u32x4_t k[C::LOADS], v[C::LOADS];
       float s;
@@ -197,12 +217,26 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
           const uint32_t row = row_of(base + tt);
           R.k[i] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
-          R.v[i] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
+          if constexpr (!K8V3) R.v[i] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
         }
       }
-      if (tid < 2 * kTile) {
+      if constexpr (K8V3) {
+        if (tid < C::VJOBS) {
+          const int tt = tid / C::NG, gi = tid % C::NG;
+          const uint32_t off = row_of(base + tt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
+          R.v[0].x = bload32(vc, off);
+          R.v[0].y = bload32(vc, off + 4);
+          R.v[0].z = bload32(vc, off + 8);
+        }
+      }
+      if (tid < (1 + C::NB) * kTile) {  // k_scale of key tid, then block (tid/32 - 1)'s V scale
         const uint32_t row = row_of(base + (tid & (kTile - 1)));
-        R.s = __builtin_bit_cast(float, bload32(tid < kTile ? ks : vs, row * 4u));
+        if constexpr (C::NB == 1) {
+          R.s = __builtin_bit_cast(float, bload32(tid < kTile ? ks : vs, row * 4u));
+        } else {
+          const int nb = tid / kTile - 1;
+          R.s = __builtin_bit_cast(float, bload32(nb < 0 ? ks : vs, nb < 0 ? row * 4u : (row * C::NB + nb) * 4u));
+        }
       }
     };
     // registers -> LDS buffer, converting int8 to fp16
@@ -219,13 +253,33 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           const half8_t k1 = i8x8_to_f16(u32x2_t{R.k[i].z, R.k[i].w});
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = k0;
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = k1;
-          const half8_t v0 = i8x8_to_f16(u32x2_t{R.v[i].x, R.v[i].y});
-          const half8_t v1 = i8x8_to_f16(u32x2_t{R.v[i].z, R.v[i].w});
-          *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32) = v0;
-          *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32 + 16) = v1;
+          if constexpr (!K8V3) {
+            const half8_t v0 = i8x8_to_f16(u32x2_t{R.v[i].x, R.v[i].y});
+            const half8_t v1 = i8x8_to_f16(u32x2_t{R.v[i].z, R.v[i].w});
+            *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32) = v0;
+            *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32 + 16) = v1;
+          }
         }
       }
-      if (tid < 2 * kTile) sb[tid] = R.s;
+      if constexpr (K8V3) {  // 32 codes of one group -> 32 fp16 codebook entries
+        if (tid < C::VJOBS) {
+          const int tt = tid / C::NG, gi = tid % C::NG;
+          const uint32_t w0 = R.v[0].x, w1 = R.v[0].y, w2 = R.v[0].z;
+          char* dst = vb + vrow_of(tt) * C::VROW + gi * 64;
+#pragma unroll
+          for (int q4 = 0; q4 < 8; q4 += 2) {
+            u32x4_t o;
+            const uint32_t sel0 = spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
+            const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
+                                  (spread4(w2 >> (4 * q4 + 4)) << 2);
+            const u32x2_t r0 = codebook_lookup4(sel0, tlo03, tlo47, thi03, thi47);
+            const u32x2_t r1 = codebook_lookup4(sel1, tlo03, tlo47, thi03, thi47);
+            o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+            *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
+          }
+        }
+      }
+      if (tid < (1 + C::NB) * kTile) sb[tid] = R.s;
     };
 
     // ---- one 32-key tile from LDS buffer `buf` ----
@@ -247,11 +301,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         }
         sc[s] = cacc;
       }
-      float4_t ksc[2], vsc[2];
+      float4_t ksc[2], vsc[2], vsc1[2];  // vsc1: K8V3 head_dim 256, the second block's norms
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         ksc[s] = *reinterpret_cast<const float4_t*>(sb + 16 * s + 4 * g);
         vsc[s] = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * s + 4 * g);
+        if constexpr (C::NB == 2) vsc1[s] = *reinterpret_cast<const float4_t*>(sb + 2 * kTile + 16 * s + 4 * g);
       }
       float pr[2][4];
       float mt = kNegInf;
@@ -281,7 +336,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
         m_run = m_new;
       }
-      half8_t pbh, pbl;
+      half8_t pbh, pbl, pbh1, pbl1;  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -293,6 +348,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           const _Float16 wh = (_Float16)w;
           pbh[4 * s + i] = wh;
           pbl[4 * s + i] = (_Float16)(w - (float)wh);
+          if constexpr (C::NB == 2) {
+            const float w1 = materialize(e * vsc1[s][i]);
+            const _Float16 wh1 = (_Float16)w1;
+            pbh1[4 * s + i] = wh1;
+            pbl1[4 * s + i] = (_Float16)(w1 - (float)wh1);
+          }
         }
       }
 #pragma unroll
@@ -304,8 +365,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + (r0 + 4) * C::VROW + colb));
         const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
         const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-        acc[n] = mfma16x16x32(va, pbh, acc[n]);
-        acc[n] = mfma16x16x32(va, pbl, acc[n]);
+        const bool second = C::NB == 2 && 16 * n >= 128;  // dims 128..255 of a K8V3 head_dim-256 key
+        acc[n] = mfma16x16x32(va, second ? pbh1 : pbh, acc[n]);
+        acc[n] = mfma16x16x32(va, second ? pbl1 : pbl, acc[n]);
       }
     };
 
@@ -356,12 +418,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   }
 }
 
-template <int D>
+template <int D, bool K8V3>
 static int launch(VerifyArgs& a, hipStream_t stream) {
-  using C = Cfg<D>;
+  using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -374,7 +436,7 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_kernel<D, K8V3>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
   return check_launch("s8kv_verify");
 }
 
@@ -383,14 +445,13 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
 
 using namespace s8kv;
 
-extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
-                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
-                                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
-                                const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
-                                int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
-  S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
-  if (batch == 0 || max_queries == 0) return S8KV_OK;
+// Checks and arguments shared by both layouts (everything but V).
+static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num_q_heads, int num_kv_heads,
+                        int head_dim, int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                        const int8_t* k_cache, const float* k_scale, int64_t num_blocks, int block_size,
+                        const int32_t* block_table, int64_t block_table_stride, const int32_t* prefix_lens,
+                        const int32_t* query_lens, const int64_t* tree_mask, int max_context_len, float scale,
+                        void* out) {
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
@@ -399,11 +460,10 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
   S8KV_REQUIRE(is_pow2(block_size) && block_size >= 4, S8KV_ERR_UNSUPPORTED,
                "verify: block_size %d must be a power of two >= 4", block_size);
   S8KV_REQUIRE(num_blocks > 0 && max_context_len >= 0, S8KV_ERR_INVALID, "verify: bad num_blocks/max_context_len");
-  S8KV_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && block_table && prefix_lens && out, S8KV_ERR_INVALID,
+  S8KV_REQUIRE(q && k_cache && k_scale && block_table && prefix_lens && out, S8KV_ERR_INVALID,
                "verify: null pointer argument");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "verify: per-layer cache exceeds 4 GiB");
-  verify::VerifyArgs a{};
   a.q = (const _Float16*)q;
   a.q_stride_b = q_stride_b;
   a.q_stride_h = q_stride_h;
@@ -415,8 +475,6 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
   a.max_queries = max_queries;
   a.k_cache = k_cache;
   a.k_scale = k_scale;
-  a.v_cache = v_cache;
-  a.v_scale = v_scale;
   a.kc_bytes = (uint32_t)(rows * head_dim);
   a.ks_bytes = (uint32_t)(rows * 4);
   a.block_table = block_table;
@@ -429,11 +487,60 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
   a.n_qblocks = (a.group * max_queries + verify::kRowsPerWg - 1) / verify::kRowsPerWg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
+  return S8KV_OK;
+}
+
+extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                                const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
+  S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
+  if (batch == 0 || max_queries == 0) return S8KV_OK;
+  verify::VerifyArgs a{};
+  const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                              q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
+  if (rc != S8KV_OK) return rc;
+  S8KV_REQUIRE(v_cache && v_scale, S8KV_ERR_INVALID, "verify: null pointer argument");
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.vc_bytes = a.kc_bytes;
+  a.vs_bytes = a.ks_bytes;
   hipStream_t s = (hipStream_t)stream;
   switch (head_dim) {
-    case 64: return verify::launch<64>(a, s);
-    case 128: return verify::launch<128>(a, s);
-    case 256: return verify::launch<256>(a, s);
+    case 64: return verify::launch<64, false>(a, s);
+    case 128: return verify::launch<128, false>(a, s);
+    case 256: return verify::launch<256, false>(a, s);
   }
   return S8KV_ERR_UNSUPPORTED;
+}
+
+extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
+                                const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
+                                int max_context_len, float scale, void* out, void* stream) {
+  S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
+  if (batch == 0 || max_queries == 0) return S8KV_OK;
+  S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
+               "verify k8v3: head_dim %d not in {128, 256}", head_dim);
+  S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "verify k8v3: lloyd_block %d != 128", lloyd_block);
+  verify::VerifyArgs a{};
+  const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                              q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
+  if (rc != S8KV_OK) return rc;
+  S8KV_REQUIRE(v_packed && v_norm && v_codebook, S8KV_ERR_INVALID, "verify: null pointer argument");
+  const int64_t rows = num_blocks * num_kv_heads * block_size;
+  a.v_cache = v_packed;
+  a.v_scale = v_norm;
+  a.v_codebook = v_codebook;
+  a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
+  a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
+  hipStream_t s = (hipStream_t)stream;
+  return head_dim == 128 ? verify::launch<128, true>(a, s) : verify::launch<256, true>(a, s);
 }

@@ -27,6 +27,7 @@ __all__ = [
     "attn_paged_decode_append_k8v3",
     "decode_workspace_bytes",
     "attn_paged_verify",
+    "attn_paged_verify_k8v3",
     "copy_blocks",
 ]
 
@@ -326,31 +327,19 @@ def attn_paged_decode_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
     return out
 
 
-def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix_lens, block_size, *,
-                      query_lens=None, tree_mask=None, max_context_len, scale):
-    """Multi-query attention of draft / chunk queries over the int8 paged cache.
-
-    ``q``: fp16 ``[B, Hq, S, D]`` (any strides with D contiguous, e.g. the
-    ``[B, S, Hq, D] -> [B, Hq, S, D]`` transpose view).  Row b's S drafts sit
-    at cache positions ``prefix_lens[b] ..`` (appended beforehand).  Query s
-    sees the prefix plus draft i when ``i <= s`` (``tree_mask`` None: chain
-    verify, gqa_attention.py:217-292, and bottom-right causal chunked prefill,
-    gqa_attention.py:105-129) or when bit i of ``tree_mask[b, s]`` (int64
-    ``[B, S]``) is set (tree verify).  Queries ``s >= query_lens[b]`` give
-    zeros.  Returns fp16 ``[B, Hq, S, D]``."""
+def _verify_inputs(q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask,
+                   max_context_len):
+    """Checks and views shared by both cache layouts; returns the prepared
+    arguments and the output tensor."""
     _on_gpu("q", q, torch.float16)
     dev = q.device
     _on_gpu("k_cache", k_cache, torch.int8, dev)
     _on_gpu("k_scale", k_scale, torch.float32, dev)
-    _on_gpu("v_cache", v_cache, torch.int8, dev)
-    _on_gpu("v_scale", v_scale, torch.float32, dev)
     _on_gpu("block_table", block_table, torch.int32, dev)
     _on_gpu("prefix_lens", prefix_lens, torch.int32, dev)
     n, hkv, bs, d = _cache_geometry(k_cache)
     _require(int(block_size) == bs, f"block_size {block_size} does not match the cache ({bs})")
-    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
     _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
-    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
     _require(q.dim() == 4 and q.shape[3] == d, f"verify q must be [B, Hq, S, {d}], got {tuple(q.shape)}")
     if q.stride(3) != 1:
         q = q.contiguous()
@@ -377,16 +366,69 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     _require(0 <= max_context_len <= block_table.shape[1] * bs,
              f"max_context_len {max_context_len} exceeds the block table capacity {block_table.shape[1] * bs}")
     out = torch.empty((b, hq, s_, d), dtype=torch.float16, device=dev)
-    if b == 0 or s_ == 0:
+    # keep the contiguous copies alive until the launch is enqueued
+    keep = (q, block_table, prefix_lens, query_lens, tree_mask)
+    head = (q.data_ptr(), b, hq, hkv, d, s_, q.stride(0), q.stride(1), q.stride(2))
+    tail = (block_table.data_ptr(), block_table.stride(0), prefix_lens.data_ptr(), ql_ptr, tm_ptr, max_context_len)
+    return keep, head, tail, (n, hkv, bs, d), out
+
+
+def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix_lens, block_size, *,
+                      query_lens=None, tree_mask=None, max_context_len, scale):
+    """Multi-query attention of draft / chunk queries over the int8 paged cache.
+
+    ``q``: fp16 ``[B, Hq, S, D]`` (any strides with D contiguous, e.g. the
+    ``[B, S, Hq, D] -> [B, Hq, S, D]`` transpose view).  Row b's S drafts sit
+    at cache positions ``prefix_lens[b] ..`` (appended beforehand).  Query s
+    sees the prefix plus draft i when ``i <= s`` (``tree_mask`` None: chain
+    verify, gqa_attention.py:217-292, and bottom-right causal chunked prefill,
+    gqa_attention.py:105-129) or when bit i of ``tree_mask[b, s]`` (int64
+    ``[B, S]``) is set (tree verify).  Queries ``s >= query_lens[b]`` give
+    zeros.  Returns fp16 ``[B, Hq, S, D]``."""
+    keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
+        q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
+    dev = out.device
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
+    if out.shape[0] == 0 or out.shape[2] == 0:
         return out
     lib = _lib.load()
     rc = lib.s8kv_verify_int8(
-        q.data_ptr(), b, hq, hkv, d, s_, q.stride(0), q.stride(1), q.stride(2),
-        k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
-        block_table.data_ptr(), block_table.stride(0), prefix_lens.data_ptr(), ql_ptr, tm_ptr,
-        max_context_len, float(scale), out.data_ptr(), _stream(q),
+        *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+        *tail, float(scale), out.data_ptr(), _stream(keep[0]),
     )
     _lib.check(rc, "attn_paged_verify")
+    return out
+
+
+def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, prefix_lens, block_size,
+                           *, query_lens=None, tree_mask=None, max_context_len, scale):
+    """``attn_paged_verify`` over the K8V3 cache (int8 K, 3-bit Lloyd-Max V
+    ``codebook[code] * block norm``): one launch for what the reference
+    computes on a k8v3 cache with S sequential ``attn_paged_decode_k8v3``
+    calls (chain verify, gqa_attention.py:259-277) or ``read_dense`` plus
+    dense attention (chunked prefill).  head_dim 128 or 256, lloyd_block 128."""
+    keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
+        q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
+    dev = out.device
+    _on_gpu("v_packed", v_packed, torch.int32, dev)
+    _on_gpu("v_norm", v_norm, torch.float32, dev)
+    _on_gpu("v_codebook", v_codebook, torch.float32, dev)
+    _require(tuple(v_packed.shape) == (n, hkv, bs, d * 3 // 32) and v_packed.is_contiguous(),
+             "v_packed must be [N, Hkv, bs, D*3/32]")
+    lloyd_block = d // v_norm.shape[-1] if v_norm.dim() == 4 and v_norm.shape[-1] > 0 else 0
+    _require(tuple(v_norm.shape[:3]) == (n, hkv, bs) and v_norm.is_contiguous(), "v_norm must be [N, Hkv, bs, D/128]")
+    _require(v_codebook.numel() == 8 and v_codebook.is_contiguous(), "v_codebook must hold 8 contiguous entries")
+    if out.shape[0] == 0 or out.shape[2] == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_verify_k8v3(
+        *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
+        lloyd_block, n, bs, *tail, float(scale), out.data_ptr(), _stream(keep[0]),
+    )
+    _lib.check(rc, "attn_paged_verify_k8v3")
     return out
 
 

@@ -436,18 +436,22 @@ class PagedKVCache:
         """Multi-query attention of drafts (already written at positions
         ``prefix_lens[b] ..``): chain / chunk when `tree_mask` is None, else tree.
         ``q``: fp16 ``[B, Hq, S, D]``."""
-        if self.v_quant != "int8":
-            raise NotImplementedError("verify attention is implemented for the int8 layout")
         row = self._layer_row(layer)
         s = q.shape[2]
         ql = query_lens if query_lens is not None else [s] * len(slots)
         max_ctx = max((p + n for p, n in zip(prefix_lens, ql)), default=0)
-        return ops.attn_paged_verify(
-            q, self.k_cache[row], self.k_scale[row], self.v_cache[row], self.v_scale[row], self.block_table(slots),
-            torch.tensor(prefix_lens, dtype=torch.int32, device=self.device), self.block_size,
+        common = dict(
             query_lens=None if query_lens is None else torch.tensor(query_lens, dtype=torch.int32, device=self.device),
             tree_mask=tree_mask, max_context_len=min(max_ctx, self.max_blocks_per_seq * self.block_size),
             scale=scale)
+        bt = self.block_table(slots)
+        pl = torch.tensor(prefix_lens, dtype=torch.int32, device=self.device)
+        if self.v_quant == "lloydmax3":
+            return ops.attn_paged_verify_k8v3(
+                q, self.k_cache[row], self.k_scale[row], self.v_packed[row], self.v_norm[row], self.v_codebook[row],
+                bt, pl, self.block_size, **common)
+        return ops.attn_paged_verify(q, self.k_cache[row], self.k_scale[row], self.v_cache[row], self.v_scale[row],
+                                     bt, pl, self.block_size, **common)
 
     def read_dense(self, layer: int, slot: int, length: int, *, window: int | None = None,
                    dtype: torch.dtype = torch.float16) -> tuple[torch.Tensor, torch.Tensor]:

@@ -96,10 +96,11 @@ def test_decode_step_equals_write_then_attend(v_quant):
         assert torch.equal(getattr(caches[0], name), getattr(caches[1], name)), name
 
 
-def test_chunked_prefill_positions_and_verify():
+@pytest.mark.parametrize("v_quant", ["int8", "lloydmax3"])
+def test_chunked_prefill_positions_and_verify(v_quant):
     g = torch.Generator(device=DEV).manual_seed(1)
     hq, hkv, d, bs = 8, 2, 128, 16
-    c = PagedKVCache(1, 2, hkv, 512, d, device=DEV, block_size=bs)
+    c = PagedKVCache(1, 2, hkv, 512, d, device=DEV, block_size=bs, v_quant=v_quant)
     s = c.alloc()
     prefix, chunk = 100, 40
     c.ensure_capacity([s], [prefix + chunk])
@@ -112,7 +113,7 @@ def test_chunked_prefill_positions_and_verify():
     out = c.verify_attn(0, q, [s], [prefix], scale=0.1)
     bt = c.block_table([s]).cpu().numpy()
     ref = O.paged_verify(q.cpu().numpy(), _layer(c, 0), bt, np.array([prefix]), 0.1)
-    _close(out.float().cpu().numpy(), ref, "chunk via cache")
+    _close(out.float().cpu().numpy(), ref, f"{v_quant} chunk via cache")
 
 
 def test_prefix_share_copy_on_write():
