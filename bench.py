@@ -253,15 +253,17 @@ def calibrate_copy(mib: int) -> None:
 VERIFY_LAYERS = 4  # distinct per-layer storage, rotated so no layer is served from the Infinity Cache
 
 
-def verify_workload(kind: str, device):
+def verify_workload(kind: str, device, k8v3: bool = False):
     """Chunked prefill: 16 sequences sharing a 4096-token prefix (the prefix
     blocks appear in every block table) each append a 512-token chunk and
     attend bottom-right causally.  Tree verify: 32 sequences with 8192-token
     prefixes each append 16..64 draft nodes of a random tree (BFS, 1-4
-    children per expanded node) and attend prefix + ancestors.  Seeds 3 / 4."""
+    children per expanded node) and attend prefix + ancestors.  Seeds 3 / 4.
+    `k8v3`: the same over the K8V3 cache (int8 K, 3-bit Lloyd-Max V)."""
     import torch
 
     from superl8_serve_amd import ops
+    from superl8_serve_amd.codebook import gaussian_codebook
 
     rng = np.random.default_rng(3 if kind == "chunk" else 4)
     if kind == "chunk":
@@ -301,9 +303,20 @@ def verify_workload(kind: str, device):
     width = bt.shape[1]
     shape = (VERIFY_LAYERS, n_blocks, HKV, BS, D)
     kc = torch.zeros(shape, dtype=torch.int8, device=device)
-    vc = torch.zeros(shape, dtype=torch.int8, device=device)
     ks = torch.ones(shape[:4], dtype=torch.float32, device=device)
-    vs = torch.ones(shape[:4], dtype=torch.float32, device=device)
+    cb = torch.from_numpy(gaussian_codebook()).to(device)
+    if k8v3:  # vc / vs hold the packed codes and the block norms
+        vc = torch.zeros(shape[:4] + (D * 3 // 32,), dtype=torch.int32, device=device)
+        vs = torch.zeros(shape[:4] + (D // 128,), dtype=torch.float32, device=device)
+    else:
+        vc = torch.zeros(shape, dtype=torch.int8, device=device)
+        vs = torch.ones(shape[:4], dtype=torch.float32, device=device)
+
+    def append(k, v, layer, slots):
+        if k8v3:
+            ops.quantize_kv_write_paged_k8v3(k, v, kc[layer], ks[layer], vc[layer], vs[layer], cb, slots)
+        else:
+            ops.quantize_kv_write_paged(k, v, kc[layer], ks[layer], vc[layer], vs[layer], slots)
     gen = torch.Generator(device=device)
     gen.manual_seed(3 if kind == "chunk" else 4)
     # prefix tokens (the shared prefix once for the chunk workload)
@@ -316,7 +329,7 @@ def verify_workload(kind: str, device):
     for layer in range(VERIFY_LAYERS):
         kp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
         vp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
-        ops.quantize_kv_write_paged(kp, vp, kc[layer], ks[layer], vc[layer], vs[layer], sm)
+        append(kp, vp, layer, sm)
     t_new = int(new_slots.size)
     k_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
     v_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
@@ -326,7 +339,7 @@ def verify_workload(kind: str, device):
          "ql": torch.from_numpy(nq.astype(np.int32)).to(device),
          "tree": None if tree is None else torch.from_numpy(tree).to(device),
          "new_sm": torch.from_numpy(new_slots).to(device), "k_new": k_new, "v_new": v_new, "q": q,
-         "max_ctx": width * BS}
+         "max_ctx": width * BS, "cb": cb, "append": append}
     # useful work: every query attends prefix + its visible drafts
     if kind == "chunk":
         ctx = [prefix_len + s + 1 for i in range(b_) for s in range(nq[i])]
@@ -335,28 +348,31 @@ def verify_workload(kind: str, device):
         ctx = [prefix_len + bin(int(m) & ((1 << 64) - 1)).count("1") for i in range(b_) for m in tree[i, : nq[i]]]
         kv_tokens = int((prefix + nq).sum())
     flops = 4 * D * HQ * int(np.sum(ctx))
-    hbm = kv_tokens * HKV * BYTES_PER_TOKEN_HEAD + 2 * 2 * b_ * HQ * nq_max * D
-    append_bytes = t_new * HKV * (D * 4 + BYTES_PER_TOKEN_HEAD) + 4 * t_new
+    per_head = K8V3_BYTES_PER_TOKEN_HEAD if k8v3 else BYTES_PER_TOKEN_HEAD
+    hbm = kv_tokens * HKV * per_head + 2 * 2 * b_ * HQ * nq_max * D
+    append_bytes = t_new * HKV * (D * 4 + per_head) + 4 * t_new
     torch.cuda.synchronize()
     return w, {"batch": b_, "prefix": prefix_len, "queries": int(nq.sum()), "flops_layer": flops,
                "kv_bytes_layer": hbm, "append_bytes_layer": append_bytes}
 
 
-def run_verify(kind: str, steps: int, warmup: int) -> None:
+def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
     import torch
 
     from superl8_serve_amd import ops
 
-    w, info = verify_workload(kind, "cuda")
+    w, info = verify_workload(kind, "cuda", k8v3)
     scale = 1.0 / math.sqrt(D)
 
     def layer_ops(layer, append=True):
         if append:
-            ops.quantize_kv_write_paged(w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer],
-                                        w["vc"][layer], w["vs"][layer], w["new_sm"])
+            w["append"](w["k_new"][layer], w["v_new"][layer], layer, w["new_sm"])
+        kw = dict(query_lens=w["ql"], tree_mask=w["tree"], max_context_len=w["max_ctx"], scale=scale)
+        if k8v3:
+            return ops.attn_paged_verify_k8v3(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
+                                              w["vs"][layer], w["cb"], w["bt"], w["prefix"], BS, **kw)
         return ops.attn_paged_verify(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer],
-                                     w["bt"], w["prefix"], BS, query_lens=w["ql"], tree_mask=w["tree"],
-                                     max_context_len=w["max_ctx"], scale=scale)
+                                     w["bt"], w["prefix"], BS, **kw)
 
     for i in range(warmup * VERIFY_LAYERS):
         layer_ops(i % VERIFY_LAYERS)
@@ -380,10 +396,11 @@ def run_verify(kind: str, steps: int, warmup: int) -> None:
     name = "chunked prefill (16 x (4096 shared prefix + 512 chunk))" if kind == "chunk" else \
         "tree verify (32 x (8192 prefix + 16..64 draft tree))"
     print(json.dumps({
-        "metric": f"paged int8 verify attention TFLOP/s, {name}, Qwen3-8B heads",
+        "metric": f"paged {'k8v3' if k8v3 else 'int8'} verify attention TFLOP/s, {name}, Qwen3-8B heads",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_layer_attention": round(t_attn * 1e3, 4), "ms_per_layer_append_plus_attention": round(t_layer * 1e3, 4),
-        "higher_is_better": True, "dtype": "int8 cache, fp16 MFMA (hi+lo split operands)",
+        "higher_is_better": True,
+        "dtype": f"{'int8 K / 3-bit V' if k8v3 else 'int8'} cache, fp16 MFMA (hi+lo split operands)",
         "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20)",
         "config": {"workload": name, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
                    "layers_rotated": VERIFY_LAYERS, **info},
@@ -603,11 +620,13 @@ def main():
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "k8v3", "copy", "append", "append_k8v3"],
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "copy",
+                                           "append", "append_k8v3"],
                     default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
-                         "attention; k8v3: the K8V3 decode step (batch 32, 8k-32k); copy: copy_blocks; "
-                         "append / append_k8v3: prefill append of 131,072 tokens")
+                         "attention (chunk_k8v3 / tree_k8v3: over the K8V3 cache); k8v3: the K8V3 decode step "
+                         "(batch 32, 8k-32k); copy: copy_blocks; append / append_k8v3: prefill append of 131,072 "
+                         "tokens")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -626,8 +645,8 @@ def main():
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
         return
-    if args.workload in ("chunk", "tree"):
-        run_verify(args.workload, args.steps, args.warmup)
+    if args.workload in ("chunk", "tree", "chunk_k8v3", "tree_k8v3"):
+        run_verify(args.workload.split("_")[0], args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
         return
     if args.workload == "k8v3":
         run_k8v3(args.steps, args.warmup, not args.separate_append)

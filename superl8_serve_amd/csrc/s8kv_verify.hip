@@ -55,8 +55,11 @@ struct Cfg {
   static constexpr int BUF = KBYTES + VBYTES + SBYTES;
   static constexpr int CHUNKS = kTile * D / 16;                 // 16-byte int8 chunks per K (or V) tile
   static constexpr int LOADS = (CHUNKS + kThreads - 1) / kThreads;
-  static constexpr int VJOBS = kTile * NG;                       // K8V3: code groups per tile
-  static_assert(!K8V3 || VJOBS <= kThreads, "one K8V3 code group per thread");
+  // K8V3: a code group's 32 values are expanded by SPLIT threads (16 values
+  // each when the tile has fewer groups than the workgroup has threads)
+  static constexpr int SPLIT = kTile * NG < kThreads ? kThreads / (kTile * NG) : 1;
+  static constexpr int VJOBS = kTile * NG * SPLIT;              // K8V3: expansion jobs per tile
+  static_assert(!K8V3 || (VJOBS <= kThreads && (SPLIT == 1 || SPLIT == 2)), "one K8V3 job per thread");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
 };
 
@@ -222,7 +225,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       }
       if constexpr (K8V3) {
         if (tid < C::VJOBS) {
-          const int tt = tid / C::NG, gi = tid % C::NG;
+          const int grp = tid / C::SPLIT;
+          const int tt = grp / C::NG, gi = grp % C::NG;
           const uint32_t off = row_of(base + tt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
           R.v[0].x = bload32(vc, off);
           R.v[0].y = bload32(vc, off + 4);
@@ -261,13 +265,15 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           }
         }
       }
-      if constexpr (K8V3) {  // 32 codes of one group -> 32 fp16 codebook entries
+      if constexpr (K8V3) {  // 32 / SPLIT codes of one group -> fp16 codebook entries
         if (tid < C::VJOBS) {
-          const int tt = tid / C::NG, gi = tid % C::NG;
-          const uint32_t w0 = R.v[0].x, w1 = R.v[0].y, w2 = R.v[0].z;
-          char* dst = vb + vrow_of(tt) * C::VROW + gi * 64;
+          const int grp = tid / C::SPLIT, part = tid % C::SPLIT;  // part: which 32 / SPLIT values
+          const int tt = grp / C::NG, gi = grp % C::NG;
+          const int sh = part * (32 / C::SPLIT);
+          const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
+          char* dst = vb + vrow_of(tt) * C::VROW + gi * 64 + sh * 2;
 #pragma unroll
-          for (int q4 = 0; q4 < 8; q4 += 2) {
+          for (int q4 = 0; q4 < 8 / C::SPLIT; q4 += 2) {
             u32x4_t o;
             const uint32_t sel0 = spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
             const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
