@@ -166,6 +166,29 @@ int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
                      void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Sliding-window decode: s8kv_decode_int8 / s8kv_decode_k8v3 where row b
+ * attends only its last `window` tokens, positions
+ * [max(0, L - window), L) for L = min(context_lens[b], max_context_len).
+ * The reference's paged kernels have no window; its sliding-window layers
+ * read the window back dense (read_dense(..., window=window_left),
+ * kv_cache.py:1233-1299) and run a dense decode per row
+ * (gqa_attention.py:191-196).  window >= 1; other arguments, the workspace
+ * and head_dim support as the unwindowed entry points.
+ */
+int s8kv_decode_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                            const int8_t* v_cache, const float* v_scale, int64_t num_blocks, int block_size,
+                            const int32_t* block_table, int64_t block_table_stride, const int32_t* context_lens,
+                            int max_context_len, int window, float scale, void* out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+int s8kv_decode_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache, const float* k_scale,
+                            const int32_t* v_packed, const float* v_norm, const float* v_codebook, int lloyd_block,
+                            int64_t num_blocks, int block_size, const int32_t* block_table,
+                            int64_t block_table_stride, const int32_t* context_lens, int max_context_len, int window,
+                            float scale, void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Multi-query verify attention over the int8 paged cache: tree verify and
  * chunked prefill.  No single reference op: it computes what the reference
  * gets from S sequential paged decodes in chain verify

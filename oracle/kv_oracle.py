@@ -414,11 +414,15 @@ def _softmax_attend(q, k, v, scale, visible=None):
     return out
 
 
-def paged_decode(q, layer: LayerCache, block_table, context_lens, scale) -> np.ndarray:
+def paged_decode(q, layer: LayerCache, block_table, context_lens, scale, window=None) -> np.ndarray:
     """Ragged-batch GQA decode over the paged cache in float64
     (``attn_paged_decode_cached`` / ``attn_paged_decode_k8v3`` semantics,
     kv_cache.py:1167-1201): row b attends its first ``context_lens[b]``
     tokens; q head h reads KV head ``h // (Hq/Hkv)`` (gqa_attention.py:208-212).
+    ``window``: only the last ``window`` of them, positions
+    ``[max(0, n - window), n)`` -- the reference's sliding-window decode reads
+    that range back dense (``first = max(0, length - window)`` in
+    kv_cache.py:1233-1299, called at gqa_attention.py:191-196).
 
     q: ``[B, Hq, D]`` (any float) -> float64 ``[B, Hq, D]``."""
     q = np.asarray(q, dtype=np.float64)
@@ -431,6 +435,9 @@ def paged_decode(q, layer: LayerCache, block_table, context_lens, scale) -> np.n
         if n <= 0:
             continue
         k, v = exact_kv(layer, block_table[b], n)
+        if window is not None:
+            first = max(0, n - int(window))
+            k, v = k[:, first:], v[:, first:]
         for h in range(hkv):
             out[b, h * g:(h + 1) * g] = _softmax_attend(q[b, h * g:(h + 1) * g], k[h], v[h], scale)
     return out

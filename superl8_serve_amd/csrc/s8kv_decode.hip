@@ -136,6 +136,9 @@ struct DecodeArgs {
   int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
   float rot_norm;         // fp32(1/sqrt(D)): the K rotation's normalisation
   int smem_new;           // LDS byte offset of the new token's rows (DecCfg NEW_*)
+  // sliding window (decode_kernel<D, K8V3, false, true>): row b attends only
+  // its last `window` tokens (window >= 1)
+  int window;
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -238,10 +241,24 @@ __device__ __forceinline__ int raw_len_at(const DecodeArgs& a, const int* lens_l
   return b < kLensLds ? lens_lds[b] : a.context_lens[b];
 }
 
+// Sliding window: a row of L tokens attends positions [L - window, L); the
+// kernel views it from win_base, that start rounded down to a multiple of 32
+// (so its tiles stay 32-aligned in the block table), and masks the tokens of
+// the first tile below the start.
+__device__ __forceinline__ int win_base(const DecodeArgs& a, int L) { return max(0, L - a.window) & ~31; }
+// Tokens of row b the kernel streams: all of them, or those from win_base on.
+template <bool WIN>
+__device__ __forceinline__ int view_len(const DecodeArgs& a, const int* lens_lds, int b) {
+  const int L = lens_at(a, lens_lds, b);
+  if constexpr (WIN) return L - win_base(a, L);
+  return L;
+}
+
 // Stream length of rows c0 + lane (0 past the batch).
+template <bool WIN>
 __device__ __forceinline__ int row_stream_len(const DecodeArgs& a, const int* lens_lds, int c0, int lane) {
   const int r = c0 + lane;
-  return r < a.batch ? stream_len(a, lens_at(a, lens_lds, r)) : 0;
+  return r < a.batch ? stream_len(a, view_len<WIN>(a, lens_lds, r)) : 0;
 }
 
 // Position of tile token tt (0..31) in the LDS-staged V tile: lane group g's
@@ -272,8 +289,9 @@ struct TileIO {
   float4_t vs[2][C::NB];
 };
 
-template <int D, bool K8V3, bool FUSE>
+template <int D, bool K8V3, bool FUSE, bool WIN = false>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
+  static_assert(!(FUSE && WIN), "the sliding-window form has no fused append");
   using C = DecCfg<D, K8V3>;
   constexpr int E = RowLayout<D>::E;
   // LDS: [V staging of the 4 waves | rotated q; the cross-wave merge reuses both][block ids]
@@ -295,11 +313,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   __syncthreads();
 
   // ---- stream positions: prefix of the rows' stream lengths (every wave) ----
-  const int v0 = row_stream_len(a, lens_lds, 0, lane);
+  const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
   const int incl0 = wave_incl_scan(v0);  // rows 0..63
   int total = __builtin_amdgcn_readlane(incl0, 63);
   for (int c0 = 64; c0 < a.batch; c0 += 64)
-    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len(a, lens_lds, c0, lane)), 63);
+    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len<WIN>(a, lens_lds, c0, lane)), 63);
   total = __builtin_amdgcn_readfirstlane(total);
 
   // ---- this workgroup's slice [lo, hi) of the token stream ----
@@ -326,7 +344,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     rpb = 0;
     int carry = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
-      const int v = c0 == 0 ? v0 : row_stream_len(a, lens_lds, c0, lane);
+      const int v = c0 == 0 ? v0 : row_stream_len<WIN>(a, lens_lds, c0, lane);
       const int incl = (c0 == 0 ? incl0 : wave_incl_scan(v)) + carry;
       const uint64_t m = __builtin_amdgcn_ballot_w64(incl > pos);
       if (m != 0) {
@@ -379,7 +397,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // length, or 0 when the slice holds no further segment.
   auto find_segment = [&](int& rb, int& rpb) -> int {
     for (; rb < a.batch && rpb + a.ghost < hi; ++rb) {
-      const int L = __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, rb));
+      const int L = __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, rb));
       if (L == 0) continue;
       if (rpb + a.ghost + padded32(L) > lo) return L;
       rpb += stream_len(a, L);
@@ -417,7 +435,8 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       for (int e = 0; e < E; ++e)
         qraw[k][e] = (cq < G && lane_q < RowLayout<D>::ACTIVE) ? qp[lane_q + 64 * e] : (_Float16)0.0f;
     }
-    const int fb = s0 >> bs_log2;
+    const int al = WIN ? win_base(a, __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, rb))) : 0;
+    const int fb = (s0 + al) >> bs_log2;
     const int32_t* bt_row = a.block_table + (int64_t)rb * a.bt_stride + fb;
 #pragma unroll
     for (int k = 0; k < kBtRegs; ++k) {
@@ -448,7 +467,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   {
     int bl, pbl;
     find_row(hi - 1, bl, pbl);
-    const int Ll = bl > b ? __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, bl)) : 0;
+    const int Ll = bl > b ? __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, bl)) : 0;
     if (Ll > 0 && pbl + a.ghost < hi && pbl + a.ghost + padded32(Ll) > hi) {
       b = bl;
       pb = pbl;
@@ -476,6 +495,14 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     const bool whole_row = (s0 == 0) && (s1 == padL);
     const int last = L - 1;
     const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+    // sliding window: row coordinates start at absolute position al; tokens
+    // below lo_tok (in the row's first tile) are outside the window
+    int al = 0, lo_tok = 0;
+    if constexpr (WIN) {
+      const int Lf = __builtin_amdgcn_readfirstlane(lens_at(a, lens_lds, b));
+      al = win_base(a, Lf);
+      lo_tok = max(0, Lf - a.window) - al;
+    }
 
     // q: each wave rotates the heads c = wave + 4k of the group (lane l holds
     // dims l + 64e: the append's fp32 FWHT, stages h = 1 .. D/2 in order),
@@ -542,7 +569,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     for (int u0 = s0; u0 < s1; u0 += kSubTokens) {
       const int u1 = min(s1, u0 + kSubTokens);
       const int t1 = min(u1, L);               // valid tokens end
-      const int fb = u0 >> bs_log2;
+      const int fb = (u0 + al) >> bs_log2;     // block-table index of the sub-split's first block
       // Lane-derived addresses of the tile loop are recomputed per sub-split:
       // the opaque copy of the thread id stops the compiler from hoisting them
       // out of the segment loop, where they would stay live across the q
@@ -551,7 +578,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       const int c = lane & 15;
       const int g = lane >> 4;
       if (u0 != s0) {  // later sub-splits of a long segment: stage their block ids now
-        const int nblk = ((t1 - 1) >> bs_log2) - fb + 1;
+        const int nblk = ((t1 - 1 + al) >> bs_log2) - fb + 1;
         __syncthreads();
         for (int i = tid; i < nblk; i += 64 * kDecWaves) bt_lds[i] = bt_row[fb + i];
         __syncthreads();
@@ -559,10 +586,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
       // storage row of token `tok` (already clamped to the row's last token)
       auto row_of = [&](int tok) -> uint32_t {
+        if constexpr (WIN) tok += al;
         const uint32_t blk = (uint32_t)bt_lds[(tok >> bs_log2) - fb];
         return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tok & bsm);
       };
       auto tile_row0 = [&](int tb) -> uint32_t {
+        if constexpr (WIN) tb += al;
         const uint32_t blk = (uint32_t)bt_lds[(tb >> bs_log2) - fb];
         return __builtin_amdgcn_readfirstlane(((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tb & bsm));
       };
@@ -758,7 +787,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float x = sc[s][i] * io.ks[s][i];
-            if constexpr (MASKED) x = (tb + 16 * s + 4 * g + i) < t1 ? x : kNegInf;
+            if constexpr (MASKED) {
+              const int tok = tb + 16 * s + 4 * g + i;
+              x = (tok < t1 && (!WIN || tok >= lo_tok)) ? x : kNegInf;
+            }
             p[s][i] = x;
             mt = fmaxf(mt, x);
           }
@@ -794,8 +826,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float w = materialize(p[s][i] * io.vs[s][nb][i]);  // one value for hi and lo
-              // masked tokens: p = 0 but the scale past the row end may be any value
-              if constexpr (MASKED) w = (tb + 16 * s + 4 * g + i) < t1 ? w : 0.0f;
+              // masked tokens: p = 0 but the scale past the row end (or below
+              // the window) may be any value
+              if constexpr (MASKED) {
+                const int tok = tb + 16 * s + 4 * g + i;
+                w = (tok < t1 && (!WIN || tok >= lo_tok)) ? w : 0.0f;
+              }
               const _Float16 wh = (_Float16)w;
               pbh[nb][4 * s + i] = wh;
               pbl[nb][4 * s + i] = (_Float16)(w - (float)wh);
@@ -835,6 +871,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
         issue_kv(tb, r0);
         issue_scales(tb, r0);
+        if constexpr (WIN) {  // the row's first tile holds tokens below the window
+          if (tb < lo_tok && tb + kTile * kDecWaves < t1) {
+            process(tb, std::true_type{}, std::true_type{});
+            tb += kTile * kDecWaves;
+          }
+        }
         while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
           process(tb, std::false_type{}, std::true_type{});
           tb += kTile * kDecWaves;
@@ -1071,7 +1113,7 @@ static int plan_wg_per_head(int num_kv_heads, int resident_per_cu) {
   return w < 1 ? 1 : (w > cap ? cap : w);
 }
 
-template <int D, bool K8V3, bool FUSE>
+template <int D, bool K8V3, bool FUSE, bool WIN = false>
 static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
   constexpr int kNewBytes = FUSE ? C::NEW_BYTES : 0;  // fused append: the new token's rows
@@ -1088,7 +1130,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   static int resident_by_group[17] = {};
   static bool lds_raised = false;
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3, FUSE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3, FUSE, WIN>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             smem_main_for(16) + (kMaxSubBlocks + kLensLds) * 4 + kNewBytes) != hipSuccess) {
       set_error("s8kv_decode: cannot raise the dynamic LDS limit");
@@ -1099,7 +1141,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   int& resident = resident_by_group[a.group];
   if (resident == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3, FUSE>, 64 * kDecWaves, smem) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3, FUSE, WIN>, 64 * kDecWaves, smem) != hipSuccess ||
         n <= 0)
       n = 2;
     resident = n < kMaxResidentPerCU ? n : kMaxResidentPerCU;
@@ -1114,9 +1156,9 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
   hipEvent_t* ev = timing_slot(stream);
   if (ev) {  // events stamped with the kernel's own start and end times
-    hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
+    hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE>), grid, dim3(64 * kDecWaves), smem, stream, a);
+    hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, a);
   }
   return check_launch("s8kv_decode");
 }
@@ -1185,6 +1227,15 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   a.ws_cnt = reinterpret_cast<unsigned long long*>(a.ws_acc + partials * head_dim);
   a.tag = next_launch_tag();
   hipStream_t s = (hipStream_t)stream;
+  if (a.window > 0) {  // sliding window (no fused append)
+    switch (head_dim) {
+      case 32: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<32, false, false, true>(a, s);
+      case 64: return k8v3 ? S8KV_ERR_UNSUPPORTED : launch_decode<64, false, false, true>(a, s);
+      case 128: return k8v3 ? launch_decode<128, true, false, true>(a, s) : launch_decode<128, false, false, true>(a, s);
+      case 256: return k8v3 ? launch_decode<256, true, false, true>(a, s) : launch_decode<256, false, false, true>(a, s);
+    }
+    return S8KV_ERR_UNSUPPORTED;
+  }
   if (fuse) {
     if (k8v3) {
       switch (head_dim) {
@@ -1341,6 +1392,53 @@ extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int n
   a.bt_stride = block_table_stride;
   a.context_lens = context_lens;
   a.out = (_Float16*)out;
+  return decode_common(a, true, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache,
+                                       const float* k_scale, const int8_t* v_cache, const float* v_scale,
+                                       int64_t num_blocks, int block_size, const int32_t* block_table,
+                                       int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                       int window, float scale, void* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "decode_window: window %d < 1", window);
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  a.window = window;
+  return decode_common(a, false, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const int8_t* k_cache,
+                                       const float* k_scale, const int32_t* v_packed, const float* v_norm,
+                                       const float* v_codebook, int lloyd_block, int64_t num_blocks, int block_size,
+                                       const int32_t* block_table, int64_t block_table_stride,
+                                       const int32_t* context_lens, int max_context_len, int window, float scale,
+                                       void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "decode_window: window %d < 1", window);
+  S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "decode_k8v3: lloyd_block %d != 128", lloyd_block);
+  S8KV_REQUIRE(v_codebook != nullptr, S8KV_ERR_INVALID, "decode_k8v3: null codebook");
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_packed; a.v_scale = v_norm;
+  a.v_codebook = v_codebook;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  a.window = window;
   return decode_common(a, true, false, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, scale, workspace, workspace_bytes, stream);
 }

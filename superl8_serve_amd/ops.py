@@ -23,6 +23,8 @@ __all__ = [
     "quantize_kv_write_paged_k8v3",
     "attn_paged_decode_cached",
     "attn_paged_decode_k8v3",
+    "attn_paged_decode_window",
+    "attn_paged_decode_window_k8v3",
     "attn_paged_decode_append",
     "attn_paged_decode_append_k8v3",
     "decode_workspace_bytes",
@@ -212,6 +214,36 @@ def attn_paged_decode_cached(q, k_cache, k_scale, v_cache, v_scale, block_table,
     return out
 
 
+def attn_paged_decode_window(q, k_cache, k_scale, v_cache, v_scale, block_table, context_lens, block_size, *,
+                             max_context_len, window, scale):
+    """``attn_paged_decode_cached`` for a sliding-window layer: row b attends
+    only its last ``window`` tokens, positions ``[max(0, L - window), L)``.
+    The reference reads that window back dense and decodes per row
+    (gqa_attention.py:191-196 with kv_cache.py:1233-1299)."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_cache", v_cache, torch.int8, dev)
+    _on_gpu("v_scale", v_scale, torch.float32, dev)
+    _require(v_cache.shape == k_cache.shape and v_cache.is_contiguous(), "v_cache must match k_cache")
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_scale.shape) == (n, hkv, bs) and v_scale.is_contiguous(), "v_scale must be [N, Hkv, bs]")
+    _require(int(window) >= 1, f"window must be >= 1, got {window}")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_window_int8(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+        bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, int(window), float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_window")
+    return out
+
+
 def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale, block_table, context_lens,
                              block_size, *, max_context_len, scale):
     """One decode step of a layer in one launch: append row b's new token at
@@ -324,6 +356,38 @@ def attn_paged_decode_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
     _lib.check(rc, "attn_paged_decode_k8v3")
+    return out
+
+
+def attn_paged_decode_window_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, context_lens,
+                                  block_size, *, max_context_len, window, scale):
+    """``attn_paged_decode_k8v3`` for a sliding-window layer: row b attends
+    only its last ``window`` tokens (see ``attn_paged_decode_window``)."""
+    q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
+        q, k_cache, block_table, context_lens, block_size, max_context_len)
+    n, hkv, bs, d, b, hq = geo
+    dev = q3.device
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    _on_gpu("v_packed", v_packed, torch.int32, dev)
+    _on_gpu("v_norm", v_norm, torch.float32, dev)
+    _on_gpu("v_codebook", v_codebook, torch.float32, dev)
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    _require(tuple(v_packed.shape) == (n, hkv, bs, d * 3 // 32) and v_packed.is_contiguous(),
+             "v_packed must be [N, Hkv, bs, D*3/32]")
+    lloyd_block = d // v_norm.shape[-1] if v_norm.dim() == 4 and v_norm.shape[-1] > 0 else 0
+    _require(tuple(v_norm.shape[:3]) == (n, hkv, bs) and v_norm.is_contiguous(), "v_norm must be [N, Hkv, bs, D/128]")
+    _require(v_codebook.numel() == 8 and v_codebook.is_contiguous(), "v_codebook must hold 8 contiguous entries")
+    _require(int(window) >= 1, f"window must be >= 1, got {window}")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_decode_window_k8v3(
+        q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
+        lloyd_block, n, bs, bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, int(window), float(scale),
+        out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
+    )
+    _lib.check(rc, "attn_paged_decode_window_k8v3")
     return out
 
 

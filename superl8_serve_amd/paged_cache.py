@@ -385,8 +385,21 @@ class PagedKVCache:
     # --------------------------------------------------------------- attention
 
     def decode_attn_static(self, layer: int, q: torch.Tensor, block_table: torch.Tensor, context_lens: torch.Tensor,
-                           max_context_len: int, *, scale: float) -> torch.Tensor:
+                           max_context_len: int, *, scale: float, window: int | None = None) -> torch.Tensor:
+        """Batched paged decode (kv_cache.py:1148-1201).  ``window``: a
+        sliding-window layer attends only each row's last ``window`` tokens
+        (what the reference gets from ``read_dense(..., window=)`` plus a dense
+        decode per row, gqa_attention.py:191-196)."""
         row = self._layer_row(layer)
+        if window is not None:
+            if self.v_quant == "lloydmax3":
+                return ops.attn_paged_decode_window_k8v3(
+                    q, self.k_cache[row], self.k_scale[row], self.v_packed[row], self.v_norm[row],
+                    self.v_codebook[row], block_table, context_lens, self.block_size,
+                    max_context_len=max_context_len, window=window, scale=scale)
+            return ops.attn_paged_decode_window(q, self.k_cache[row], self.k_scale[row], self.v_cache[row],
+                                                self.v_scale[row], block_table, context_lens, self.block_size,
+                                                max_context_len=max_context_len, window=window, scale=scale)
         if self.v_quant == "lloydmax3":
             return ops.attn_paged_decode_k8v3(q, self.k_cache[row], self.k_scale[row], self.v_packed[row],
                                               self.v_norm[row], self.v_codebook[row], block_table, context_lens,
@@ -396,13 +409,14 @@ class PagedKVCache:
                                             max_context_len=max_context_len, scale=scale)
 
     def decode_attn(self, layer: int, q: torch.Tensor, slots: list[int], lengths: list[int], *,
-                    scale: float) -> torch.Tensor:
+                    scale: float, window: int | None = None) -> torch.Tensor:
         """`lengths[i]` is the position of the token just written, so row i
-        attends `lengths[i] + 1` tokens (kv_cache.py:1129-1146)."""
+        attends `lengths[i] + 1` tokens (kv_cache.py:1129-1146), or the last
+        ``window`` of them."""
         ctx = [n + 1 for n in lengths]
         return self.decode_attn_static(layer, q, self.block_table(slots),
                                        torch.tensor(ctx, dtype=torch.int32, device=self.device),
-                                       max(ctx) if ctx else 0, scale=scale)
+                                       max(ctx) if ctx else 0, scale=scale, window=window)
 
     def decode_step_static(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                            block_table: torch.Tensor, context_lens: torch.Tensor, max_context_len: int, *,

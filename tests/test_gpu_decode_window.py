@@ -1,0 +1,146 @@
+"""GPU parity of the sliding-window paged decode (row b attends its last
+`window` tokens) against the float64 oracle, through the C ABI.
+
+The reference's sliding-window layers read the window back dense and decode
+per row (gqa_attention.py:191-196, kv_cache.py:1233-1299); the oracle restates
+that range, [max(0, L - window), L).  Tolerance as for decode:
+max(|out-ref| / max(1,|ref|)) <= 2e-3 and relative RMS <= 1e-3.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from superl8_serve_amd import ops
+from tests.kvcase import make_case, oracle_fill_int8, oracle_fill_k8v3
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+CODEBOOK = O.gaussian_codebook(3, 128)
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _close(out, ref, what):
+    mx, rel = O.attention_errors(out, ref)
+    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"{what}: max err {mx:.3e}, rel rms {rel:.3e}"
+
+
+def _int8(case, cache, window, q=None):
+    kc, ks, vc, vs = (_t(x) for x in cache)
+    q = _t(case.q if q is None else q)[:, :, None, :]
+    args = (q, kc, ks, vc, vs, _t(case.block_table), _t(case.lens.astype(np.int32)), case.block_size)
+    kw = dict(max_context_len=int(case.lens.max()), scale=case.scale)
+    out = ops.attn_paged_decode_cached(*args, **kw) if window is None else \
+        ops.attn_paged_decode_window(*args, window=window, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()[:, :, 0, :]
+
+
+def _k8v3(case, cache, window):
+    kc, ks, vp, vn = (_t(x) for x in cache)
+    q = _t(case.q)[:, :, None, :]
+    args = (q, kc, ks, vp, vn, _t(CODEBOOK), _t(case.block_table), _t(case.lens.astype(np.int32)), case.block_size)
+    kw = dict(max_context_len=int(case.lens.max()), scale=case.scale)
+    out = ops.attn_paged_decode_k8v3(*args, **kw) if window is None else \
+        ops.attn_paged_decode_window_k8v3(*args, window=window, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()[:, :, 0, :]
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,lens,window", [
+    (8, 2, 128, 16, [300, 37, 256, 1, 0, 4100], 100),    # window inside, shorter rows, empty row
+    (8, 2, 128, 256, [700, 2600, 31, 33], 33),           # start not on a 32-token tile
+    (32, 8, 128, 256, [5000, 4096, 4097, 300], 4096),    # window = a row's length, long rows
+    (16, 16, 64, 4, [90, 17, 64], 5),                    # tiny blocks (tiles cross blocks), G = 1
+    (4, 2, 256, 16, [120, 257], 64),                     # head_dim 256
+    (8, 2, 32, 16, [45, 80], 1),                         # window 1: the last token's V
+    (64, 4, 128, 16, [2000, 999, 1500], 1000),           # G = 16
+])
+def test_window_decode_int8(hq, hkv, d, bs, lens, window):
+    case = make_case(300 + d + bs + window, len(lens), hq, hkv, d, bs, lens, outlier_channels=2)
+    cache = oracle_fill_int8(case)
+    ref = O.paged_decode(case.q, O.LayerCache(*cache), case.block_table, case.lens, case.scale, window=window)
+    _close(_int8(case, cache, window), ref, f"window {window}")
+
+
+@pytest.mark.parametrize("d,bs,lens,window", [(128, 16, [300, 4100, 7], 200), (256, 256, [1000, 260], 77)])
+def test_window_decode_k8v3(d, bs, lens, window):
+    case = make_case(400 + d + window, len(lens), 8, 2, d, bs, lens, outlier_channels=2)
+    cache = oracle_fill_k8v3(case, CODEBOOK)
+    layer = O.LayerCache(cache[0], cache[1], v_packed=cache[2], v_norm=cache[3], v_codebook=CODEBOOK)
+    ref = O.paged_decode(case.q, layer, case.block_table, case.lens, case.scale, window=window)
+    _close(_k8v3(case, cache, window), ref, f"k8v3 window {window}")
+
+
+def test_window_covering_every_row_equals_full_decode():
+    """A window at least as long as every row views each row from position 0:
+    the same slices and the same arithmetic as the unwindowed decode."""
+    case = make_case(451, 5, 8, 2, 128, 16, [300, 37, 256, 1, 900])
+    cache = oracle_fill_int8(case)
+    assert np.array_equal(_int8(case, cache, 900), _int8(case, cache, None))
+    kcase = make_case(452, 3, 8, 2, 128, 16, [300, 37, 900])
+    kcache = oracle_fill_k8v3(kcase, CODEBOOK)
+    assert np.array_equal(_k8v3(kcase, kcache, 5000), _k8v3(kcase, kcache, None))
+
+
+def test_tokens_outside_the_window_are_not_read_into_the_result():
+    """Garbage K and non-finite scales before the window (in the window's
+    first tile and in earlier blocks) leave the windowed output unchanged."""
+    case = make_case(461, 3, 8, 2, 128, 16, [300, 150, 77], outlier_channels=1)
+    cache = oracle_fill_int8(case)
+    window = 45
+    before = _int8(case, cache, window)
+    kc, ks, vc, vs = (x.copy() for x in cache)
+    for b, n in enumerate(case.lens):
+        for p in range(max(0, int(n) - window)):
+            blk, off = case.block_table[b, p // case.block_size], p % case.block_size
+            kc[blk, :, off] = 127
+            ks[blk, :, off] = np.inf
+            vc[blk, :, off] = -127
+            vs[blk, :, off] = np.nan
+    after = _int8(case, (kc, ks, vc, vs), window)
+    assert np.all(np.isfinite(after))
+    assert np.array_equal(after, before)
+
+
+def test_window_must_be_positive():
+    case = make_case(471, 1, 4, 2, 128, 16, [20])
+    cache = oracle_fill_int8(case)
+    with pytest.raises(ValueError, match="window"):
+        _int8(case, cache, 0)
+
+
+def test_host_cache_windowed_decode():
+    """PagedKVCache.decode_attn(window=...) routes to the windowed kernel."""
+    from superl8_serve_amd.paged_cache import PagedKVCache
+
+    g = torch.Generator(device=DEV).manual_seed(5)
+    hq, hkv, d, bs = 8, 2, 128, 16
+    for v_quant in ("int8", "lloydmax3"):
+        c = PagedKVCache(1, 2, hkv, 512, d, device=DEV, block_size=bs, v_quant=v_quant)
+        slots = [c.alloc(), c.alloc()]
+        lens = [200, 61]
+        c.ensure_capacity(slots, lens)
+        for s, n in zip(slots, lens):
+            k = torch.randn(1, hkv, n, d, generator=g, device=DEV).half()
+            c.write_prefill(0, k, torch.randn_like(k), slot=s)
+        q = torch.randn(2, hq, 1, d, generator=g, device=DEV).half()
+        out = c.decode_attn(0, q, slots, [n - 1 for n in lens], scale=0.1, window=50)
+        r = c._layer_row(0)
+        if v_quant == "lloydmax3":
+            layer = O.LayerCache(c.k_cache[r].cpu().numpy(), c.k_scale[r].cpu().numpy(),
+                                 v_packed=c.v_packed[r].cpu().numpy(), v_norm=c.v_norm[r].cpu().numpy(),
+                                 v_codebook=c.v_codebook[r].cpu().numpy())
+        else:
+            layer = O.LayerCache(c.k_cache[r].cpu().numpy(), c.k_scale[r].cpu().numpy(), c.v_cache[r].cpu().numpy(),
+                                 c.v_scale[r].cpu().numpy())
+        ref = O.paged_decode(q[:, :, 0].cpu().numpy(), layer, c.block_table(slots).cpu().numpy(), np.array(lens), 0.1,
+                             window=50)
+        _close(out[:, :, 0].float().cpu().numpy(), ref, f"{v_quant} via cache")

@@ -426,3 +426,38 @@ def test_attention_errors_definition():
     mx, rel = O.attention_errors(out, ref)
     assert abs(mx - 1e-3) < 1e-12
     assert abs(rel - math.sqrt((1e-6 + 16e-6) / 3) / math.sqrt((0.25 + 16 + 100) / 3)) < 1e-12
+
+
+def test_paged_decode_window():
+    """Sliding-window decode attends positions [n - window, n): window >= n is
+    the full decode; window 1 returns the last token's V for every q head
+    (a softmax over one key); tokens outside the window do not matter."""
+    rng = np.random.default_rng(12)
+    hq, hkv, d, bs, n = 8, 2, 64, 16, 70
+    k = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    nb = (n + bs - 1) // bs + 1
+    kc, ks = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    vc, vs = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    bt = np.array([[3, 0, 4, 1, 2]], np.int32)
+    slots = (bt[0, np.arange(n) // bs] * bs + np.arange(n) % bs).astype(np.int32)
+    O.quantize_kv_write_paged(k, v, kc, ks, vc, vs, slots)
+    layer = O.LayerCache(kc, ks, vc, vs)
+    q = rng.standard_normal((1, hq, d))
+    lens = np.array([n])
+    full = O.paged_decode(q, layer, bt, lens, 0.125)
+    assert np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125, window=n), full)
+    assert np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125, window=10 * n), full)
+    assert not np.allclose(O.paged_decode(q, layer, bt, lens, 0.125, window=n - 1), full)
+    last_v = O.exact_kv(layer, bt[0], n)[1][:, -1]  # [Hkv, D]
+    w1 = O.paged_decode(q, layer, bt, lens, 0.125, window=1)[0]
+    assert np.allclose(w1, np.repeat(last_v, hq // hkv, axis=0), rtol=1e-12, atol=1e-12)
+    # garbage before the window leaves the windowed output unchanged
+    w = 23
+    before = O.paged_decode(q, layer, bt, lens, 0.125, window=w)
+    for p in range(n - w):
+        blk, off = bt[0, p // bs], p % bs
+        kc[blk, :, off] = 127
+        ks[blk, :, off] = 1e3
+    assert np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125, window=w), before)
+    assert not np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125), full)
