@@ -575,6 +575,86 @@ def run_append(steps: int, warmup: int, k8v3: bool = False) -> None:
                       "bytes_per_call": moved, "pct_of_hbm_peak": round(100 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
 
 
+WINDOW = 4096
+WINDOW_LAYERS = 4  # distinct storage, rotated so no layer is served from the Infinity Cache
+
+
+def run_window(steps: int, warmup: int) -> None:
+    """Sliding-window decode (attn_paged_decode_window): Qwen3-8B int8 heads,
+    batch 64, contexts U{8192..32768} (seed 5), window 4096 -- each row reads
+    its last 4096 tokens.  Only the windowed positions (and the rest of the
+    32-token tile holding a window start) are filled; earlier positions are
+    never read.  Four layers of distinct storage, rotated."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    dev = "cuda"
+    rng = np.random.default_rng(5)
+    lens = rng.integers(8192, 32769, size=BATCH)
+    need = (lens + BS - 1) // BS
+    n_blocks = int(need.sum()) + 4
+    perm = rng.permutation(n_blocks)
+    width = int(need.max())
+    bt = np.zeros((BATCH, width), np.int32)
+    pos = 0
+    for b in range(BATCH):
+        bt[b, : need[b]] = perm[pos: pos + need[b]]
+        pos += need[b]
+    first = [(max(0, int(n) - WINDOW)) & ~31 for n in lens]
+    slots = np.concatenate([bt[b, np.arange(first[b], lens[b]) // BS] * BS + np.arange(first[b], lens[b]) % BS
+                            for b in range(BATCH)]).astype(np.int32)
+    shape = (n_blocks, HKV, BS, D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    sm = torch.from_numpy(slots).to(dev)
+    layers = []
+    for layer in range(WINDOW_LAYERS):
+        kc = torch.zeros(shape, dtype=torch.int8, device=dev)
+        vc = torch.zeros(shape, dtype=torch.int8, device=dev)
+        ks = torch.zeros(shape[:3], dtype=torch.float32, device=dev)
+        vs = torch.zeros(shape[:3], dtype=torch.float32, device=dev)
+        ch = torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(dev)
+        for c0 in range(0, slots.size, 65536):
+            n = min(65536, slots.size - c0)
+            kp = _fp16_outliers(gen, (n, HKV, D), ch, dev)
+            vp = _fp16_outliers(gen, (n, HKV, D), ch, dev)
+            ops.quantize_kv_write_paged(kp, vp, kc, ks, vc, vs, sm[c0:c0 + n])
+        q = _fp16_outliers(gen, (BATCH, HQ, 1, D), ch, dev)
+        layers.append((q, kc, ks, vc, vs))
+    btd = torch.from_numpy(bt).to(dev)
+    cl = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def attend(i):
+        q, kc, ks, vc, vs = layers[i % WINDOW_LAYERS]
+        return ops.attn_paged_decode_window(q, kc, ks, vc, vs, btd, cl, BS, max_context_len=width * BS,
+                                            window=WINDOW, scale=scale)
+
+    for i in range(warmup * WINDOW_LAYERS):
+        attend(i)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(steps * WINDOW_LAYERS):
+        attend(i)
+    en.record()
+    torch.cuda.synchronize()
+    t = st.elapsed_time(en) * 1e-3 / (steps * WINDOW_LAYERS)
+    tokens = int(np.minimum(lens, WINDOW).sum())
+    nbytes = tokens * HKV * BYTES_PER_TOKEN_HEAD + 2 * 2 * BATCH * HQ * D + 4 * BATCH * (1 + WINDOW // BS + 1)
+    print(json.dumps({
+        "metric": f"paged int8 sliding-window decode HBM GB/s, Qwen3-8B shapes, b={BATCH}, window {WINDOW}, "
+                  "8k-32k contexts",
+        "value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "us_per_launch": round(t * 1e6, 2), "higher_is_better": True, "dtype": "int8",
+        "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20, seed 5)",
+        "config": {"workload": "sliding-window decode", "batch": BATCH, "window": WINDOW,
+                   "sum_window_tokens": tokens, "bytes_per_launch": nbytes, "layers_rotated": WINDOW_LAYERS},
+        "pct_of_hbm_peak": round(nbytes / t / 1e9 / 8000.0 * 100, 2),
+    }))
+
+
 def run_copy(steps: int) -> None:
     """copy_blocks over a 4096-block synthetic pool (Qwen3-8B int8 block: K, V,
     two scale tensors; 1 layer): 1024 random source blocks moved to 1024 other
@@ -620,13 +700,13 @@ def main():
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "copy",
-                                           "append", "append_k8v3"],
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "window",
+                                           "copy", "append", "append_k8v3"],
                     default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
                          "attention (chunk_k8v3 / tree_k8v3: over the K8V3 cache); k8v3: the K8V3 decode step "
-                         "(batch 32, 8k-32k); copy: copy_blocks; append / append_k8v3: prefill append of 131,072 "
-                         "tokens")
+                         "(batch 32, 8k-32k); window: sliding-window decode (batch 64, window 4096); copy: "
+                         "copy_blocks; append / append_k8v3: prefill append of 131,072 tokens")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -653,6 +733,9 @@ def main():
         return
     if args.workload == "copy":
         run_copy(args.steps)
+        return
+    if args.workload == "window":
+        run_window(args.steps, args.warmup)
         return
     if args.workload in ("append", "append_k8v3"):
         run_append(args.steps, args.warmup, k8v3=args.workload == "append_k8v3")
