@@ -234,6 +234,29 @@ int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
                      const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream);
 
 /*
+ * Verify attention of a sliding-window layer: as s8kv_verify_int8 /
+ * s8kv_verify_k8v3, but of the prefix only the last `window` keys,
+ * [max(0, prefix_lens[b] - window), prefix_lens[b]), are visible (drafts as
+ * before).  The reference reads that prefix window back dense and appends the
+ * drafts (gqa_attention.py:305-314, read_dense at kv_cache.py:1233-1299).
+ * window >= 1.
+ */
+int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                            const int8_t* k_cache, const float* k_scale, const int8_t* v_cache, const float* v_scale,
+                            int64_t num_blocks, int block_size, const int32_t* block_table,
+                            int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                            const int64_t* tree_mask, int max_context_len, int window, float scale, void* out,
+                            void* stream);
+int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                            const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
+                            const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                            int block_size, const int32_t* block_table, int64_t block_table_stride,
+                            const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
+                            int max_context_len, int window, float scale, void* out, void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its kernel with HIP events stamped with the

@@ -443,7 +443,8 @@ def paged_decode(q, layer: LayerCache, block_table, context_lens, scale, window=
     return out
 
 
-def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query_lens=None, tree_mask=None) -> np.ndarray:
+def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query_lens=None, tree_mask=None,
+                 window=None) -> np.ndarray:
     """Multi-query verify attention over the paged cache in float64.
 
     Query s of row b sees every prefix key ``j < prefix_lens[b]`` plus draft key
@@ -453,7 +454,10 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
     S decode steps with context ``L + t + 1`` (gqa_attention.py:259-277), and
     the bottom-right-aligned causal chunk of chunked prefill
     (gqa_attention.py:117-126, gated_gqa_attention.py:167-185).
-    Queries ``s >= query_lens[b]`` produce zeros.
+    Queries ``s >= query_lens[b]`` produce zeros.  ``window``: a sliding-window
+    layer sees only the last ``window`` prefix keys, ``[max(0, p - window), p)``,
+    plus its drafts -- the reference reads that prefix window back dense and
+    appends the drafts (gqa_attention.py:305-314 with kv_cache.py:1233-1299).
 
     q: ``[B, Hq, S, D]`` -> float64 ``[B, Hq, S, D]``."""
     q = np.asarray(q, dtype=np.float64)
@@ -477,6 +481,8 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
                 bits = int(np.asarray(tree_mask)[b, s]) & ((1 << 64) - 1)
                 draft = np.array([(bits >> i) & 1 for i in range(nq)], dtype=bool)
                 vis[s] = (j < p) | np.concatenate([np.zeros(p, dtype=bool), draft])
+        if window is not None:
+            vis &= (j >= max(0, p - int(window)))[None, :]
         for h in range(hkv):
             for gg in range(g):
                 hh = h * g + gg

@@ -81,6 +81,7 @@ struct VerifyArgs {
   int bs_log2;
   int max_context_len;
   int n_qblocks;              // 64-row query blocks per (sequence, KV head)
+  int window;                 // verify_kernel<.., WIN>: only the last `window` prefix keys are visible
   float qscale;
   _Float16* out;              // [batch][Hq][max_queries][D]
 };
@@ -89,7 +90,7 @@ struct VerifyArgs {
 // transpose-read rows (keys 4g..4g+3 and 16+4g..16+4g+3) are rows 8g..8g+7.
 __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool WIN = false>
 __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   using C = Cfg<D, K8V3>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -120,6 +121,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   int kv_end = prefix + (tree ? nq : pos_hi);
   kv_end = min(kv_end, a.max_context_len);
   if (row0 / G >= nq) kv_end = 0;  // no query of this block exists
+  // sliding window: prefix keys below lo_key are invisible to every row; the
+  // key loop starts at the 32-key tile holding lo_key, whose lower keys are masked
+  const int lo_key = WIN ? max(0, prefix - a.window) : 0;
 
   // this lane's column: query row r -> (position, q head)
   const int r = row0 + wave * 16 + c;
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   const uint32_t hkv = (uint32_t)a.num_kv_heads;
   const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
 
-  for (int u0 = 0; u0 < kv_end; u0 += kSubKeys) {
+  for (int u0 = lo_key & ~(kTile - 1); u0 < kv_end; u0 += kSubKeys) {
     const int u1 = min(kv_end, u0 + kSubKeys);
     const int fb = u0 >> bs_log2;
     const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
@@ -275,7 +279,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 #pragma unroll
           for (int q4 = 0; q4 < 8 / C::SPLIT; q4 += 2) {
             u32x4_t o;
-            const uint32_t sel0 = spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
+            const uint32_t sel0 = spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 *
+            q4)) << 2);
             const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
                                   (spread4(w2 >> (4 * q4 + 4)) << 2);
             const u32x2_t r0 = codebook_lookup4(sel0, tlo03, tlo47, thi03, thi47);
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           if constexpr (MASKED) {
             const int kk = base + 16 * s + 4 * g + i;
             const int di = kk - prefix;  // draft index when >= 0
-            bool vis = kk < kv_end && row_live;
+            bool vis = kk < kv_end && row_live && (!WIN || kk >= lo_key);
             if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask >> di) & 1ull)) : di <= pos);
             x = vis ? x : kNegInf;
           }
@@ -384,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       // a tile needs masking when it reaches the drafts or the end of the
       // visible keys (wave-uniform: MFMAs must run with every lane active;
       // rows past the query count are zeroed at the end instead)
-      if (base + kTile <= prefix && base + kTile <= kv_end)
+      if (base + kTile <= prefix && base + kTile <= kv_end && (!WIN || base >= lo_key))
         process(buf, base, std::false_type{});
       else
         process(buf, base, std::true_type{});
@@ -424,12 +429,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   }
 }
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool WIN = false>
 static int launch(VerifyArgs& a, hipStream_t stream) {
   using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -442,7 +447,7 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D, K8V3>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
   return check_launch("s8kv_verify");
 }
 
@@ -496,12 +501,13 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   return S8KV_OK;
 }
 
-extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                 int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
                                 const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
                                 const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                 int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream,
+                            int window) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   verify::VerifyArgs a{};
@@ -509,12 +515,21 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
+  a.window = window;
   S8KV_REQUIRE(v_cache && v_scale, S8KV_ERR_INVALID, "verify: null pointer argument");
   a.v_cache = v_cache;
   a.v_scale = v_scale;
   a.vc_bytes = a.kc_bytes;
   a.vs_bytes = a.ks_bytes;
   hipStream_t s = (hipStream_t)stream;
+  if (a.window > 0) {
+    switch (head_dim) {
+      case 64: return verify::launch<64, false, true>(a, s);
+      case 128: return verify::launch<128, false, true>(a, s);
+      case 256: return verify::launch<256, false, true>(a, s);
+    }
+    return S8KV_ERR_UNSUPPORTED;
+  }
   switch (head_dim) {
     case 64: return verify::launch<64, false>(a, s);
     case 128: return verify::launch<128, false>(a, s);
@@ -523,13 +538,41 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
   return S8KV_ERR_UNSUPPORTED;
 }
 
-extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                                const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
+  return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                          q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
+                          block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
+                          stream, 0);
+}
+
+extern "C" int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
+                                const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
+                                const int64_t* tree_mask, int max_context_len, int window, float scale, void* out,
+                                void* stream) {
+  S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
+  return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                          q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
+                          block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
+                          stream, window);
+}
+
+
+static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                 int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
                                 const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
                                 const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                                 int block_size, const int32_t* block_table, int64_t block_table_stride,
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                                int max_context_len, float scale, void* out, void* stream) {
+                                int max_context_len, float scale, void* out, void* stream,
+                            int window) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
@@ -540,6 +583,7 @@ extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int n
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
+  a.window = window;
   S8KV_REQUIRE(v_packed && v_norm && v_codebook, S8KV_ERR_INVALID, "verify: null pointer argument");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   a.v_cache = v_packed;
@@ -548,5 +592,35 @@ extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int n
   a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
   a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
   hipStream_t s = (hipStream_t)stream;
+  if (a.window > 0)
+    return head_dim == 128 ? verify::launch<128, true, true>(a, s) : verify::launch<256, true, true>(a, s);
   return head_dim == 128 ? verify::launch<128, true>(a, s) : verify::launch<256, true>(a, s);
 }
+
+extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
+                                const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
+                                int max_context_len, float scale, void* out, void* stream) {
+  return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                          q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
+                          block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
+                          max_context_len, scale, out, stream, 0);
+}
+
+extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+                                const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
+                                const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
+                                int max_context_len, int window, float scale, void* out, void* stream) {
+  S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
+  return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
+                          q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
+                          block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
+                          max_context_len, scale, out, stream, window);
+}
+

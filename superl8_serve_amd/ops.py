@@ -438,7 +438,7 @@ def _verify_inputs(q, k_cache, k_scale, block_table, prefix_lens, block_size, qu
 
 
 def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix_lens, block_size, *,
-                      query_lens=None, tree_mask=None, max_context_len, scale):
+                      query_lens=None, tree_mask=None, max_context_len, scale, window=None):
     """Multi-query attention of draft / chunk queries over the int8 paged cache.
 
     ``q``: fp16 ``[B, Hq, S, D]`` (any strides with D contiguous, e.g. the
@@ -448,7 +448,9 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     verify, gqa_attention.py:217-292, and bottom-right causal chunked prefill,
     gqa_attention.py:105-129) or when bit i of ``tree_mask[b, s]`` (int64
     ``[B, S]``) is set (tree verify).  Queries ``s >= query_lens[b]`` give
-    zeros.  Returns fp16 ``[B, Hq, S, D]``."""
+    zeros.  ``window`` (a sliding-window layer): of the prefix only the last
+    ``window`` keys are visible (gqa_attention.py:305-314).  Returns fp16
+    ``[B, Hq, S, D]``."""
     keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
         q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
     dev = out.device
@@ -459,16 +461,23 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     if out.shape[0] == 0 or out.shape[2] == 0:
         return out
     lib = _lib.load()
-    rc = lib.s8kv_verify_int8(
-        *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
-        *tail, float(scale), out.data_ptr(), _stream(keep[0]),
-    )
+    if window is not None:
+        _require(int(window) >= 1, f"window must be >= 1, got {window}")
+        rc = lib.s8kv_verify_window_int8(
+            *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+            *tail, int(window), float(scale), out.data_ptr(), _stream(keep[0]),
+        )
+    else:
+        rc = lib.s8kv_verify_int8(
+            *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
+            *tail, float(scale), out.data_ptr(), _stream(keep[0]),
+        )
     _lib.check(rc, "attn_paged_verify")
     return out
 
 
 def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, prefix_lens, block_size,
-                           *, query_lens=None, tree_mask=None, max_context_len, scale):
+                           *, query_lens=None, tree_mask=None, max_context_len, scale, window=None):
     """``attn_paged_verify`` over the K8V3 cache (int8 K, 3-bit Lloyd-Max V
     ``codebook[code] * block norm``): one launch for what the reference
     computes on a k8v3 cache with S sequential ``attn_paged_decode_k8v3``
@@ -488,10 +497,18 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
     if out.shape[0] == 0 or out.shape[2] == 0:
         return out
     lib = _lib.load()
-    rc = lib.s8kv_verify_k8v3(
-        *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
-        lloyd_block, n, bs, *tail, float(scale), out.data_ptr(), _stream(keep[0]),
-    )
+    if window is not None:
+        _require(int(window) >= 1, f"window must be >= 1, got {window}")
+        rc = lib.s8kv_verify_window_k8v3(
+            *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
+            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, int(window), float(scale), out.data_ptr(),
+            _stream(keep[0]),
+        )
+    else:
+        rc = lib.s8kv_verify_k8v3(
+            *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
+            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, float(scale), out.data_ptr(), _stream(keep[0]),
+        )
     _lib.check(rc, "attn_paged_verify_k8v3")
     return out
 

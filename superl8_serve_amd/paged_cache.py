@@ -446,7 +446,8 @@ class PagedKVCache:
                                        max(ctx) if ctx else 0, scale=scale)
 
     def verify_attn(self, layer: int, q: torch.Tensor, slots: list[int], prefix_lens: list[int], *, scale: float,
-                    query_lens: list[int] | None = None, tree_mask: torch.Tensor | None = None) -> torch.Tensor:
+                    query_lens: list[int] | None = None, tree_mask: torch.Tensor | None = None,
+                    window: int | None = None) -> torch.Tensor:
         """Multi-query attention of drafts (already written at positions
         ``prefix_lens[b] ..``): chain / chunk when `tree_mask` is None, else tree.
         ``q``: fp16 ``[B, Hq, S, D]``."""
@@ -457,7 +458,7 @@ class PagedKVCache:
         common = dict(
             query_lens=None if query_lens is None else torch.tensor(query_lens, dtype=torch.int32, device=self.device),
             tree_mask=tree_mask, max_context_len=min(max_ctx, self.max_blocks_per_seq * self.block_size),
-            scale=scale)
+            scale=scale, window=window)
         bt = self.block_table(slots)
         pl = torch.tensor(prefix_lens, dtype=torch.int32, device=self.device)
         if self.v_quant == "lloydmax3":

@@ -144,3 +144,84 @@ def test_host_cache_windowed_decode():
         ref = O.paged_decode(q[:, :, 0].cpu().numpy(), layer, c.block_table(slots).cpu().numpy(), np.array(lens), 0.1,
                              window=50)
         _close(out[:, :, 0].float().cpu().numpy(), ref, f"{v_quant} via cache")
+
+
+# ---------------------------------------------------------------------------
+# verify attention of a sliding-window layer: the last `window` prefix keys
+# plus the drafts (gqa_attention.py:305-314)
+# ---------------------------------------------------------------------------
+
+
+def _verify_case(seed, batch, hq, hkv, d, bs, prefix, nq, k8v3=False):
+    prefix = np.asarray(prefix)
+    case = make_case(seed, batch, hq, hkv, d, bs, prefix + nq, outlier_channels=2)
+    cache = oracle_fill_k8v3(case, CODEBOOK) if k8v3 else oracle_fill_int8(case)
+    q = np.random.default_rng(seed + 7).standard_normal((batch, hq, nq, d)).astype(np.float16)
+    return case, cache, q, prefix
+
+
+def _verify(case, cache, q, prefix, window, k8v3=False, tree_mask=None):
+    c = [_t(x) for x in cache]
+    kw = dict(tree_mask=None if tree_mask is None else _t(tree_mask),
+              max_context_len=int(case.block_table.shape[1] * case.block_size), scale=case.scale, window=window)
+    bt, pl = _t(case.block_table), _t(prefix.astype(np.int32))
+    if k8v3:
+        out = ops.attn_paged_verify_k8v3(_t(q), *c, _t(CODEBOOK), bt, pl, case.block_size, **kw)
+    else:
+        out = ops.attn_paged_verify(_t(q), *c, bt, pl, case.block_size, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def _verify_ref(case, cache, q, prefix, window, k8v3=False, tree_mask=None):
+    layer = O.LayerCache(cache[0], cache[1], v_packed=cache[2], v_norm=cache[3], v_codebook=CODEBOOK) if k8v3 \
+        else O.LayerCache(*cache)
+    return O.paged_verify(q, layer, case.block_table, prefix, case.scale, tree_mask=tree_mask, window=window)
+
+
+@pytest.mark.parametrize("k8v3,hq,hkv,d,bs,prefix,nq,window", [
+    (False, 8, 2, 128, 16, [1000, 37, 300], 6, 300),     # chain: one row shorter than the window
+    (False, 8, 2, 128, 256, [777, 64], 200, 100),        # a 200-query chunk
+    (False, 16, 16, 64, 4, [90, 50], 5, 33),             # tiny blocks, G = 1
+    (True, 8, 2, 128, 16, [1000, 130], 9, 129),          # K8V3
+    (True, 4, 2, 256, 16, [700, 260], 4, 70),            # K8V3 head_dim 256
+])
+def test_window_verify(k8v3, hq, hkv, d, bs, prefix, nq, window):
+    case, cache, q, pre = _verify_case(600 + d + window, len(prefix), hq, hkv, d, bs, prefix, nq, k8v3)
+    _close(_verify(case, cache, q, pre, window, k8v3), _verify_ref(case, cache, q, pre, window, k8v3),
+           f"verify window {window}")
+
+
+def test_window_tree_verify():
+    rng = np.random.default_rng(5)
+    case, cache, q, pre = _verify_case(611, 2, 16, 4, 128, 16, [2048, 500], 16)
+    masks = []
+    for _ in range(2):
+        m = []
+        for i in range(16):
+            parent = int(rng.integers(0, i)) if i else -1
+            m.append((m[parent] if parent >= 0 else 0) | (1 << i))
+        masks.append(m)
+    masks = np.array(masks, np.int64)
+    _close(_verify(case, cache, q, pre, 400, tree_mask=masks), _verify_ref(case, cache, q, pre, 400, tree_mask=masks),
+           "tree verify window")
+
+
+def test_window_verify_covering_the_prefix_equals_verify():
+    case, cache, q, pre = _verify_case(621, 3, 8, 2, 128, 16, [300, 37, 256], 7)
+    assert np.array_equal(_verify(case, cache, q, pre, 300), _verify(case, cache, q, pre, None))
+
+
+def test_window_verify_ignores_keys_before_the_window():
+    case, cache, q, pre = _verify_case(631, 2, 8, 2, 128, 16, [400, 150], 5)
+    window = 61
+    before = _verify(case, cache, q, pre, window)
+    kc, ks, vc, vs = (x.copy() for x in cache)
+    for b, p in enumerate(pre):
+        for pos in range(max(0, int(p) - window)):
+            blk, off = case.block_table[b, pos // case.block_size], pos % case.block_size
+            kc[blk, :, off] = 127
+            ks[blk, :, off] = 1e4
+            vc[blk, :, off] = -127
+            vs[blk, :, off] = 1e4
+    assert np.array_equal(_verify(case, (kc, ks, vc, vs), q, pre, window), before)

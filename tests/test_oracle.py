@@ -461,3 +461,30 @@ def test_paged_decode_window():
         ks[blk, :, off] = 1e3
     assert np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125, window=w), before)
     assert not np.array_equal(O.paged_decode(q, layer, bt, lens, 0.125), full)
+
+
+def test_paged_verify_window():
+    """Verify of a sliding-window layer sees only the last `window` prefix keys:
+    window >= prefix is the plain verify, keys before the window do not matter."""
+    rng = np.random.default_rng(13)
+    hq, hkv, d, bs, p, s = 4, 2, 64, 16, 50, 4
+    n = p + s
+    k = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    nb = (n + bs - 1) // bs
+    kc, ks = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    vc, vs = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    bt = np.arange(nb, dtype=np.int32)[None][:, ::-1].copy()
+    slots = (bt[0, np.arange(n) // bs] * bs + np.arange(n) % bs).astype(np.int32)
+    O.quantize_kv_write_paged(k, v, kc, ks, vc, vs, slots)
+    layer = O.LayerCache(kc, ks, vc, vs)
+    q = rng.standard_normal((1, hq, s, d))
+    pl = np.array([p])
+    full = O.paged_verify(q, layer, bt, pl, 0.125)
+    assert np.array_equal(O.paged_verify(q, layer, bt, pl, 0.125, window=p), full)
+    w = 20
+    before = O.paged_verify(q, layer, bt, pl, 0.125, window=w)
+    assert not np.allclose(before, full)
+    for pos in range(p - w):
+        kc[bt[0, pos // bs], :, pos % bs] = 127
+    assert np.array_equal(O.paged_verify(q, layer, bt, pl, 0.125, window=w), before)
