@@ -257,6 +257,25 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
                             int max_context_len, int window, float scale, void* out, void* stream);
 
 /*
+ * Prefill attention over fresh fp16 K / V (not the cache), varlen batched:
+ * the role of superl8.attn_int8_varlen (gqa_attention.py:81-104) and of
+ * attn_int8_fwd over fresh K / V (gqa_attention.py:124-128).  Sequence b's
+ * queries are tokens cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 of q
+ * [tokens, num_q_heads, head_dim] and its keys tokens cu_seqlens_k[b] .. of
+ * k, v [tokens, num_kv_heads, head_dim] (element strides per token and head,
+ * head_dim contiguous; K and V rows 16-byte aligned).  causal: query s sees
+ * keys j <= s + nk - nq (bottom-right aligned; none when that is negative),
+ * else all nk keys.  out [tokens_q, num_q_heads, head_dim] with strides
+ * o_stride_t, o_stride_h; only the sequences' own query tokens are written.
+ * head_dim 64, 128 or 256; at most 16 q heads per KV head.
+ */
+int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                         int max_seqlen_q, int max_seqlen_k, int64_t q_stride_t, int64_t q_stride_h,
+                         int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h, int causal,
+                         float scale, void* out, int64_t o_stride_t, int64_t o_stride_h, void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its kernel with HIP events stamped with the

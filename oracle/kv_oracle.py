@@ -490,6 +490,35 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
     return out
 
 
+def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True) -> np.ndarray:
+    """Prefill attention over fresh K / V in float64 (the role of
+    ``superl8.attn_int8_varlen``, gqa_attention.py:81-104): q ``[Tq, Hq, D]``,
+    k, v ``[Tk, Hkv, D]``; sequence b = query tokens ``cu_q[b] ..``, key tokens
+    ``cu_k[b] ..``; causal is bottom-right aligned (query s sees keys
+    ``j <= s + nk - nq``; a query that sees none gives zeros).  The reference's
+    kernel is absent (the superl8 package), so this is the exact attention the
+    reference's int8 kernel approximates.  Returns float64 ``[Tq, Hq, D]``."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    hq, hkv = q.shape[1], k.shape[1]
+    g = hq // hkv
+    out = np.zeros_like(q)
+    for b in range(len(cu_q) - 1):
+        qs, qe, ks_, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        nq, nk = qe - qs, ke - ks_
+        if nq <= 0 or nk <= 0:
+            continue
+        j = np.arange(nk)
+        vis = (j[None, :] <= np.arange(nq)[:, None] + nk - nq) if causal else np.ones((nq, nk), bool)
+        live = vis.any(axis=1)
+        for h in range(hq):
+            kv = h // g
+            o = _softmax_attend(q[qs:qe, h][live], k[ks_:ke, kv], v[ks_:ke, kv], scale, vis[live])
+            out[np.arange(qs, qe)[live], h] = o
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Block copy (copy-on-write / compaction)
 # ---------------------------------------------------------------------------

@@ -55,6 +55,8 @@ struct Cfg {
   static constexpr int BUF = KBYTES + VBYTES + SBYTES;
   static constexpr int CHUNKS = kTile * D / 16;                 // 16-byte int8 chunks per K (or V) tile
   static constexpr int LOADS = (CHUNKS + kThreads - 1) / kThreads;
+  static constexpr int CHUNKS_F16 = kTile * D / 8;              // dense fp16 inputs: 16-byte chunks per tile
+  static constexpr int LOADS_F16 = (CHUNKS_F16 + kThreads - 1) / kThreads;
   // K8V3: a code group's 32 values are expanded by SPLIT threads (16 values
   // each when the tile has fewer groups than the workgroup has threads)
   static constexpr int SPLIT = kTile * NG < kThreads ? kThreads / (kTile * NG) : 1;
@@ -82,6 +84,14 @@ struct VerifyArgs {
   int max_context_len;
   int n_qblocks;              // 64-row query blocks per (sequence, KV head)
   int window;                 // verify_kernel<.., WIN>: only the last `window` prefix keys are visible
+  // dense inputs (verify_kernel<D, false, false, true>: prefill attention over
+  // fresh fp16 K / V, token-major, sequences delimited by cu_seqlens)
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const _Float16* k_f16;
+  const _Float16* v_f16;
+  int64_t k_stride_t, k_stride_h, v_stride_t, v_stride_h, o_stride_t, o_stride_h;
+  int causal;
   float qscale;
   _Float16* out;              // [batch][Hq][max_queries][D]
 };
@@ -90,8 +100,9 @@ struct VerifyArgs {
 // transpose-read rows (keys 4g..4g+3 and 16+4g..16+4g+3) are rows 8g..8g+7.
 __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-template <int D, bool K8V3, bool WIN = false>
+template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
 __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
+  static_assert(!DENSE || (!K8V3 && !WIN), "dense inputs: fp16 K / V, no window");
   using C = Cfg<D, K8V3>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
@@ -112,14 +123,26 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  const int nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
-  const int prefix = max(0, a.prefix_lens[b]);
+  // dense: sequence b's queries are tokens cu_q[b] .., its keys cu_k[b] ..;
+  // causal is bottom-right aligned (query s sees keys j <= s + nk - nq, which
+  // may be none), else every key is visible
+  int nq, prefix, nk = 0, q0 = 0, k0 = 0;
+  if constexpr (DENSE) {
+    q0 = a.cu_q[b];
+    k0 = a.cu_k[b];
+    nq = max(0, min(a.cu_q[b + 1] - q0, a.max_queries));
+    nk = max(0, min(a.cu_k[b + 1] - k0, a.max_context_len));
+    prefix = a.causal ? nk - nq : nk;
+  } else {
+    nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
+    prefix = max(0, a.prefix_lens[b]);
+  }
   const int row0 = qb * kRowsPerWg;                 // first row of the workgroup
   const int pos_hi = min(nq, (row0 + kRowsPerWg + G - 1) / G);  // positions of this block that exist
   const bool tree = a.tree_mask != nullptr;
   // keys any row of this block can see
   int kv_end = prefix + (tree ? nq : pos_hi);
-  kv_end = min(kv_end, a.max_context_len);
+  kv_end = min(kv_end, DENSE ? nk : a.max_context_len);
   if (row0 / G >= nq) kv_end = 0;  // no query of this block exists
   // sliding window: prefix keys below lo_key are invisible to every row; the
   // key loop starts at the 32-key tile holding lo_key, whose lower keys are masked
@@ -136,12 +159,14 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   half8_t qhi[C::NQK], qlo[C::NQK];
   {
     float x[C::KCH];
-    const _Float16* qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)head * a.q_stride_h +
-                         (int64_t)(row_live ? pos : 0) * a.q_stride_s + g * C::KCH;
+    const int64_t qrow = DENSE ? (int64_t)q0 * a.q_stride_s : (int64_t)b * a.q_stride_b;
+    const _Float16* qp = a.q + qrow + (int64_t)head * a.q_stride_h + (int64_t)(row_live ? pos : 0) * a.q_stride_s +
+                         g * C::KCH;
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) x[i] = row_live ? (float)qp[i] : 0.0f;
+    // dense inputs: K is not rotated, so neither is q
 #pragma unroll
-    for (int hs = 1; hs < C::KCH; hs <<= 1) {
+    for (int hs = 1; hs < (DENSE ? 1 : C::KCH); hs <<= 1) {
 #pragma unroll
       for (int i = 0; i < C::KCH; ++i) {
         if ((i & hs) == 0) {
@@ -151,10 +176,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         }
       }
     }
+    if constexpr (!DENSE) {
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x16(x[i], lane);
+      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x16(x[i], lane);
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x32(x[i], lane);
+      for (int i = 0; i < C::KCH; ++i) x[i] = butterfly_x32(x[i], lane);
+    }
 #pragma unroll
     for (int m = 0; m < C::NQK; ++m) {
 #pragma unroll
@@ -200,7 +227,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     const int fb = u0 >> bs_log2;
     const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
     __syncthreads();  // previous users of bt_lds and the tile buffers are done
-    for (int i = tid; i < nblk; i += kThreads) bt_lds[i] = bt_row[fb + i];
+    if constexpr (!DENSE)
+      for (int i = tid; i < nblk; i += kThreads) bt_lds[i] = bt_row[fb + i];
     __syncthreads();
 
     // storage row of key kk (clamped to the last key, so every address is a real row)
@@ -212,11 +240,26 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 
     // ---- cooperative tile load: int8 K/V chunks (K8V3: a code group's three
     // words per thread) and scales -> registers ----
+    constexpr int NREG = DENSE ? C::LOADS_F16 : C::LOADS;
     struct TileRegs {
-      u32x4_t k[C::LOADS], v[C::LOADS];
+      u32x4_t k[NREG], v[NREG];
       float s;
     };
     auto load_tile = [&](TileRegs& R, int base) {
+      if constexpr (DENSE) {  // fp16 K / V rows of keys base .. base+31 (clamped to the last key)
+#pragma unroll
+        for (int i = 0; i < C::LOADS_F16; ++i) {
+          const int ch = tid + i * kThreads;
+          if (ch < C::CHUNKS_F16) {
+            const int tt = ch / (D / 8), part = ch % (D / 8);
+            const int64_t tok = k0 + min(base + tt, nk - 1);
+            R.k[i] = *reinterpret_cast<const u32x4_t*>(a.k_f16 + tok * a.k_stride_t + h * a.k_stride_h + part * 8);
+            R.v[i] = *reinterpret_cast<const u32x4_t*>(a.v_f16 + tok * a.v_stride_t + h * a.v_stride_h + part * 8);
+          }
+        }
+        R.s = 1.0f;
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < C::LOADS; ++i) {
         const int ch = tid + i * kThreads;
@@ -252,6 +295,19 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       char* kb = smem + buf * C::BUF;
       char* vb = kb + C::KBYTES;
       float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
+      if constexpr (DENSE) {
+#pragma unroll
+        for (int i = 0; i < C::LOADS_F16; ++i) {
+          const int ch = tid + i * kThreads;
+          if (ch < C::CHUNKS_F16) {
+            const int tt = ch / (D / 8), part = ch % (D / 8);
+            *reinterpret_cast<u32x4_t*>(kb + tt * C::KROW + part * 16) = R.k[i];
+            *reinterpret_cast<u32x4_t*>(vb + vrow_of(tt) * C::VROW + part * 16) = R.v[i];
+          }
+        }
+        if (tid < 2 * kTile) sb[tid] = R.s;
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < C::LOADS; ++i) {
         const int ch = tid + i * kThreads;
@@ -416,9 +472,11 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 
   // ---- normalize and write this wave's 16 rows ----
   const float l_tot = sum_x32(sum_x16(l_run));
-  if (pos < a.max_queries && (r - pos * G) < G) {
+  // (dense: only the sequence's own query tokens -- the next ones belong to the next sequence)
+  if ((DENSE ? row_live : pos < a.max_queries) && (r - pos * G) < G) {
     const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    _Float16* op = a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
+    _Float16* op = DENSE ? a.out + (int64_t)(q0 + pos) * a.o_stride_t + (int64_t)head * a.o_stride_h
+                         : a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) {
       half4_t o;
@@ -429,12 +487,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   }
 }
 
-template <int D, bool K8V3, bool WIN = false>
+template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
 static int launch(VerifyArgs& a, hipStream_t stream) {
   using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN, DENSE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -447,7 +505,7 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
   return check_launch("s8kv_verify");
 }
 
@@ -624,3 +682,56 @@ extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads
                           max_context_len, scale, out, stream, window);
 }
 
+
+extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
+                                    const int32_t* cu_seqlens_k, int batch, int num_q_heads, int num_kv_heads,
+                                    int head_dim, int max_seqlen_q, int max_seqlen_k, int64_t q_stride_t,
+                                    int64_t q_stride_h, int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t,
+                                    int64_t v_stride_h, int causal, float scale, void* out, int64_t o_stride_t,
+                                    int64_t o_stride_h, void* stream) {
+  S8KV_REQUIRE(batch >= 0 && max_seqlen_q >= 0 && max_seqlen_k >= 0, S8KV_ERR_INVALID,
+               "attn_varlen: negative batch or sequence length");
+  if (batch == 0 || max_seqlen_q == 0) return S8KV_OK;
+  S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
+               "attn_varlen: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
+  S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "attn_varlen: more than 16 q heads per kv head");
+  S8KV_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
+               "attn_varlen: head_dim %d not in {64, 128, 256}", head_dim);
+  S8KV_REQUIRE(q && k && v && cu_seqlens_q && cu_seqlens_k && out, S8KV_ERR_INVALID,
+               "attn_varlen: null pointer argument");
+  S8KV_REQUIRE((uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && k_stride_t % 8 == 0 && k_stride_h % 8 == 0 &&
+                   v_stride_t % 8 == 0 && v_stride_h % 8 == 0,
+               S8KV_ERR_INVALID, "attn_varlen: K and V rows must be 16-byte aligned");
+  verify::VerifyArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_s = q_stride_t;
+  a.q_stride_h = q_stride_h;
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.max_queries = max_seqlen_q;
+  a.max_context_len = max_seqlen_k;
+  a.bs_log2 = 5;
+  a.n_qblocks = (a.group * max_seqlen_q + verify::kRowsPerWg - 1) / verify::kRowsPerWg;
+  a.qscale = (float)((double)scale * 1.4426950408889634);  // K is not rotated: no 1/sqrt(D)
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.k_f16 = (const _Float16*)k;
+  a.v_f16 = (const _Float16*)v;
+  a.k_stride_t = k_stride_t;
+  a.k_stride_h = k_stride_h;
+  a.v_stride_t = v_stride_t;
+  a.v_stride_h = v_stride_h;
+  a.o_stride_t = o_stride_t;
+  a.o_stride_h = o_stride_h;
+  a.causal = causal ? 1 : 0;
+  a.out = (_Float16*)out;
+  hipStream_t s = (hipStream_t)stream;
+  switch (head_dim) {
+    case 64: return verify::launch<64, false, false, true>(a, s);
+    case 128: return verify::launch<128, false, false, true>(a, s);
+    case 256: return verify::launch<256, false, false, true>(a, s);
+  }
+  return S8KV_ERR_UNSUPPORTED;
+}

@@ -30,6 +30,8 @@ __all__ = [
     "decode_workspace_bytes",
     "attn_paged_verify",
     "attn_paged_verify_k8v3",
+    "attn_varlen",
+    "attn_fwd",
     "copy_blocks",
 ]
 
@@ -511,6 +513,64 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
         )
     _lib.check(rc, "attn_paged_verify_k8v3")
     return out
+
+
+def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *, causal, scale):
+    """Prefill attention over fresh fp16 K / V, varlen batched (the role of
+    ``superl8.attn_int8_varlen``, gqa_attention.py:81-104): ``q`` fp16
+    ``[Tq, Hq, D]``, ``k``, ``v`` fp16 ``[Tk, Hkv, D]`` token-major (head_dim
+    contiguous), sequences delimited by int32 ``cu_seqlens_q`` / ``cu_seqlens_k``
+    (``[B + 1]``).  ``causal``: bottom-right aligned.  Returns fp16
+    ``[Tq, Hq, D]``."""
+    _on_gpu("q", q, torch.float16)
+    dev = q.device
+    _on_gpu("k", k, torch.float16, dev)
+    _on_gpu("v", v, torch.float16, dev)
+    _on_gpu("cu_seqlens_q", cu_seqlens_q, torch.int32, dev)
+    _on_gpu("cu_seqlens_k", cu_seqlens_k, torch.int32, dev)
+    _require(q.dim() == 3 and k.dim() == 3 and v.shape == k.shape and k.shape[2] == q.shape[2],
+             "attn_varlen: q [Tq, Hq, D], k / v [Tk, Hkv, D]")
+    tq, hq, d = q.shape
+    hkv = k.shape[1]
+    _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.shape == cu_seqlens_k.shape and cu_seqlens_q.numel() >= 1,
+             "attn_varlen: cu_seqlens_q / cu_seqlens_k must be [B + 1]")
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    if k.stride(2) != 1 or k.data_ptr() % 16 or k.stride(0) % 8 or k.stride(1) % 8:
+        k = k.contiguous()
+    if v.stride(2) != 1 or v.data_ptr() % 16 or v.stride(0) % 8 or v.stride(1) % 8:
+        v = v.contiguous()
+    cu_q, cu_k = cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous()
+    out = torch.zeros((tq, hq, d), dtype=torch.float16, device=dev)
+    b = cu_q.numel() - 1
+    if b == 0 or tq == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.s8kv_attn_varlen_f16(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(), b, hq, hkv, d,
+        int(max_seqlen_q), int(max_seqlen_k), q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0),
+        v.stride(1), 1 if causal else 0, float(scale), out.data_ptr(), out.stride(0), out.stride(1), _stream(q),
+    )
+    _lib.check(rc, "attn_varlen")
+    return out
+
+
+def attn_fwd(q, k, v, *, causal, scale):
+    """Dense prefill attention over fresh fp16 K / V in the ``[B, H, S, D]``
+    layout (the role of ``superl8.attn_int8_fwd`` on fresh K / V,
+    gqa_attention.py:124-128): ``q`` ``[B, Hq, Sq, D]``, ``k``, ``v``
+    ``[B, Hkv, Sk, D]``; causal is bottom-right aligned.  Runs
+    ``attn_varlen`` on token-major copies.  Returns fp16 ``[B, Hq, Sq, D]``."""
+    _require(q.dim() == 4 and k.dim() == 4 and v.shape == k.shape, "attn_fwd: q [B, Hq, Sq, D], k / v [B, Hkv, Sk, D]")
+    b, hq, sq, d = q.shape
+    sk = k.shape[2]
+    qt = q.transpose(1, 2).reshape(b * sq, hq, d)
+    kt = k.transpose(1, 2).reshape(b * sk, k.shape[1], d)
+    vt = v.transpose(1, 2).reshape(b * sk, v.shape[1], d)
+    cu_q = torch.arange(0, (b + 1) * sq, sq, dtype=torch.int32, device=q.device)
+    cu_k = torch.arange(0, (b + 1) * sk, sk, dtype=torch.int32, device=q.device)
+    out = attn_varlen(qt, kt, vt, cu_q, cu_k, sq, sk, causal=causal, scale=scale)
+    return out.reshape(b, sq, hq, d).transpose(1, 2)
 
 
 def copy_blocks(tensors: Sequence[torch.Tensor], src: Sequence[int] | torch.Tensor,

@@ -488,3 +488,25 @@ def test_paged_verify_window():
     for pos in range(p - w):
         kc[bt[0, pos // bs], :, pos % bs] = 127
     assert np.array_equal(O.paged_verify(q, layer, bt, pl, 0.125, window=w), before)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_dense_varlen_attention_matches_torch_sdpa(causal):
+    """The dense prefill oracle against torch's float64 scaled_dot_product_attention
+    with an explicitly built bottom-right causal mask, GQA by repeated KV heads."""
+    rng = np.random.default_rng(21)
+    hq, hkv, d = 8, 2, 32
+    qlens, klens = [5, 1, 9, 7], [5, 4, 20, 7]  # equal, chunked (nq < nk), and a one-token query
+    cu_q, cu_k = np.cumsum([0] + qlens), np.cumsum([0] + klens)
+    q = rng.standard_normal((cu_q[-1], hq, d))
+    k = rng.standard_normal((cu_k[-1], hkv, d))
+    v = rng.standard_normal((cu_k[-1], hkv, d))
+    got = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.3, causal)
+    for b in range(len(qlens)):
+        nq, nk = qlens[b], klens[b]
+        qb = torch.from_numpy(q[cu_q[b]:cu_q[b + 1]]).permute(1, 0, 2)
+        kb = torch.from_numpy(k[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        vb = torch.from_numpy(v[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        mask = torch.ones(nq, nk, dtype=torch.bool).tril(diagonal=nk - nq) if causal else None
+        ref = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask, scale=0.3)
+        assert np.allclose(got[cu_q[b]:cu_q[b + 1]], ref.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
