@@ -575,6 +575,61 @@ def run_append(steps: int, warmup: int, k8v3: bool = False) -> None:
                       "bytes_per_call": moved, "pct_of_hbm_peak": round(100 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
 
 
+PREFILL_SEQS, PREFILL_LEN = 16, 4096
+
+
+def run_prefill(steps: int, warmup: int) -> None:
+    """Dense causal prefill attention over fresh fp16 K / V (attn_varlen):
+    16 prompts of 4096 tokens, Qwen3-8B heads (Hq 32, Hkv 8, D 128), four
+    rotated layers of distinct inputs.  Useful flops: 4*D*Hq per visible
+    (query, key) pair."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    rng = np.random.default_rng(6)
+    t = PREFILL_SEQS * PREFILL_LEN
+    cu = torch.arange(0, t + 1, PREFILL_LEN, dtype=torch.int32, device=dev)
+    layers = []
+    for _ in range(4):
+        ch = torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(dev)
+        layers.append((_fp16_outliers(gen, (t, HQ, D), ch, dev), _fp16_outliers(gen, (t, HKV, D), ch, dev),
+                       _fp16_outliers(gen, (t, HKV, D), ch, dev)))
+    scale = 1.0 / math.sqrt(D)
+
+    def attend(i):
+        q, k, v = layers[i % 4]
+        return ops.attn_varlen(q, k, v, cu, cu, PREFILL_LEN, PREFILL_LEN, causal=True, scale=scale)
+
+    for i in range(warmup * 4):
+        attend(i)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(steps * 4):
+        attend(i)
+    en.record()
+    torch.cuda.synchronize()
+    sec = st.elapsed_time(en) * 1e-3 / (steps * 4)
+    flops = 4 * D * HQ * PREFILL_SEQS * PREFILL_LEN * (PREFILL_LEN + 1) // 2
+    tflops = flops / sec / 1e12
+    print(json.dumps({
+        "metric": "dense causal prefill attention TFLOP/s (fresh fp16 K/V), 16 x 4096 tokens, Qwen3-8B heads",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_layer": round(sec * 1e3, 4), "higher_is_better": True,
+        "dtype": "fp16 inputs, fp16 MFMA (hi+lo split q and P), fp32 accumulate",
+        "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20, seed 6)",
+        "config": {"workload": "dense varlen prefill attention", "sequences": PREFILL_SEQS, "tokens": PREFILL_LEN,
+                   "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "flops_layer": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4),
+                     "note": "useful flops; the kernel issues 2x MFMAs (hi+lo operands)"},
+    }))
+
+
 WINDOW = 4096
 WINDOW_LAYERS = 4  # distinct storage, rotated so no layer is served from the Infinity Cache
 
@@ -701,11 +756,12 @@ def main():
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
     ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "window",
-                                           "copy", "append", "append_k8v3"],
+                                           "prefill", "copy", "append", "append_k8v3"],
                     default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
                          "attention (chunk_k8v3 / tree_k8v3: over the K8V3 cache); k8v3: the K8V3 decode step "
-                         "(batch 32, 8k-32k); window: sliding-window decode (batch 64, window 4096); copy: "
+                         "(batch 32, 8k-32k); window: sliding-window decode (batch 64, window 4096); prefill: dense "
+                         "causal prefill attention (16 x 4096 tokens); copy: "
                          "copy_blocks; append / append_k8v3: prefill append of 131,072 tokens")
     args = ap.parse_args()
 
@@ -736,6 +792,9 @@ def main():
         return
     if args.workload == "window":
         run_window(args.steps, args.warmup)
+        return
+    if args.workload == "prefill":
+        run_prefill(args.steps, args.warmup)
         return
     if args.workload in ("append", "append_k8v3"):
         run_append(args.steps, args.warmup, k8v3=args.workload == "append_k8v3")

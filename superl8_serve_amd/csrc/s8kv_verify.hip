@@ -147,6 +147,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   // sliding window: prefix keys below lo_key are invisible to every row; the
   // key loop starts at the 32-key tile holding lo_key, whose lower keys are masked
   const int lo_key = WIN ? max(0, prefix - a.window) : 0;
+  // keys below vis_all are visible to every row of the block: the prefix, and
+  // for a chain / causal block also the drafts up to its first position
+  const int vis_all = tree ? prefix : prefix + row0 / G + 1;
 
   // this lane's column: query row r -> (position, q head)
   const int r = row0 + wave * 16 + c;
@@ -442,10 +445,11 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     // two tiles ahead into two register sets (A for even tiles, B for odd),
     // so a load has two tiles of compute to arrive.
     auto compute = [&](int buf, int base) {
-      // a tile needs masking when it reaches the drafts or the end of the
-      // visible keys (wave-uniform: MFMAs must run with every lane active;
-      // rows past the query count are zeroed at the end instead)
-      if (base + kTile <= prefix && base + kTile <= kv_end && (!WIN || base >= lo_key))
+      // a tile needs masking when it reaches keys that some row of the block
+      // does not see, or the end of the visible keys (wave-uniform: MFMAs must
+      // run with every lane active; rows past the query count are zeroed at the
+      // end instead)
+      if (base + kTile <= vis_all && base + kTile <= kv_end && (!WIN || base >= lo_key))
         process(buf, base, std::false_type{});
       else
         process(buf, base, std::true_type{});
