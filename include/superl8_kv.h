@@ -265,7 +265,9 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * k, v [tokens, num_kv_heads, head_dim] (element strides per token and head,
  * head_dim contiguous; K and V rows 16-byte aligned).  causal: query s sees
  * keys j <= s + nk - nq (bottom-right aligned; none when that is negative),
- * else all nk keys.  out [tokens_q, num_q_heads, head_dim] with strides
+ * else all nk keys; window_left >= 0 (causal only) also hides keys
+ * j < s + nk - nq - window_left (a sliding-window layer), -1 for none.
+ * out [tokens_q, num_q_heads, head_dim] with strides
  * o_stride_t, o_stride_h; only the sequences' own query tokens are written.
  * head_dim 64, 128 or 256; at most 16 q heads per KV head.
  */
@@ -273,7 +275,8 @@ int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v, const int3
                          const int32_t* cu_seqlens_k, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                          int max_seqlen_q, int max_seqlen_k, int64_t q_stride_t, int64_t q_stride_h,
                          int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h, int causal,
-                         float scale, void* out, int64_t o_stride_t, int64_t o_stride_h, void* stream);
+                         int window_left, float scale, void* out, int64_t o_stride_t, int64_t o_stride_h,
+                         void* stream);
 
 /*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between

@@ -490,14 +490,17 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
     return out
 
 
-def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True) -> np.ndarray:
+def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True, window_left=None) -> np.ndarray:
     """Prefill attention over fresh K / V in float64 (the role of
     ``superl8.attn_int8_varlen``, gqa_attention.py:81-104): q ``[Tq, Hq, D]``,
     k, v ``[Tk, Hkv, D]``; sequence b = query tokens ``cu_q[b] ..``, key tokens
     ``cu_k[b] ..``; causal is bottom-right aligned (query s sees keys
     ``j <= s + nk - nq``; a query that sees none gives zeros).  The reference's
     kernel is absent (the superl8 package), so this is the exact attention the
-    reference's int8 kernel approximates.  Returns float64 ``[Tq, Hq, D]``."""
+    reference's int8 kernel approximates.  CHOICE: ``window_left`` (causal
+    only) follows the flash-attention convention the reference's
+    ``window_left`` argument comes from: query i (aligned bottom-right) sees
+    keys ``i - window_left .. i``.  Returns float64 ``[Tq, Hq, D]``."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -511,6 +514,8 @@ def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True) -> np.ndarra
             continue
         j = np.arange(nk)
         vis = (j[None, :] <= np.arange(nq)[:, None] + nk - nq) if causal else np.ones((nq, nk), bool)
+        if window_left is not None:
+            vis &= j[None, :] >= np.arange(nq)[:, None] + nk - nq - int(window_left)
         live = vis.any(axis=1)
         for h in range(hq):
             kv = h // g

@@ -109,7 +109,7 @@ SIGNATURES: dict[str, tuple] = {
     ]),
     "s8kv_attn_varlen_f16": (_i32, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
-        _i64, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _c_void_p, _i64, _i64, _c_void_p,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _f32, _c_void_p, _i64, _i64, _c_void_p,
     ]),
     "s8kv_timing_begin": (_i32, []),
     "s8kv_timing_end": (_i32, [ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),

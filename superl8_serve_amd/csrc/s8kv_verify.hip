@@ -102,7 +102,7 @@ __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4
 
 template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
 __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
-  static_assert(!DENSE || (!K8V3 && !WIN), "dense inputs: fp16 K / V, no window");
+  static_assert(!DENSE || !K8V3, "dense inputs: fp16 K / V");
   using C = Cfg<D, K8V3>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
@@ -146,7 +146,11 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   if (row0 / G >= nq) kv_end = 0;  // no query of this block exists
   // sliding window: prefix keys below lo_key are invisible to every row; the
   // key loop starts at the 32-key tile holding lo_key, whose lower keys are masked
-  const int lo_key = WIN ? max(0, prefix - a.window) : 0;
+  // (dense inputs: a band -- query s sees keys j >= prefix + s - window, so the
+  // block's loop starts at its first position's bound and keys from its last
+  // position's bound on are visible to every row)
+  const int lo_key = WIN ? max(0, prefix + (DENSE ? row0 / G : 0) - a.window) : 0;
+  const int lo_all = WIN && DENSE ? prefix + min(nq - 1, (row0 + kRowsPerWg - 1) / G) - a.window : lo_key;
   // keys below vis_all are visible to every row of the block: the prefix, and
   // for a chain / causal block also the drafts up to its first position
   const int vis_all = tree ? prefix : prefix + row0 / G + 1;
@@ -388,7 +392,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           if constexpr (MASKED) {
             const int kk = base + 16 * s + 4 * g + i;
             const int di = kk - prefix;  // draft index when >= 0
-            bool vis = kk < kv_end && row_live && (!WIN || kk >= lo_key);
+            bool vis = kk < kv_end && row_live && (!WIN || kk >= (DENSE ? prefix + pos - a.window : lo_key));
             if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask >> di) & 1ull)) : di <= pos);
             x = vis ? x : kNegInf;
           }
@@ -449,7 +453,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       // does not see, or the end of the visible keys (wave-uniform: MFMAs must
       // run with every lane active; rows past the query count are zeroed at the
       // end instead)
-      if (base + kTile <= vis_all && base + kTile <= kv_end && (!WIN || base >= lo_key))
+      if (base + kTile <= vis_all && base + kTile <= kv_end && (!WIN || base >= lo_all))
         process(buf, base, std::false_type{});
       else
         process(buf, base, std::true_type{});
@@ -691,8 +695,8 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
                                     const int32_t* cu_seqlens_k, int batch, int num_q_heads, int num_kv_heads,
                                     int head_dim, int max_seqlen_q, int max_seqlen_k, int64_t q_stride_t,
                                     int64_t q_stride_h, int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t,
-                                    int64_t v_stride_h, int causal, float scale, void* out, int64_t o_stride_t,
-                                    int64_t o_stride_h, void* stream) {
+                                    int64_t v_stride_h, int causal, int window_left, float scale, void* out,
+                                    int64_t o_stride_t, int64_t o_stride_h, void* stream) {
   S8KV_REQUIRE(batch >= 0 && max_seqlen_q >= 0 && max_seqlen_k >= 0, S8KV_ERR_INVALID,
                "attn_varlen: negative batch or sequence length");
   if (batch == 0 || max_seqlen_q == 0) return S8KV_OK;
@@ -703,6 +707,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
                "attn_varlen: head_dim %d not in {64, 128, 256}", head_dim);
   S8KV_REQUIRE(q && k && v && cu_seqlens_q && cu_seqlens_k && out, S8KV_ERR_INVALID,
                "attn_varlen: null pointer argument");
+  S8KV_REQUIRE(window_left < 0 || causal, S8KV_ERR_UNSUPPORTED, "attn_varlen: window_left needs causal");
   S8KV_REQUIRE((uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && k_stride_t % 8 == 0 && k_stride_h % 8 == 0 &&
                    v_stride_t % 8 == 0 && v_stride_h % 8 == 0,
                S8KV_ERR_INVALID, "attn_varlen: K and V rows must be 16-byte aligned");
@@ -732,6 +737,15 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.causal = causal ? 1 : 0;
   a.out = (_Float16*)out;
   hipStream_t s = (hipStream_t)stream;
+  if (window_left >= 0) {  // query s sees keys [s + nk - nq - window_left, s + nk - nq]
+    a.window = window_left;
+    switch (head_dim) {
+      case 64: return verify::launch<64, false, true, true>(a, s);
+      case 128: return verify::launch<128, false, true, true>(a, s);
+      case 256: return verify::launch<256, false, true, true>(a, s);
+    }
+    return S8KV_ERR_UNSUPPORTED;
+  }
   switch (head_dim) {
     case 64: return verify::launch<64, false, false, true>(a, s);
     case 128: return verify::launch<128, false, false, true>(a, s);

@@ -515,12 +515,14 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
     return out
 
 
-def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *, causal, scale):
+def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *, causal, scale, window_left=None):
     """Prefill attention over fresh fp16 K / V, varlen batched (the role of
     ``superl8.attn_int8_varlen``, gqa_attention.py:81-104): ``q`` fp16
     ``[Tq, Hq, D]``, ``k``, ``v`` fp16 ``[Tk, Hkv, D]`` token-major (head_dim
     contiguous), sequences delimited by int32 ``cu_seqlens_q`` / ``cu_seqlens_k``
-    (``[B + 1]``).  ``causal``: bottom-right aligned.  Returns fp16
+    (``[B + 1]``).  ``causal``: bottom-right aligned.  ``window_left``
+    (causal only): query i also sees no key below ``i - window_left`` (the
+    flash-attention convention, i aligned bottom-right).  Returns fp16
     ``[Tq, Hq, D]``."""
     _on_gpu("q", q, torch.float16)
     dev = q.device
@@ -549,17 +551,19 @@ def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
     rc = lib.s8kv_attn_varlen_f16(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(), b, hq, hkv, d,
         int(max_seqlen_q), int(max_seqlen_k), q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0),
-        v.stride(1), 1 if causal else 0, float(scale), out.data_ptr(), out.stride(0), out.stride(1), _stream(q),
+        v.stride(1), 1 if causal else 0, -1 if window_left is None else int(window_left), float(scale),
+        out.data_ptr(), out.stride(0), out.stride(1), _stream(q),
     )
     _lib.check(rc, "attn_varlen")
     return out
 
 
-def attn_fwd(q, k, v, *, causal, scale):
+def attn_fwd(q, k, v, *, causal, scale, window_left=None):
     """Dense prefill attention over fresh fp16 K / V in the ``[B, H, S, D]``
     layout (the role of ``superl8.attn_int8_fwd`` on fresh K / V,
     gqa_attention.py:124-128): ``q`` ``[B, Hq, Sq, D]``, ``k``, ``v``
-    ``[B, Hkv, Sk, D]``; causal is bottom-right aligned.  Runs
+    ``[B, Hkv, Sk, D]``; causal is bottom-right aligned; ``window_left`` as
+    in ``attn_varlen`` (negative: none).  Runs
     ``attn_varlen`` on token-major copies.  Returns fp16 ``[B, Hq, Sq, D]``."""
     _require(q.dim() == 4 and k.dim() == 4 and v.shape == k.shape, "attn_fwd: q [B, Hq, Sq, D], k / v [B, Hkv, Sk, D]")
     b, hq, sq, d = q.shape
@@ -569,7 +573,8 @@ def attn_fwd(q, k, v, *, causal, scale):
     vt = v.transpose(1, 2).reshape(b * sk, v.shape[1], d)
     cu_q = torch.arange(0, (b + 1) * sq, sq, dtype=torch.int32, device=q.device)
     cu_k = torch.arange(0, (b + 1) * sk, sk, dtype=torch.int32, device=q.device)
-    out = attn_varlen(qt, kt, vt, cu_q, cu_k, sq, sk, causal=causal, scale=scale)
+    out = attn_varlen(qt, kt, vt, cu_q, cu_k, sq, sk, causal=causal, scale=scale,
+                      window_left=None if window_left is None or window_left < 0 else window_left)
     return out.reshape(b, sq, hq, d).transpose(1, 2)
 
 

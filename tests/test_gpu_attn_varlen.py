@@ -85,3 +85,30 @@ def test_attn_varlen_writes_only_own_tokens():
     ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.1, True)
     assert np.all(o[:3] == 0) and np.all(ref[:3] == 0)  # queries 0..2 of sequence 0 see no key
     _close(o, ref, "nq > nk")
+
+
+@pytest.mark.parametrize("d,qlens,klens,w", [
+    (128, [300, 33, 7], [300, 33, 7], 64),      # band inside long sequences, shorter ones
+    (128, [100, 40], [400, 40], 0),             # only the diagonal key; a chunk after a prefix
+    (64, [257], [257], 31),                     # band edge off a 32-key tile
+    (256, [90, 130], [200, 130], 100),          # head_dim 256
+])
+def test_attn_varlen_window_left(d, qlens, klens, w):
+    q, k, v, cu_q, cu_k = _case(750 + d + w, 8, 2, d, qlens, klens)
+    scale = 1.0 / np.sqrt(d)
+    out = ops.attn_varlen(_t(q), _t(k), _t(v), _t(cu_q), _t(cu_k), max(qlens), max(klens), causal=True, scale=scale,
+                          window_left=w)
+    torch.cuda.synchronize()
+    ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, scale, True, window_left=w)
+    _close(out.float().cpu().numpy(), ref, f"window_left {w}")
+
+
+def test_attn_varlen_wide_window_equals_plain_causal():
+    q, k, v, cu_q, cu_k = _case(761, 8, 2, 128, [200, 50], [200, 90])
+    args = (_t(q), _t(k), _t(v), _t(cu_q), _t(cu_k), 200, 200)
+    a = ops.attn_varlen(*args, causal=True, scale=0.1, window_left=1000)
+    b = ops.attn_varlen(*args, causal=True, scale=0.1)
+    torch.cuda.synchronize()
+    ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.1, True)
+    _close(a.float().cpu().numpy(), ref, "wide window")
+    _close(b.float().cpu().numpy(), ref, "plain")

@@ -510,3 +510,27 @@ def test_dense_varlen_attention_matches_torch_sdpa(causal):
         mask = torch.ones(nq, nk, dtype=torch.bool).tril(diagonal=nk - nq) if causal else None
         ref = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask, scale=0.3)
         assert np.allclose(got[cu_q[b]:cu_q[b + 1]], ref.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_dense_varlen_attention_window_left_matches_torch_sdpa():
+    """window_left: query i (bottom-right aligned) sees keys i - W .. i, as a
+    torch band mask built with tril / triu."""
+    rng = np.random.default_rng(22)
+    hq, hkv, d, w = 4, 2, 16, 5
+    qlens, klens = [12, 3], [12, 20]
+    cu_q, cu_k = np.cumsum([0] + qlens), np.cumsum([0] + klens)
+    q = rng.standard_normal((cu_q[-1], hq, d))
+    k = rng.standard_normal((cu_k[-1], hkv, d))
+    v = rng.standard_normal((cu_k[-1], hkv, d))
+    got = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True, window_left=w)
+    for b in range(2):
+        nq, nk = qlens[b], klens[b]
+        qb = torch.from_numpy(q[cu_q[b]:cu_q[b + 1]]).permute(1, 0, 2)
+        kb = torch.from_numpy(k[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        vb = torch.from_numpy(v[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        ones = torch.ones(nq, nk, dtype=torch.bool)
+        mask = ones.tril(diagonal=nk - nq) & ones.triu(diagonal=nk - nq - w)
+        ref = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask, scale=0.25)
+        assert np.allclose(got[cu_q[b]:cu_q[b + 1]], ref.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
+    full = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True)
+    assert np.array_equal(O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True, window_left=100), full)
