@@ -85,7 +85,10 @@ def _fp16_outliers(gen, shape, ch, device):
     return x.half()
 
 
-def build(device):
+def build(device, layers: int = NUM_LAYERS, keep_prefix: bool = False):
+    """The decode-step workload of `layers` layers (distinct storage each):
+    the prefix of every row appended, and per layer the new tokens' K/V and
+    q.  `keep_prefix`: also return the appended prefix K/V (fp16, per layer)."""
     import torch
 
     from superl8_serve_amd import ops
@@ -97,7 +100,7 @@ def build(device):
                                 for b in range(BATCH)]).astype(np.int32)
     new_slots = np.array([bt_np[b, prefix[b] // BS] * BS + prefix[b] % BS for b in range(BATCH)], dtype=np.int32)
 
-    shape = (NUM_LAYERS, POOL_BLOCKS, HKV, BS, D)
+    shape = (layers, POOL_BLOCKS, HKV, BS, D)
     kc = torch.zeros(shape, dtype=torch.int8, device=device)
     vc = torch.zeros(shape, dtype=torch.int8, device=device)
     ks = torch.ones(shape[:4], dtype=torch.float32, device=device)
@@ -105,24 +108,27 @@ def build(device):
     gen = torch.Generator(device=device)
     gen.manual_seed(SEED)
     pre_sm = torch.from_numpy(pre_slots).to(device)
-    chans = []
-    for layer in range(NUM_LAYERS):
+    chans, kept = [], []
+    for layer in range(layers):
         ch = torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(device)
         chans.append(ch)
         kp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch, device)
         vp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch, device)
         ops.quantize_kv_write_paged(kp, vp, kc[layer], ks[layer], vc[layer], vs[layer], pre_sm)
+        if keep_prefix:
+            kept.append((kp, vp))
         del kp, vp
-    k_new = [_fp16_outliers(gen, (BATCH, HKV, D), chans[l], device) for l in range(NUM_LAYERS)]
-    v_new = [_fp16_outliers(gen, (BATCH, HKV, D), chans[l], device) for l in range(NUM_LAYERS)]
+    k_new = [_fp16_outliers(gen, (BATCH, HKV, D), chans[l], device) for l in range(layers)]
+    v_new = [_fp16_outliers(gen, (BATCH, HKV, D), chans[l], device) for l in range(layers)]
     # q as the attention seam passes it: a [B,1,Hq,D] -> [B,Hq,1,D] transpose view
-    q = [_fp16_outliers(gen, (BATCH, 1, HQ, D), chans[l], device).transpose(1, 2) for l in range(NUM_LAYERS)]
+    q = [_fp16_outliers(gen, (BATCH, 1, HQ, D), chans[l], device).transpose(1, 2) for l in range(layers)]
     torch.cuda.synchronize()
     return {
         "lens": lens, "kc": kc, "vc": vc, "ks": ks, "vs": vs,
         "bt": torch.from_numpy(bt_np).to(device), "bt_np": bt_np,
         "cl": torch.from_numpy(lens.astype(np.int32)).to(device),
-        "new_sm": torch.from_numpy(new_slots).to(device), "k_new": k_new, "v_new": v_new, "q": q,
+        "new_sm": torch.from_numpy(new_slots).to(device), "new_slots": new_slots, "pre_slots": pre_slots,
+        "k_new": k_new, "v_new": v_new, "q": q, "prefix": kept,
     }
 
 
@@ -253,7 +259,7 @@ def calibrate_copy(mib: int) -> None:
 VERIFY_LAYERS = 4  # distinct per-layer storage, rotated so no layer is served from the Infinity Cache
 
 
-def verify_workload(kind: str, device, k8v3: bool = False):
+def verify_workload(kind: str, device, k8v3: bool = False, layers: int = VERIFY_LAYERS, keep_prefix: bool = False):
     """Chunked prefill: 16 sequences sharing a 4096-token prefix (the prefix
     blocks appear in every block table) each append a 512-token chunk and
     attend bottom-right causally.  Tree verify: 32 sequences with 8192-token
@@ -301,7 +307,7 @@ def verify_workload(kind: str, device, k8v3: bool = False):
                     nxt += 1
             tree[i, : nq[i]] = [m - (1 << 64) if m >= 1 << 63 else m for m in masks]
     width = bt.shape[1]
-    shape = (VERIFY_LAYERS, n_blocks, HKV, BS, D)
+    shape = (layers, n_blocks, HKV, BS, D)
     kc = torch.zeros(shape, dtype=torch.int8, device=device)
     ks = torch.ones(shape[:4], dtype=torch.float32, device=device)
     cb = torch.from_numpy(gaussian_codebook()).to(device)
@@ -324,17 +330,22 @@ def verify_workload(kind: str, device, k8v3: bool = False):
     pre_slots = np.concatenate([bt[i, np.arange(prefix_len) // BS] * BS + np.arange(prefix_len) % BS for i in rows])
     new_slots = np.concatenate([bt[i, (prefix_len + np.arange(nq[i])) // BS] * BS + (prefix_len + np.arange(nq[i])) % BS
                                 for i in range(b_)]).astype(np.int32)
-    ch = [torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(device) for _ in range(VERIFY_LAYERS)]
+    ch = [torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(device) for _ in range(layers)]
     sm = torch.from_numpy(pre_slots.astype(np.int32)).to(device)
-    for layer in range(VERIFY_LAYERS):
+    kept = []
+    for layer in range(layers):
         kp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
         vp = _fp16_outliers(gen, (pre_slots.size, HKV, D), ch[layer], device)
         append(kp, vp, layer, sm)
+        if keep_prefix:
+            kept.append((kp, vp))
     t_new = int(new_slots.size)
-    k_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
-    v_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(VERIFY_LAYERS)]
-    q = [_fp16_outliers(gen, (b_, nq_max, HQ, D), ch[l], device).transpose(1, 2) for l in range(VERIFY_LAYERS)]
-    w = {"kc": kc, "vc": vc, "ks": ks, "vs": vs, "bt": torch.from_numpy(bt).to(device),
+    k_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(layers)]
+    v_new = [_fp16_outliers(gen, (t_new, HKV, D), ch[l], device) for l in range(layers)]
+    q = [_fp16_outliers(gen, (b_, nq_max, HQ, D), ch[l], device).transpose(1, 2) for l in range(layers)]
+    w = {"kc": kc, "vc": vc, "ks": ks, "vs": vs, "bt": torch.from_numpy(bt).to(device), "bt_np": bt,
+         "prefix_np": prefix, "nq_np": nq, "tree_np": tree, "pre_slots": pre_slots.astype(np.int32),
+         "new_slots": new_slots, "prefix_kv": kept,
          "prefix": torch.from_numpy(prefix.astype(np.int32)).to(device),
          "ql": torch.from_numpy(nq.astype(np.int32)).to(device),
          "tree": None if tree is None else torch.from_numpy(tree).to(device),
@@ -418,17 +429,17 @@ K8V3_BATCH = 32
 K8V3_BYTES_PER_TOKEN_HEAD = D + 4 + D * 3 // 8 + 4 * (D // 128)  # 184 B
 
 
-def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
-    """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
-    36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
-    needed, distinct storage per layer; one launch per layer
-    (attn_paged_decode_append_k8v3) unless `fused` is False."""
+def k8v3_workload(dev, layers: int = NUM_LAYERS, keep_rows=()):
+    """The K8V3 decode-step workload (batch 32, contexts U{8192..32768},
+    seed 2) over `layers` layers of distinct storage: every row's prefix
+    appended, and per layer the new tokens' K/V and q.  `keep_rows`: rows whose
+    layer-0 prefix K/V (fp16) are returned too, as (row, first position, k, v)
+    chunks."""
     import torch
 
     from superl8_serve_amd import ops
     from superl8_serve_amd.codebook import gaussian_codebook
 
-    dev = "cuda"
     rng = np.random.default_rng(2)
     lens = rng.integers(8192, 32769, size=K8V3_BATCH)
     need = (lens + BS - 1) // BS
@@ -441,7 +452,7 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
         bt[b, : need[b]] = perm[pos: pos + need[b]]
         pos += need[b]
     prefix = lens - 1
-    shape = (NUM_LAYERS, n_blocks, HKV, BS, D)
+    shape = (layers, n_blocks, HKV, BS, D)
     kc = torch.zeros(shape, dtype=torch.int8, device=dev)
     ks = torch.ones(shape[:4], dtype=torch.float32, device=dev)
     vp = torch.zeros(shape[:4] + (D * 3 // 32,), dtype=torch.int32, device=dev)
@@ -450,7 +461,8 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
     gen = torch.Generator(device=dev)
     gen.manual_seed(2)
     chunk = 65536
-    for layer in range(NUM_LAYERS):
+    kept = []
+    for layer in range(layers):
         ch = torch.from_numpy(rng.choice(D, OUTLIER_CH, replace=False)).to(dev)
         for b in range(K8V3_BATCH):
             for c0 in range(0, int(prefix[b]), chunk):
@@ -460,14 +472,34 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
                 kp = _fp16_outliers(gen, (n, HKV, D), ch, dev)
                 vq = _fp16_outliers(gen, (n, HKV, D), ch, dev)
                 ops.quantize_kv_write_paged_k8v3(kp, vq, kc[layer], ks[layer], vp[layer], vn[layer], cb, sm)
-    new_sm = torch.from_numpy(np.array([bt[b, prefix[b] // BS] * BS + prefix[b] % BS for b in range(K8V3_BATCH)],
-                                       np.int32)).to(dev)
-    k_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(NUM_LAYERS)]
-    v_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(NUM_LAYERS)]
-    q = [torch.randn((K8V3_BATCH, 1, HQ, D), generator=gen, device=dev).half().transpose(1, 2) for _ in range(NUM_LAYERS)]
-    btd = torch.from_numpy(bt).to(dev)
-    cl = torch.from_numpy(lens.astype(np.int32)).to(dev)
-    max_ctx = width * BS
+                if layer == 0 and b in keep_rows:
+                    kept.append((b, c0, kp, vq))
+    new_slots = np.array([bt[b, prefix[b] // BS] * BS + prefix[b] % BS for b in range(K8V3_BATCH)], np.int32)
+    k_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(layers)]
+    v_new = [torch.randn((K8V3_BATCH, HKV, D), generator=gen, device=dev).half() for _ in range(layers)]
+    q = [torch.randn((K8V3_BATCH, 1, HQ, D), generator=gen, device=dev).half().transpose(1, 2) for _ in range(layers)]
+    torch.cuda.synchronize()
+    return {"lens": lens, "need": need, "bt_np": bt, "n_blocks": n_blocks, "kc": kc, "ks": ks, "vp": vp, "vn": vn,
+            "cb": cb, "new_slots": new_slots, "new_sm": torch.from_numpy(new_slots).to(dev), "k_new": k_new,
+            "v_new": v_new, "q": q, "bt": torch.from_numpy(bt).to(dev),
+            "cl": torch.from_numpy(lens.astype(np.int32)).to(dev), "max_ctx": int(need.max()) * BS,
+            "prefix_kv": kept}
+
+
+def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
+    """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
+    36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
+    needed, distinct storage per layer; one launch per layer
+    (attn_paged_decode_append_k8v3) unless `fused` is False."""
+    import torch
+
+    from superl8_serve_amd import ops
+
+    w = k8v3_workload("cuda")
+    lens, need, n_blocks = w["lens"], w["need"], w["n_blocks"]
+    kc, ks, vp, vn, cb = w["kc"], w["ks"], w["vp"], w["vn"], w["cb"]
+    new_sm, k_new, v_new, q, btd, cl, max_ctx = (w[k] for k in ("new_sm", "k_new", "v_new", "q", "bt", "cl",
+                                                                 "max_ctx"))
     scale = 1.0 / math.sqrt(D)
 
     def step():

@@ -269,6 +269,11 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * j < s + nk - nq - window_left (a sliding-window layer), -1 for none.
  * out [tokens_q, num_q_heads, head_dim] with strides
  * o_stride_t, o_stride_h; only the sequences' own query tokens are written.
+ * The causal diagonal comes from each sequence's own counts.  max_seqlen_q
+ * sizes the grid and must be >= every sequence's query count (queries past it
+ * are not computed); max_seqlen_k is informational.  cu_seqlens must be
+ * non-decreasing and within the q / k / v token counts: K, V and out are
+ * addressed from them without further bounds.
  * head_dim 64, 128 or 256; at most 16 q heads per KV head.
  */
 int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,

@@ -1151,7 +1151,16 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   a.slot_classes = resident;
   a.slot_skew = kSlotSkewPermille;
   if (const char* env = getenv("S8KV_DECODE_SLOT_SKEW")) a.slot_skew = atoi(env);
-  if (const char* env = getenv("S8KV_DECODE_GHOST")) a.ghost = (atoi(env) < 0 ? 0 : atoi(env) + 31) / 32 * 32;
+  if (const char* env = getenv("S8KV_DECODE_GHOST")) {
+    const int g = atoi(env);
+    a.ghost = (g < 0 ? 0 : (g > (1 << 16) ? (1 << 16) : g) + 31) / 32 * 32;
+  }
+  // stream positions are int32: every row's padded length plus its ghost
+  // tokens, summed over the batch, must stay below 2^31
+  if ((int64_t)a.batch * ((int64_t)a.max_context_len + 31 + a.ghost) >= (int64_t(1) << 31)) {
+    set_error("s8kv_decode: batch * (max_context_len + %d) too large", a.ghost + 31);
+    return S8KV_ERR_UNSUPPORTED;
+  }
   a.slots = a.batch + a.wg_per_head;
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
   hipEvent_t* ev = timing_slot(stream);

@@ -125,14 +125,18 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 
   // dense: sequence b's queries are tokens cu_q[b] .., its keys cu_k[b] ..;
   // causal is bottom-right aligned (query s sees keys j <= s + nk - nq, which
-  // may be none), else every key is visible
+  // may be none), else every key is visible.  The diagonal comes from the
+  // sequence's own counts; max_queries (max_seqlen_q) only sizes the grid, so
+  // queries past it are not computed (the entry point requires it to bound
+  // every sequence), and max_seqlen_k is not used to clamp the keys.
   int nq, prefix, nk = 0, q0 = 0, k0 = 0;
   if constexpr (DENSE) {
     q0 = a.cu_q[b];
     k0 = a.cu_k[b];
-    nq = max(0, min(a.cu_q[b + 1] - q0, a.max_queries));
-    nk = max(0, min(a.cu_k[b + 1] - k0, a.max_context_len));
-    prefix = a.causal ? nk - nq : nk;
+    const int nq_seq = max(0, a.cu_q[b + 1] - q0);
+    nk = max(0, a.cu_k[b + 1] - k0);
+    nq = min(nq_seq, a.max_queries);
+    prefix = a.causal ? nk - nq_seq : nk;
   } else {
     nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
     prefix = max(0, a.prefix_lens[b]);
@@ -383,18 +387,21 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         if constexpr (C::NB == 2) vsc1[s] = *reinterpret_cast<const float4_t*>(sb + 2 * kTile + 16 * s + 4 * g);
       }
       float pr[2][4];
+      bool vm[2][4];  // MASKED: key visible to this lane's row
       float mt = kNegInf;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float x = sc[s][i] * ksc[s][i];
+          vm[s][i] = true;
           if constexpr (MASKED) {
             const int kk = base + 16 * s + 4 * g + i;
             const int di = kk - prefix;  // draft index when >= 0
             bool vis = kk < kv_end && row_live && (!WIN || kk >= (DENSE ? prefix + pos - a.window : lo_key));
             if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask >> di) & 1ull)) : di <= pos);
             x = vis ? x : kNegInf;
+            vm[s][i] = vis;
           }
           pr[s][i] = x;
           mt = fmaxf(mt, x);
@@ -418,12 +425,16 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           const float x = pr[s][i];
           const float e = __builtin_amdgcn_exp2f(x - m_run);
           l_run += e;
-          const float w = materialize(e * vsc[s][i]);  // one value for hi and lo
+          // masked keys: e = 0, but their scale (past the visible keys, or
+          // below a window) may be any value, inf and NaN included
+          float w = materialize(e * vsc[s][i]);  // one value for hi and lo
+          if constexpr (MASKED) w = vm[s][i] ? w : 0.0f;
           const _Float16 wh = (_Float16)w;
           pbh[4 * s + i] = wh;
           pbl[4 * s + i] = (_Float16)(w - (float)wh);
           if constexpr (C::NB == 2) {
-            const float w1 = materialize(e * vsc1[s][i]);
+            float w1 = materialize(e * vsc1[s][i]);
+            if constexpr (MASKED) w1 = vm[s][i] ? w1 : 0.0f;
             const _Float16 wh1 = (_Float16)w1;
             pbh1[4 * s + i] = wh1;
             pbl1[4 * s + i] = (_Float16)(w1 - (float)wh1);
