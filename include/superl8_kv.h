@@ -133,6 +133,32 @@ int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_k
                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free form of s8kv_decode_append_int8.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels, cache bytes and output as s8kv_decode_append_int8,
+ * with no workspace argument: the workspace is a static device array of
+ * S8KV_NOALLOC_SCRATCH_BYTES bytes in the library, one copy per GPU, held
+ * until the process ends; its device address is looked up once per device on
+ * the first call with that device current (the stream and the tensors must be
+ * on the current device).  A geometry whose workspace
+ * (s8kv_decode_workspace_size) exceeds it is rejected with
+ * S8KV_ERR_WORKSPACE.  The scratch needs no clearing (each launch tags its
+ * counters, and a row's last arrival zeroes its word), but every call on one
+ * GPU shares it: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialized by the caller.  Calls no allocating routine.
+ */
+#define S8KV_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int s8kv_decode_append_int8_noalloc(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                    int64_t k_new_stride_b, int64_t k_new_stride_h, const void* v_new,
+                                    int64_t v_new_stride_b, int64_t v_new_stride_h, int8_t* k_cache, float* k_scale,
+                                    int8_t* v_cache, float* v_scale, int64_t num_blocks, int block_size,
+                                    const int32_t* block_table, int64_t block_table_stride,
+                                    const int32_t* context_lens, int max_context_len, float scale, void* out,
+                                    void* stream);
+
+/*
  * s8kv_decode_append_int8 for the K8V3 layout: the new token is written as
  * s8kv_append_k8v3 writes it (int8 K, 3-bit Lloyd-Max V words and per-128
  * block norms) at position context_lens[b] - 1, then the row attends as

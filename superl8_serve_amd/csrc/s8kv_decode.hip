@@ -54,6 +54,7 @@
 #include <chrono>
 
 #include <array>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -139,6 +140,7 @@ struct DecodeArgs {
   // sliding window (decode_kernel<D, K8V3, false, true>): row b attends only
   // its last `window` tokens (window >= 1)
   int window;
+  int untimed;  // host only: never stamp this launch with timing events
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -1163,7 +1165,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   }
   a.slots = a.batch + a.wg_per_head;
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
-  hipEvent_t* ev = timing_slot(stream);
+  hipEvent_t* ev = a.untimed ? nullptr : timing_slot(stream);
   if (ev) {  // events stamped with the kernel's own start and end times
     hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
   } else {
@@ -1272,6 +1274,42 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
 
 }  // namespace s8kv
 
+// Scratch of the allocation-free entry point (s8kv_decode_append_int8_noalloc):
+// the decode workspace (split-row partials and arrival counters) in a
+// file-scope device array.  Each GPU the library runs on holds its own copy
+// until the process ends.
+constexpr int64_t kScratchBytes = S8KV_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace s8kv {
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of the current device's copy of `scratch`, looked up once per
+// device with that device current.  In host code the array's name is only a
+// stand-in for the symbol: kernels and copies must be given this address.
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  S8KV_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kScratchDevices, S8KV_ERR_LAUNCH,
+               "decode_append_int8_noalloc: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    S8KV_REQUIRE(e == hipSuccess && p != nullptr, S8KV_ERR_LAUNCH,
+                 "decode_append_int8_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return S8KV_OK;
+}
+
+}  // namespace s8kv
+
 using namespace s8kv;
 
 extern "C" int s8kv_timing_begin(void) {
@@ -1351,6 +1389,46 @@ extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads
   a.vn_stride_h = v_new_stride_h;
   return decode_common(a, false, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_append_int8_noalloc(const void* q, int batch, int num_q_heads, int num_kv_heads,
+                                               int head_dim, int64_t q_stride_b, int64_t q_stride_h,
+                                               const void* k_new, int64_t k_new_stride_b, int64_t k_new_stride_h,
+                                               const void* v_new, int64_t v_new_stride_b, int64_t v_new_stride_h,
+                                               int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                                               int64_t num_blocks, int block_size, const int32_t* block_table,
+                                               int64_t block_table_stride, const int32_t* context_lens,
+                                               int max_context_len, float scale, void* out, void* stream) {
+  if (batch > 0 && num_kv_heads > 0 && num_q_heads > 0 && head_dim > 0) {
+    const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+    S8KV_REQUIRE(need <= kScratchBytes, S8KV_ERR_WORKSPACE,
+                 "decode_append_int8_noalloc: this geometry (batch %d, %d q heads, %d kv heads, head_dim %d) needs "
+                 "%lld bytes of scratch, more than the %lld-byte static scratch; use s8kv_decode_append_int8",
+                 batch, num_q_heads, num_kv_heads, head_dim, (long long)need, (long long)kScratchBytes);
+  }
+  void* ws = nullptr;
+  if (batch > 0) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc != S8KV_OK) return rc;
+  }
+  DecodeArgs a{};
+  a.q = (const _Float16*)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.out = (_Float16*)out;
+  a.k_new = (const _Float16*)k_new;
+  a.v_new = (const _Float16*)v_new;
+  a.kn_stride_b = k_new_stride_b;
+  a.kn_stride_h = k_new_stride_h;
+  a.vn_stride_b = v_new_stride_b;
+  a.vn_stride_h = v_new_stride_h;
+  a.untimed = 1;
+  return decode_common(a, false, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, scale, ws, kScratchBytes, stream);
 }
 
 extern "C" int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
