@@ -310,6 +310,52 @@ int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v, const int3
                          void* stream);
 
 /*
+ * Row codecs behind the helpers the reference's cache code calls on the
+ * `superl8` module.  Rows are head_dim contiguous elements at a uniform row
+ * stride (in elements); outputs are contiguous [num_rows][...].  Each gives
+ * the bytes the append kernels write for the same row.
+ *
+ * s8kv_rotate_rows: out = rotate_last(x), the Hadamard rotation
+ * superl8.quant.rotation.rotate_last called at kv_cache.py:594-597 (K side of
+ * the k8v3 write), kv_cache.py:1272 and 1297 (read_dense un-rotating K):
+ * fp32 Walsh-Hadamard transform, one fp32 multiply by fp32(1/sqrt(head_dim)),
+ * one rounding to the element type.  dtype: 0 fp16, 1 bf16, 2 fp32 (in and
+ * out).  head_dim 32, 64, 128 or 256.
+ */
+int s8kv_rotate_rows(const void* x, int64_t num_rows, int head_dim, int64_t x_row_stride, int dtype, void* out,
+                     int64_t out_row_stride, void* stream);
+
+/*
+ * Per-row symmetric RTN int8 of fp16 rows: superl8.quantize_i8_rowwise called
+ * at kv_cache.py:601 on rotate_last(K) (rotate = 0), and the same after the
+ * rotation in one pass (rotate = 1, the K side of s8kv_append_int8 and of
+ * superl8.quantize_kv_cache, kv_cache.py:1231).  q int8 [num_rows][head_dim],
+ * scale fp32 [num_rows] (absmax / 127; 0 for an all-zero row).
+ */
+int s8kv_quantize_rows_int8(const void* x, int64_t num_rows, int head_dim, int64_t x_row_stride, int rotate,
+                            int8_t* q, float* scale, void* stream);
+
+/*
+ * 3-bit Lloyd-Max V codec of fp16 rows: superl8.quant.lloydmax.quantize_lloydmax
+ * (bits 3, block_size 128, last dim) called at kv_cache.py:613-620.  codes uint8
+ * [num_rows][head_dim] (0..7), norms fp32 [num_rows][head_dim/128];
+ * codebook fp32 [8].  head_dim 128 or 256.
+ */
+int s8kv_quantize_rows_lloydmax3(const void* v, int64_t num_rows, int head_dim, int64_t v_row_stride,
+                                 const float* codebook, uint8_t* codes, float* norms, void* stream);
+
+/*
+ * Bit-plane packing of 3-bit codes and its inverse:
+ * superl8.quant.lloydmax.pack_indices_lowbit(codes, 3) at kv_cache.py:623 and
+ * unpack_indices_lowbit(packed, 3, head_dim) at kv_cache.py:662 and 1285.
+ * codes uint8 [num_rows][head_dim] (taken modulo 8), words int32
+ * [num_rows][head_dim*3/32]: word 3g+b holds bit b of the codes of elements
+ * 32g .. 32g+31, element 32g+i at bit i (the cache's v_packed layout).
+ */
+int s8kv_pack_codes3(const uint8_t* codes, int64_t num_rows, int head_dim, int32_t* words, void* stream);
+int s8kv_unpack_codes3(const int32_t* words, int64_t num_rows, int head_dim, uint8_t* codes, void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its kernel with HIP events stamped with the

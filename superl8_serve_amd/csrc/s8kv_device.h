@@ -327,15 +327,12 @@ __device__ __forceinline__ void lloyd3_search(float u, const float (&cb)[8], boo
 // |u - c_j| in fp32, bit-plane words (word 3g+b holds bit b of the codes of
 // elements 32g..32g+31, element 32g+i at bit i).  Lane w < 3D/32 gets word w,
 // lane nb < D/128 gets norm nb.
+// The per-128 block L2 norms of a V row in RowLayout lanes (head_dim 128 or
+// 256): every lane gets every norm.
 template <int D>
-__device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<D>::E], const float (&cb)[8], int lane,
-                                                      uint32_t& word_out, float& norm_out) {
-  constexpr int E = RowLayout<D>::E;
-  constexpr int NB = D / 128;
-  constexpr int WORDS = D / 32 * 3;
-  float norm[NB];
+__device__ __forceinline__ void lloyd3_block_norms(const float (&x)[RowLayout<D>::E], float (&norm)[D / 128]) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+  for (int nb = 0; nb < D / 128; ++nb) {
     // Block nb holds elements 128nb + {lane, lane+64}: the tree's levels
     // h = 1 .. 32 are butterflies within each half (lane l gets its group's
     // two partial sums added in either order -- the same fp32 value), h = 64
@@ -348,9 +345,15 @@ __device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<
     }
     norm[nb] = __builtin_sqrtf(s0 + s1);
   }
-  uint32_t codes[E];
+}
+
+// The lane's 3-bit codes: u = v / norm of its block (0 for a zero norm),
+// code = first index minimising |u - c_j| in fp32 (sequential scan).
+template <int D>
+__device__ __forceinline__ void lloyd3_codes(const float (&x)[RowLayout<D>::E], const float (&norm)[D / 128],
+                                             const float (&cb)[8], uint32_t (&codes)[RowLayout<D>::E]) {
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
+  for (int j = 0; j < RowLayout<D>::E; ++j) {
     const float nrm = norm[j / 2];
     const float u = nrm > 0.0f ? x[j] / nrm : 0.0f;
     float best = fabsf(u - cb[0]);
@@ -365,6 +368,18 @@ __device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<
     }
     codes[j] = c;
   }
+}
+
+template <int D>
+__device__ __forceinline__ void lloydmax3_encode_row(const float (&x)[RowLayout<D>::E], const float (&cb)[8], int lane,
+                                                      uint32_t& word_out, float& norm_out) {
+  constexpr int E = RowLayout<D>::E;
+  constexpr int NB = D / 128;
+  constexpr int WORDS = D / 32 * 3;
+  float norm[NB];
+  lloyd3_block_norms<D>(x, norm);
+  uint32_t codes[E];
+  lloyd3_codes<D>(x, norm, cb, codes);
   // Bit-plane packing: element group g (32 elements) -> words 3g+b, bit i of
   // word 3g+b = bit b of the code of element 32g+i.  Slot j of lanes 0..31
   // is group 2j, of lanes 32..63 group 2j+1.

@@ -33,6 +33,11 @@ __all__ = [
     "attn_varlen",
     "attn_fwd",
     "copy_blocks",
+    "rotate_rows",
+    "quantize_rows_int8",
+    "quantize_rows_lloydmax3",
+    "pack_codes3",
+    "unpack_codes3",
 ]
 
 
@@ -624,3 +629,108 @@ def copy_blocks(tensors: Sequence[torch.Tensor], src: Sequence[int] | torch.Tens
     rc = _lib.load().s8kv_copy_blocks(n, arr_p, arr_b, arr_s, nl, nb, src_t.data_ptr(), dst_t.data_ptr(), npairs,
                                       _stream(t0))
     _lib.check(rc, "copy_blocks")
+
+
+# ---------------------------------------------------------------------------
+# Row codecs (the helpers the reference's cache code calls on ``superl8``)
+# ---------------------------------------------------------------------------
+
+_ROT_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _rows_view(x: torch.Tensor, name: str) -> torch.Tensor:
+    """``x`` as ``[rows, D]`` with a unit stride on D (copies when the leading
+    axes cannot be flattened into one row stride)."""
+    _require(x.dim() >= 1, f"{name} must have at least one dimension")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d)
+    if x2.numel() and (x2.stride(1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < d)):
+        x2 = x2.contiguous()
+    return x2
+
+
+def rotate_rows(x: torch.Tensor) -> torch.Tensor:
+    """``rotate_last``: the normalized Hadamard rotation of the last axis
+    (fp32 transform, one multiply by fp32(1/sqrt(D)), one rounding to x's
+    dtype), the rotation the append applies to K.  fp16, bf16 or fp32; D in
+    {32, 64, 128, 256}.  Returns a new tensor of x's shape and dtype."""
+    _on_gpu("x", x)
+    _require(x.dtype in _ROT_DTYPES, f"rotate_last: dtype {x.dtype} not in fp16 / bf16 / fp32", TypeError)
+    x2 = _rows_view(x, "x")
+    d = x.shape[-1]
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    if x2.shape[0]:
+        lib = _lib.load()
+        rc = lib.s8kv_rotate_rows(x2.data_ptr(), x2.shape[0], d, x2.stride(0), _ROT_DTYPES[x.dtype], out.data_ptr(),
+                                  out.stride(0), _stream(x))
+        _lib.check(rc, "rotate_last")
+    return out.reshape(x.shape)
+
+
+def quantize_rows_int8(x: torch.Tensor, rotate: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row symmetric RTN int8 of fp16 rows (``quantize_i8_rowwise``):
+    int8 codes of x's shape and fp32 scales ``x.shape[:-1]``; ``rotate``
+    applies ``rotate_last`` first, in the same pass (the append's K bytes)."""
+    _on_gpu("x", x, torch.float16)
+    x2 = _rows_view(x, "x")
+    d = x.shape[-1]
+    q = torch.empty(x2.shape, dtype=torch.int8, device=x.device)
+    sc = torch.empty(x2.shape[0], dtype=torch.float32, device=x.device)
+    if x2.shape[0]:
+        lib = _lib.load()
+        rc = lib.s8kv_quantize_rows_int8(x2.data_ptr(), x2.shape[0], d, x2.stride(0), 1 if rotate else 0,
+                                         q.data_ptr(), sc.data_ptr(), _stream(x))
+        _lib.check(rc, "quantize_i8_rowwise")
+    return q.reshape(x.shape), sc.reshape(x.shape[:-1])
+
+
+def quantize_rows_lloydmax3(v: torch.Tensor, codebook: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """3-bit Lloyd-Max codes (uint8, v's shape) and per-128 block norms (fp32,
+    ``v.shape[:-1] + (D/128,)``) of fp16 rows -- the append's K8V3 V path."""
+    _on_gpu("v", v, torch.float16)
+    dev = v.device
+    _on_gpu("codebook", codebook, torch.float32, dev)
+    _require(codebook.numel() == 8, "codebook must hold 8 entries")
+    cb = codebook.reshape(8).contiguous()
+    v2 = _rows_view(v, "v")
+    d = v.shape[-1]
+    codes = torch.empty(v2.shape, dtype=torch.uint8, device=dev)
+    norms = torch.empty((v2.shape[0], max(1, d // 128)), dtype=torch.float32, device=dev)
+    if v2.shape[0]:
+        lib = _lib.load()
+        rc = lib.s8kv_quantize_rows_lloydmax3(v2.data_ptr(), v2.shape[0], d, v2.stride(0), cb.data_ptr(),
+                                              codes.data_ptr(), norms.data_ptr(), _stream(v))
+        _lib.check(rc, "quantize_lloydmax")
+    return codes.reshape(v.shape), norms.reshape(*v.shape[:-1], -1)
+
+
+def pack_codes3(codes: torch.Tensor) -> torch.Tensor:
+    """Bit-plane words (int32, ``[..., 3D/32]``) of uint8 3-bit codes
+    ``[..., D]``: word 3g+b holds bit b of codes 32g..32g+31 (the cache's
+    ``v_packed`` layout)."""
+    _on_gpu("codes", codes, torch.uint8)
+    c2 = codes.reshape(-1, codes.shape[-1]).contiguous()
+    d = codes.shape[-1]
+    _require(d % 32 == 0, f"pack_indices_lowbit: last dimension {d} is not a multiple of 32")
+    words = torch.empty((c2.shape[0], d * 3 // 32), dtype=torch.int32, device=codes.device)
+    if c2.numel():
+        lib = _lib.load()
+        _lib.check(lib.s8kv_pack_codes3(c2.data_ptr(), c2.shape[0], d, words.data_ptr(), _stream(codes)),
+                   "pack_indices_lowbit")
+    return words.reshape(*codes.shape[:-1], d * 3 // 32)
+
+
+def unpack_codes3(words: torch.Tensor, d: int) -> torch.Tensor:
+    """Inverse of ``pack_codes3``: int32 words ``[..., 3d/32]`` -> uint8 codes
+    ``[..., d]``."""
+    _on_gpu("words", words, torch.int32)
+    d = int(d)
+    _require(d > 0 and d % 32 == 0 and words.shape[-1] == d * 3 // 32,
+             f"unpack_indices_lowbit: {words.shape[-1]} words per row do not hold {d} 3-bit codes")
+    w2 = words.reshape(-1, words.shape[-1]).contiguous()
+    codes = torch.empty((w2.shape[0], d), dtype=torch.uint8, device=words.device)
+    if w2.numel():
+        lib = _lib.load()
+        _lib.check(lib.s8kv_unpack_codes3(w2.data_ptr(), w2.shape[0], d, codes.data_ptr(), _stream(words)),
+                   "unpack_indices_lowbit")
+    return codes.reshape(*words.shape[:-1], d)

@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import ops
@@ -52,6 +53,36 @@ def block_bytes(num_kv_heads: int, block_size: int, head_dim: int, v_quant: str 
     if v_quant == "lloydmax3":
         return k_side + tokens * (head_dim * 3 // 32 * 4 + head_dim // lloyd_block * 4)
     return k_side + tokens * (head_dim + 4)
+
+
+class _Staging:
+    """Pinned host mirrors of device buffers that captured graphs read.  A
+    refresh writes the host mirror and issues one non-blocking copy; an event
+    recorded after the copy is waited on before the mirror is written again,
+    so a pending copy never reads a half-written mirror."""
+
+    def __init__(self, pin: bool):
+        self._pin = pin
+        self._host: dict[str, torch.Tensor] = {}
+        self._done: dict[str, torch.cuda.Event] = {}
+
+    def put(self, dst: torch.Tensor, values: np.ndarray, name: str) -> None:
+        n = values.size
+        buf = self._host.get(name)
+        if buf is None or buf.numel() < n or buf.dtype != dst.dtype:
+            buf = torch.empty(max(n, 1), dtype=dst.dtype, pin_memory=self._pin)
+            self._host[name] = buf
+            self._done.pop(name, None)
+        ev = self._done.get(name)
+        if ev is not None:
+            ev.synchronize()
+        host = buf[:n].view(values.shape)
+        host.numpy()[...] = values
+        dst.copy_(host, non_blocking=self._pin)
+        if self._pin and dst.is_cuda:
+            ev = torch.cuda.Event()
+            ev.record()
+            self._done[name] = ev
 
 
 class _Entry:
@@ -114,17 +145,21 @@ class PagedKVCache:
         self._lru_clock = 0
         self._max_prefix_entries = max_prefix_entries
         self._prefix_entry_count = 0
-        if max_prefix_blocks is not None:
-            self._max_prefix_blocks: int | None = max_prefix_blocks
-        elif max_prefix_block_fraction is not None:
-            self._max_prefix_blocks = max(1, int(self.num_blocks * max_prefix_block_fraction))
-        else:
-            self._max_prefix_blocks = None
+        # distinct blocks the prefix cache may pin: explicit, else a fraction of
+        # the pool (at least one), else unbounded
+        budget = max_prefix_blocks
+        if budget is None and max_prefix_block_fraction is not None:
+            budget = max(1, int(self.num_blocks * max_prefix_block_fraction))
+        self._max_prefix_blocks: int | None = budget
         self._prefix_block_refs: dict[int, int] = {}
-        # pinned host staging for graph-replayed decode
+        # graph inputs: pinned host mirrors of the device buffers a captured
+        # graph reads (decode slot mapping / block table, prefill statics)
         self._pin = device != "cpu" and torch.cuda.is_available()
-        self._slot_map_host: torch.Tensor | None = None
-        self._block_table_host: torch.Tensor | None = None
+        self._staging = _Staging(self._pin)
+        self._prefill_mapping_static: torch.Tensor | None = None
+        self._prefill_positions_static: torch.Tensor | None = None
+        self._prefill_blocks_static: torch.Tensor | None = None
+        self._graph_prefill_mode = False
 
     # ------------------------------------------------------------------ layout
 
@@ -290,49 +325,77 @@ class PagedKVCache:
         return [owned[p // bs] * bs + p % bs for p in range(length)]
 
     def slot_mapping_for(self, slots: list[int], positions: list[int]) -> torch.Tensor:
-        bs = self.block_size
-        flat = [self._slot_blocks[s][p // bs] * bs + p % bs for s, p in zip(slots, positions)]
-        return torch.tensor(flat, dtype=torch.int32, device=self.device)
+        """int32 device tensor of the flat slots of (slot, position) pairs
+        (kv_cache.py:900-905, 960-961)."""
+        return torch.from_numpy(self._flat_slots(slots, positions)).to(self.device)
 
     _slot_mapping = slot_mapping_for
 
     def block_table(self, slots: list[int]) -> torch.Tensor:
-        table = torch.zeros(len(slots), self.max_blocks_per_seq, dtype=torch.int32)
+        """``[B, max_blocks_per_seq]`` int32 block ids, zero padded
+        (kv_cache.py:1118-1127)."""
+        return torch.from_numpy(self._table_rows(slots, self.max_blocks_per_seq)).to(self.device)
+
+    def _flat_slots(self, slots: list[int], positions: list[int]) -> np.ndarray:
+        """int32 flat slots ``block * bs + pos % bs`` of (slot, position) pairs."""
+        bs = self.block_size
+        blk = np.fromiter((self._slot_blocks[s][p // bs] for s, p in zip(slots, positions)), np.int64,
+                          count=len(slots))
+        pos = np.asarray(positions, dtype=np.int64)
+        return (blk * bs + pos % bs).astype(np.int32)
+
+    def _table_rows(self, slots: list[int], width: int) -> np.ndarray:
+        """Zero-padded int32 ``[len(slots), width]`` block ids."""
+        table = np.zeros((len(slots), width), dtype=np.int32)
         for i, s in enumerate(slots):
             owned = self._slot_blocks[s]
-            if owned:
-                table[i, : len(owned)] = torch.tensor(owned, dtype=torch.int32)
-        return table.to(self.device)
-
-    def _ensure_decode_staging(self, batch: int) -> None:
-        if self._slot_map_host is None or self._slot_map_host.numel() < batch:
-            self._slot_map_host = torch.empty(batch, dtype=torch.int32, pin_memory=self._pin)
-        if self._block_table_host is None or self._block_table_host.shape[0] < batch:
-            self._block_table_host = torch.zeros(batch, self.max_blocks_per_seq, dtype=torch.int32,
-                                                 pin_memory=self._pin)
+            table[i, : len(owned)] = owned
+        return table
 
     def fill_slot_mapping(self, dst: torch.Tensor, slots: list[int], positions: list[int]) -> None:
-        """Refresh a graph's slot-mapping buffer in place: pinned staging plus one
-        non-blocking copy (kv_cache.py:971-980)."""
-        n = len(slots)
-        self._ensure_decode_staging(n)
-        bs = self.block_size
-        flat = [self._slot_blocks[s][p // bs] * bs + p % bs for s, p in zip(slots, positions)]
-        self._slot_map_host[:n].copy_(torch.tensor(flat, dtype=torch.int32))
-        dst.copy_(self._slot_map_host[:n], non_blocking=self._pin)
+        """Refresh a graph's slot-mapping buffer in place: the values go through
+        a pinned host mirror and one non-blocking copy (the role of
+        kv_cache.py:971-980)."""
+        self._staging.put(dst, self._flat_slots(slots, positions), "slot_mapping")
 
     def fill_block_table(self, dst: torch.Tensor, slots: list[int]) -> None:
         """Refresh a graph's block-table buffer in place; short rows are zero
-        padded (kv_cache.py:982-995)."""
-        n = len(slots)
-        self._ensure_decode_staging(n)
-        host = self._block_table_host[:n]
-        host.zero_()
-        for i, s in enumerate(slots):
-            owned = self._slot_blocks[s]
-            if owned:
-                host[i, : len(owned)] = torch.tensor(owned, dtype=torch.int32)
-        dst.copy_(host, non_blocking=self._pin)
+        padded (the role of kv_cache.py:982-995)."""
+        self._staging.put(dst, self._table_rows(slots, dst.shape[1]), "block_table")
+
+    def enable_graph_prefill(self, max_len: int) -> None:
+        """Allocate the device buffers a graph-captured ``write_prefill`` reads
+        (kv_cache.py:918-932): the flat slots of ``max_len`` positions and a
+        block-id table indexed by ``position // block_size`` (one entry per
+        pool block, so no position of a slot can index past it)."""
+        self._prefill_mapping_static = torch.zeros(max_len, dtype=torch.int32, device=self.device)
+        self._prefill_blocks_static = torch.zeros(self.num_blocks, dtype=torch.int64, device=self.device)
+        self._graph_prefill_mode = True
+
+    def bind_graph_write_prefill(self, slot: int, length: int) -> None:
+        """Point the graph-prefill buffers at `slot` (kv_cache.py:934-956): its
+        first `length` flat slots and its block ids, written in place so a
+        captured ``write_prefill`` replays against them.  No-op before
+        ``enable_graph_prefill``.
+
+        CHOICE: the mapping entries past `length` become -1, which the append
+        skips, so the padding tokens of a prompt shorter than the captured
+        bucket write nothing.  The reference rewrites only the first `length`
+        entries, leaving the previous binding's slots there (the scratch
+        slot's after capture, a previous prompt's slots after a longer one)."""
+        if self._prefill_mapping_static is None:
+            return
+        n = int(length)
+        cap = self._prefill_mapping_static.numel()
+        if n > cap:
+            raise ValueError(f"bind_graph_write_prefill: {n} positions exceed the {cap} enable_graph_prefill allocated")
+        mapping = np.full(cap, -1, dtype=np.int32)
+        mapping[:n] = self._flat_slots([slot] * n, list(range(n)))
+        self._staging.put(self._prefill_mapping_static, mapping, "prefill_mapping")
+        owned = self._slot_blocks[slot]
+        if owned:
+            self._staging.put(self._prefill_blocks_static[: len(owned)], np.asarray(owned, dtype=np.int64),
+                              "prefill_blocks")
 
     # ------------------------------------------------------------------ writes
 
@@ -356,20 +419,29 @@ class PagedKVCache:
             return
         kt = k[0].transpose(0, 1)
         vt = v[0].transpose(0, 1)
+        graph = self._graph_prefill_mode
         if positions is None:
             first = min(max(start, 0), s)
             if first == s:
                 return
-            mapping = torch.tensor(self.flat_slot_mapping(slot, s)[first:], dtype=torch.int32, device=self.device)
+            if graph and self._prefill_mapping_static is not None:  # bound by bind_graph_write_prefill
+                mapping = self._prefill_mapping_static[first:s]
+            else:
+                mapping = torch.from_numpy(self._flat_slots([slot] * (s - first), list(range(first, s)))).to(
+                    self.device)
             kt, vt = kt[first:], vt[first:]
         else:
             pos = positions.reshape(-1).to(device=self.device, dtype=torch.int64)
             if start > 0:
+                # a shared prefix: one host check that anything is left to write
                 keep = pos >= start
                 if not bool(keep.any()):
                     return
                 pos, kt, vt = pos[keep], kt[keep], vt[keep]
-            owned = torch.tensor(self._slot_blocks[slot], dtype=torch.int64, device=self.device)
+            if graph and self._prefill_blocks_static is not None:
+                owned = self._prefill_blocks_static
+            else:
+                owned = torch.from_numpy(np.asarray(self._slot_blocks[slot], dtype=np.int64)).to(self.device)
             mapping = (owned[pos // self.block_size] * self.block_size + pos % self.block_size).to(torch.int32)
         self.write_prefill_varlen(layer, mapping, kt, vt)
 
