@@ -356,6 +356,48 @@ int s8kv_pack_codes3(const uint8_t* codes, int64_t num_rows, int head_dim, int32
 int s8kv_unpack_codes3(const int32_t* words, int64_t num_rows, int head_dim, uint8_t* codes, void* stream);
 
 /*
+ * SnapKV scores for prompt-time eviction: score[t] = mean over q heads h of
+ * softmax_t(scale * q_h . K_t) over a sequence's `length` keys, the quantity
+ * KVEviction.snapkv_selection ranks (kv_cache.py:124-166; GQA: q head h reads
+ * KV head h / (num_q_heads / num_kv_heads)).  q: [num_q_heads][head_dim] rows
+ * at q_stride elements, fp16 (q_is_f32 = 0) or fp32.  scores fp32 [length].
+ * Workspace: s8kv_snapkv_workspace_size bytes (the logits and per-head
+ * softmax statistics), 4-byte aligned.
+ *
+ * _paged: K is the sequence's int8 K in the paged cache (block ids in order
+ * at block_row, >= ceil(length / block_size) of them), dequantized exactly
+ * (k_i8 * k_scale, un-rotated by rotating q) -- the reference has no paged
+ * form; it takes the caller's dense K.  _dense: K fp16 / fp32
+ * [num_kv_heads][length][head_dim] with element strides (the reference's
+ * k_full).  head_dim 32, 64, 128 or 256; at most 64 q heads per KV head.
+ */
+int64_t s8kv_snapkv_workspace_size(int num_q_heads, int length);
+int s8kv_snapkv_scores_paged(const void* q, int q_is_f32, int64_t q_stride, int num_q_heads, int num_kv_heads,
+                             int head_dim, const int8_t* k_cache, const float* k_scale, int64_t num_blocks,
+                             int block_size, const int32_t* block_row, int length, float scale, float* scores,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+int s8kv_snapkv_scores_dense(const void* q, int q_is_f32, int64_t q_stride, int num_q_heads, int num_kv_heads,
+                             int head_dim, const void* k, int k_is_f32, int64_t k_stride_h, int64_t k_stride_t,
+                             int length, float scale, float* scores, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/*
+ * Keep-list compaction: for each j < num_tokens, every (layer, tensor, KV
+ * head) row at flat slot src_slots[j] is copied to flat slot dst_slots[j],
+ * byte for byte (tensor i: rows of row_bytes[i] bytes in the cache layout
+ * [layer][block][head][offset], layer_stride_bytes[i] apart; up to 8 tensors:
+ * k_cache, k_scale, v_cache, v_scale or v_packed, v_norm).  Replaces the
+ * dequantize -> un-rotate -> requantize loop of KVEviction.compact
+ * (kv_cache.py:249-296), which is lossy; slots outside
+ * [0, num_blocks * block_size) move nothing.  Source and destination slots
+ * must be disjoint.  src_slots, dst_slots: device int32 [num_tokens].
+ */
+int s8kv_gather_slots(int num_tensors, void* const* tensor_ptrs, const int64_t* row_bytes,
+                      const int64_t* layer_stride_bytes, int num_layers, int num_kv_heads, int64_t num_blocks,
+                      int block_size, const int32_t* src_slots, const int32_t* dst_slots, int num_tokens,
+                      void* stream);
+
+/*
  * Kernel timing (diagnostics; no counterpart in the reference).  Between
  * s8kv_timing_begin() and s8kv_timing_end(), every decode call made outside
  * graph capture launches its kernel with HIP events stamped with the

@@ -541,6 +541,63 @@ def copy_blocks(tensors: list[np.ndarray], src: list[int], dst: list[int]) -> No
         t[:, list(dst)] = t[:, list(src)]
 
 
+def snapkv_scores(q, k, num_heads: int, num_kv_heads: int, scale: float | None = None) -> np.ndarray:
+    """SnapKV ranking in float64 (``KVEviction.snapkv_selection``,
+    kv_cache.py:149-163): q ``[num_heads, D]``, k ``[Hkv, S, D]``; q head h
+    reads KV head ``h // (num_heads / num_kv_heads)`` (the reference's
+    expand + reshape repeat); ``softmax_t(q_h . k_t * scale)`` averaged over
+    the heads, ``scale`` 1/sqrt(D) by default."""
+    q = np.asarray(q, dtype=np.float64).reshape(num_heads, -1)
+    k = np.asarray(k, dtype=np.float64)
+    if k.ndim == 4:
+        k = k[0]
+    g = num_heads // num_kv_heads
+    d = q.shape[1]
+    sc = 1.0 / math.sqrt(d) if scale is None else scale
+    logits = np.einsum("hd,hsd->hs", q, np.repeat(k, g, axis=0)) * sc
+    logits -= logits.max(axis=1, keepdims=True)
+    p = np.exp(logits)
+    return (p / p.sum(axis=1, keepdims=True)).mean(axis=0)
+
+
+def snapkv_scores_paged(q, layer: "LayerCache", block_row, length: int, num_heads: int) -> np.ndarray:
+    """``snapkv_scores`` over a sequence's exactly dequantized cached K
+    (``H (k_i8 * s_k)`` in float64, as ``exact_kv``; only K is read)."""
+    hkv, bs, d = layer.num_kv_heads, layer.block_size, layer.head_dim
+    rows = gather_rows(block_row, hkv, bs, length)
+    kq = layer.k_cache.reshape(-1, d)[rows].astype(np.float64)
+    ks = layer.k_scale.reshape(-1)[rows].astype(np.float64)
+    k = ((kq * ks[..., None]) @ hadamard_matrix(d)).transpose(1, 0, 2)
+    return snapkv_scores(q, k, num_heads, hkv)
+
+
+def snapkv_select(scores, budget: int) -> list[int]:
+    """Sorted positions of the ``budget`` largest scores (all of them when
+    there are at most ``budget``; kv_cache.py:145-147, 165-166).  CHOICE:
+    equal scores keep the lower position (the reference leaves ties to
+    ``torch.topk``)."""
+    s = np.asarray(scores, dtype=np.float64)
+    if s.size <= budget:
+        return list(range(s.size))
+    order = np.lexsort((np.arange(s.size), -s))
+    return sorted(int(i) for i in order[:budget])
+
+
+def gather_slots(tensors: list[np.ndarray], src: list[int], dst: list[int]) -> None:
+    """Keep-list compaction as a byte move: for every tensor ``[NL, N, Hkv,
+    bs, ...]`` the rows of flat slot ``src[j]`` go to flat slot ``dst[j]``
+    in every layer and head (the closed form of moving kept tokens without
+    re-quantizing them; the reference's KVEviction.compact re-quantizes,
+    kv_cache.py:249-296)."""
+    if set(src) & set(dst):
+        raise ValueError("source and destination slots overlap")
+    for t in tensors:
+        bs = t.shape[3]
+        sb, so = np.asarray(src) // bs, np.asarray(src) % bs
+        db, do = np.asarray(dst) // bs, np.asarray(dst) % bs
+        t[:, db, :, do] = t[:, sb, :, so]
+
+
 def block_bytes(num_kv_heads, block_size, head_dim, v_quant="int8", lloyd_block=128) -> int:
     """HBM bytes of one block per layer (kv_cache.py:98-120)."""
     n = num_kv_heads * block_size

@@ -124,6 +124,19 @@ SIGNATURES: dict[str, tuple] = {
     "s8kv_quantize_rows_lloydmax3": (_i32, [_c_void_p, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "s8kv_pack_codes3": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p]),
     "s8kv_unpack_codes3": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p]),
+    "s8kv_snapkv_workspace_size": (_i64, [_i32, _i32]),
+    "s8kv_snapkv_scores_paged": (_i32, [
+        _c_void_p, _i32, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i32, _f32,
+        _c_void_p, _c_void_p, _i64, _c_void_p,
+    ]),
+    "s8kv_snapkv_scores_dense": (_i32, [
+        _c_void_p, _i32, _i64, _i32, _i32, _i32, _c_void_p, _i32, _i64, _i64, _i32, _f32,
+        _c_void_p, _c_void_p, _i64, _c_void_p,
+    ]),
+    "s8kv_gather_slots": (_i32, [
+        _i32, ctypes.POINTER(_c_void_p), ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, _i32, _i64, _i32,
+        _c_void_p, _c_void_p, _i32, _c_void_p,
+    ]),
     "s8kv_timing_begin": (_i32, []),
     "s8kv_timing_end": (_i32, [ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "s8kv_copy_blocks": (_i32, [

@@ -12,6 +12,7 @@ CPU tensors are rejected: there is no host implementation.
 from __future__ import annotations
 
 import ctypes
+import math
 from collections.abc import Sequence
 
 import torch
@@ -38,6 +39,9 @@ __all__ = [
     "quantize_rows_lloydmax3",
     "pack_codes3",
     "unpack_codes3",
+    "snapkv_scores",
+    "snapkv_scores_paged",
+    "gather_slots",
 ]
 
 
@@ -734,3 +738,113 @@ def unpack_codes3(words: torch.Tensor, d: int) -> torch.Tensor:
         _lib.check(lib.s8kv_unpack_codes3(w2.data_ptr(), w2.shape[0], d, codes.data_ptr(), _stream(words)),
                    "unpack_indices_lowbit")
     return codes.reshape(*words.shape[:-1], d)
+
+
+# ---------------------------------------------------------------------------
+# Prompt-time eviction: SnapKV scores and the keep-list gather
+# ---------------------------------------------------------------------------
+
+
+def _q_rows(q: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+    _require(q.dtype in (torch.float16, torch.float32), f"q must be fp16 or fp32, got {q.dtype}", TypeError)
+    q2 = q.reshape(num_q_heads, -1)
+    if q2.stride(1) != 1:
+        q2 = q2.contiguous()
+    return q2
+
+
+def _snapkv_run(n: int, hq: int, dev, launch) -> torch.Tensor:
+    scores = torch.empty(n, dtype=torch.float32, device=dev)
+    if n == 0:
+        return scores
+    lib = _lib.load()
+    ws_bytes = int(lib.s8kv_snapkv_workspace_size(hq, n))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.check(launch(lib, scores, ws, ws_bytes), "snapkv_scores")
+    return scores
+
+
+def snapkv_scores(q: torch.Tensor, k: torch.Tensor, num_heads: int, num_kv_heads: int, scale: float | None = None
+                  ) -> torch.Tensor:
+    """SnapKV scores over a dense K (``KVEviction.snapkv_selection``'s
+    ranking, kv_cache.py:149-163): ``q`` ``[num_heads, D]`` (any shape with
+    that many elements), ``k`` ``[Hkv, S, D]`` or ``[1, Hkv, S, D]``, fp16 or
+    fp32; returns fp32 ``[S]``, the mean over q heads of
+    ``softmax(q_h . k / sqrt(D))`` (``scale`` overrides 1/sqrt(D))."""
+    _on_gpu("q_last", q)
+    _on_gpu("k_full", k, None, q.device)
+    if k.dim() == 4:
+        _require(k.shape[0] == 1, "k_full [1, Hkv, S, D] expected")
+        k = k[0]
+    _require(k.dim() == 3 and k.shape[0] == num_kv_heads, f"k_full must be [{num_kv_heads}, S, D]")
+    _require(k.dtype in (torch.float16, torch.float32), f"k_full must be fp16 or fp32, got {k.dtype}", TypeError)
+    d = k.shape[2]
+    q2 = _q_rows(q, num_heads)
+    _require(q2.shape[1] == d, f"q_last head_dim {q2.shape[1]} != k_full head_dim {d}")
+    if k.stride(2) != 1:
+        k = k.contiguous()
+    sc = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    return _snapkv_run(k.shape[1], num_heads, q.device, lambda lib, out, ws, nb: lib.s8kv_snapkv_scores_dense(
+        q2.data_ptr(), 1 if q2.dtype == torch.float32 else 0, q2.stride(0), num_heads, num_kv_heads, d, k.data_ptr(),
+        1 if k.dtype == torch.float32 else 0, k.stride(0), k.stride(1), k.shape[1], sc, out.data_ptr(), ws.data_ptr(),
+        nb, _stream(q2)))
+
+
+def snapkv_scores_paged(q: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor, blocks: Sequence[int],
+                        length: int, num_heads: int, scale: float | None = None) -> torch.Tensor:
+    """SnapKV scores of one sequence over its int8 K in the paged cache
+    (``k_cache`` ``[N, Hkv, bs, D]`` layer view, ``blocks`` its block ids in
+    order): the same quantity as ``snapkv_scores`` over the exactly
+    dequantized keys, without materializing them."""
+    _on_gpu("q_last", q)
+    dev = q.device
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("k_scale", k_scale, torch.float32, dev)
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(tuple(k_scale.shape) == (n, hkv, bs) and k_scale.is_contiguous(), "k_scale must be [N, Hkv, bs]")
+    length = int(length)
+    need = -(-length // bs)
+    blocks = [int(b) for b in blocks]
+    _require(len(blocks) >= need, f"{len(blocks)} blocks cannot hold {length} tokens")
+    _require(all(0 <= b < n for b in blocks[:need]), f"block ids must be in [0, {n})")
+    q2 = _q_rows(q, num_heads)
+    _require(q2.shape[1] == d, f"q_last head_dim {q2.shape[1]} != cache head_dim {d}")
+    row = torch.tensor(blocks[:max(need, 1)], dtype=torch.int32).to(dev)
+    sc = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    return _snapkv_run(length, num_heads, dev, lambda lib, out, ws, nb: lib.s8kv_snapkv_scores_paged(
+        q2.data_ptr(), 1 if q2.dtype == torch.float32 else 0, q2.stride(0), num_heads, hkv, d, k_cache.data_ptr(),
+        k_scale.data_ptr(), n, bs, row.data_ptr(), length, sc, out.data_ptr(), ws.data_ptr(), nb, _stream(q2)))
+
+
+def gather_slots(tensors: Sequence[torch.Tensor], src_slots: Sequence[int], dst_slots: Sequence[int],
+                 block_size: int) -> None:
+    """Copy the rows of flat slots ``src_slots[j]`` to ``dst_slots[j]`` in
+    every layer of every cache tensor (``[L, N, Hkv, bs, ...]``), byte for
+    byte: the kept tokens of a keep-list compaction."""
+    _require(1 <= len(tensors) <= 8, "gather_slots takes 1..8 tensors")
+    src_l, dst_l = [int(x) for x in src_slots], [int(x) for x in dst_slots]
+    _require(len(src_l) == len(dst_l), "src and dst differ in length")
+    if not src_l:
+        return
+    t0 = tensors[0]
+    _on_gpu("tensors[0]", t0)
+    dev = t0.device
+    nl, nb, hkv, bs = t0.shape[:4]
+    _require(int(block_size) == bs, f"block_size {block_size} does not match the cache ({bs})")
+    _require(all(0 <= x < nb * bs for x in src_l + dst_l), f"slots must be in [0, {nb * bs})")
+    _require(not (set(src_l) & set(dst_l)), "source and destination slots overlap")
+    ptrs, rbytes, lstrides = [], [], []
+    for i, t in enumerate(tensors):
+        _on_gpu(f"tensors[{i}]", t, None, dev)
+        _require(t.is_contiguous() and tuple(t.shape[:4]) == (nl, nb, hkv, bs),
+                 f"tensors[{i}] must be contiguous [{nl}, {nb}, {hkv}, {bs}, ...]")
+        ptrs.append(t.data_ptr())
+        rbytes.append(t[0, 0, 0, 0].numel() * t.element_size())
+        lstrides.append(t.stride(0) * t.element_size())
+    src_t = torch.tensor(src_l, dtype=torch.int32).to(dev)
+    dst_t = torch.tensor(dst_l, dtype=torch.int32).to(dev)
+    n = len(tensors)
+    rc = _lib.load().s8kv_gather_slots(n, (ctypes.c_void_p * n)(*ptrs), (ctypes.c_int64 * n)(*rbytes),
+                                       (ctypes.c_int64 * n)(*lstrides), nl, hkv, nb, bs, src_t.data_ptr(),
+                                       dst_t.data_ptr(), len(src_l), _stream(t0))
+    _lib.check(rc, "gather_slots")

@@ -26,8 +26,6 @@ the pool (moving live blocks into free holes) through the block-copy kernel.
 
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import torch
 
@@ -552,10 +550,10 @@ class PagedKVCache:
         off = pos % self.block_size
         kq = self.k_cache[row][blk, :, off].float() * self.k_scale[row][blk, :, off].unsqueeze(-1)
         d = self.head_dim
-        h = torch.ones(1, 1, dtype=torch.float32, device=self.device)
-        while h.shape[0] < d:
-            h = torch.cat([torch.cat([h, h], 1), torch.cat([h, -h], 1)], 0)
-        k = ((kq.to(dtype).float() @ (h / math.sqrt(d)))).to(dtype)
+        # the reference's recipe, rotate_last((k_i8 * s_k).to(dtype)), with the
+        # rotation on the row kernel: each row's rounding is independent of
+        # how many rows are read
+        k = ops.rotate_rows(kq.to(dtype))
         if self.v_quant == "lloydmax3":
             codes = _unpack3(self.v_packed[row][blk, :, off], d)
             nb = d // self.lloyd_block
@@ -584,7 +582,19 @@ class PagedKVCache:
         owned[-1] = new
         return new
 
-    def compact(self) -> list[tuple[int, int]]:
+    def evict_after_prefill(self, slot: int, seq_len: int, *, eviction_config, num_heads: int,
+                            keep_mask: list[int] | None = None, q_last: torch.Tensor | None = None,
+                            k_full: torch.Tensor | None = None, logits_full: torch.Tensor | None = None,
+                            logits_fn=None) -> dict:
+        """Prompt-time eviction of `slot` with this cache's geometry
+        (kv_cache.py:1303-1336); see ``eviction.KVEviction.evict``."""
+        from .eviction import KVEviction
+
+        return KVEviction.evict(self, slot, seq_len, eviction_config=eviction_config, num_heads=num_heads,
+                                num_kv_heads=self.num_kv_heads, head_dim=self.head_dim, q_last=q_last,
+                                k_full=k_full, keep_mask=keep_mask, logits_full=logits_full, logits_fn=logits_fn)
+
+    def defragment(self) -> list[tuple[int, int]]:
         """Move every live block above the free watermark into the lowest free
         holes, so the live set occupies blocks ``[0, used_blocks)``.  One GPU
         block copy for all layers and tensors, then every reference (slot

@@ -245,7 +245,7 @@ def test_c4_chunked_prefill_prefix_cow_and_compaction():
         cache.free(s)
     print(f"C4: freed {len(victims)} sequences ({used0 - cache.used_blocks} blocks), compacting", flush=True)
     before = [_np(t[0]) for t in cache._tensors()]
-    moves = cache.compact()
+    moves = cache.defragment()
     torch.cuda.synchronize()
     assert moves, "C4: nothing to compact"
     after = [_np(t[0]) for t in cache._tensors()]
