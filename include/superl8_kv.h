@@ -264,15 +264,22 @@ int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
  * s8kv_verify_k8v3, but of the prefix only the last `window` keys,
  * [max(0, prefix_lens[b] - window), prefix_lens[b]), are visible (drafts as
  * before).  The reference reads that prefix window back dense and appends the
- * drafts (gqa_attention.py:305-314, read_dense at kv_cache.py:1233-1299).
- * window >= 1.
+ * drafts' fresh fp16 K / V (gqa_attention.py:298-314, read_dense at
+ * kv_cache.py:1233-1299): pass them as k_draft (fp32, already rotated:
+ * s8kv_rotate_rows of the fp16 K) and v_draft (fp16), each
+ * [batch][max_queries][num_kv_heads][head_dim] at element strides (per row,
+ * draft, head; rows 16-byte aligned), and draft i of row b is attended with
+ * those values instead of its cache row (K carried as fp16 hi + lo).  k_draft NULL: the drafts are read
+ * from the cache, as the unwindowed verify reads them.  window >= 1.
  */
 int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                             int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
                             const int8_t* k_cache, const float* k_scale, const int8_t* v_cache, const float* v_scale,
                             int64_t num_blocks, int block_size, const int32_t* block_table,
                             int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                            const int64_t* tree_mask, int max_context_len, int window, float scale, void* out,
+                            const int64_t* tree_mask, int max_context_len, int window, const void* k_draft,
+                            int64_t kd_stride_b, int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft,
+                            int64_t vd_stride_b, int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out,
                             void* stream);
 int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                             int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
@@ -280,7 +287,9 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
                             const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                             int block_size, const int32_t* block_table, int64_t block_table_stride,
                             const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                            int max_context_len, int window, float scale, void* out, void* stream);
+                            int max_context_len, int window, const void* k_draft, int64_t kd_stride_b,
+                            int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft, int64_t vd_stride_b,
+                            int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* stream);
 
 /*
  * Prefill attention over fresh fp16 K / V (not the cache), varlen batched:
@@ -291,8 +300,11 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * k, v [tokens, num_kv_heads, head_dim] (element strides per token and head,
  * head_dim contiguous; K and V rows 16-byte aligned).  causal: query s sees
  * keys j <= s + nk - nq (bottom-right aligned; none when that is negative),
- * else all nk keys; window_left >= 0 (causal only) also hides keys
- * j < s + nk - nq - window_left (a sliding-window layer), -1 for none.
+ * else all nk keys; window_left >= 1 (causal only) also hides keys
+ * j <= s + nk - nq - window_left, so each query sees its last window_left
+ * keys, itself included (the window the reference's sliding-window decode
+ * attends: gqa_attention.py:150-154, read_dense(window=) at
+ * kv_cache.py:1233-1299); -1 for none, 0 is rejected.
  * out [tokens_q, num_q_heads, head_dim] with strides
  * o_stride_t, o_stride_h; only the sequences' own query tokens are written.
  * The causal diagonal comes from each sequence's own counts.  max_seqlen_q

@@ -444,7 +444,7 @@ def paged_decode(q, layer: LayerCache, block_table, context_lens, scale, window=
 
 
 def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query_lens=None, tree_mask=None,
-                 window=None) -> np.ndarray:
+                 window=None, fresh_drafts=None) -> np.ndarray:
     """Multi-query verify attention over the paged cache in float64.
 
     Query s of row b sees every prefix key ``j < prefix_lens[b]`` plus draft key
@@ -458,6 +458,10 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
     layer sees only the last ``window`` prefix keys, ``[max(0, p - window), p)``,
     plus its drafts -- the reference reads that prefix window back dense and
     appends the drafts (gqa_attention.py:305-314 with kv_cache.py:1233-1299).
+    ``fresh_drafts`` = (k, v) fp16 ``[B, S, Hkv, D]``: the drafts enter with
+    these values instead of their cache rows -- the reference's window verify
+    concatenates the layer's fresh fp16 draft K / V to the dequantized prefix
+    window (gqa_attention.py:298-303).
 
     q: ``[B, Hq, S, D]`` -> float64 ``[B, Hq, S, D]``."""
     q = np.asarray(q, dtype=np.float64)
@@ -472,6 +476,9 @@ def paged_verify(q, layer: LayerCache, block_table, prefix_lens, scale, *, query
             continue
         total = p + nq
         k, v = exact_kv(layer, block_table[b], total)
+        if fresh_drafts is not None:
+            k[:, p:] = np.asarray(fresh_drafts[0], dtype=np.float64)[b, :nq].transpose(1, 0, 2)
+            v[:, p:] = np.asarray(fresh_drafts[1], dtype=np.float64)[b, :nq].transpose(1, 0, 2)
         j = np.arange(total)
         vis = np.zeros((nq, total), dtype=bool)
         for s in range(nq):
@@ -497,10 +504,13 @@ def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True, window_left=
     ``cu_k[b] ..``; causal is bottom-right aligned (query s sees keys
     ``j <= s + nk - nq``; a query that sees none gives zeros).  The reference's
     kernel is absent (the superl8 package), so this is the exact attention the
-    reference's int8 kernel approximates.  CHOICE: ``window_left`` (causal
-    only) follows the flash-attention convention the reference's
-    ``window_left`` argument comes from: query i (aligned bottom-right) sees
-    keys ``i - window_left .. i``.  Returns float64 ``[Tq, Hq, D]``."""
+    reference's int8 kernel approximates.  CHOICE: ``window_left >= 1``
+    (causal only) lets query i (aligned bottom-right) see its last
+    ``window_left`` keys, ``i - window_left + 1 .. i`` -- the window the
+    reference's decode side attends for the same layer (``_window`` keeps the
+    last ``window_left`` keys, gqa_attention.py:150-154; ``read_dense(window=)``
+    starts at ``length - window``, kv_cache.py:1251), so a token sees the same
+    keys at prefill and at decode.  Returns float64 ``[Tq, Hq, D]``."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -515,7 +525,9 @@ def dense_varlen_attention(q, k, v, cu_q, cu_k, scale, causal=True, window_left=
         j = np.arange(nk)
         vis = (j[None, :] <= np.arange(nq)[:, None] + nk - nq) if causal else np.ones((nq, nk), bool)
         if window_left is not None:
-            vis &= j[None, :] >= np.arange(nq)[:, None] + nk - nq - int(window_left)
+            if int(window_left) < 1:
+                raise ValueError("window_left must be >= 1")
+            vis &= j[None, :] > np.arange(nq)[:, None] + nk - nq - int(window_left)
         live = vis.any(axis=1)
         for h in range(hq):
             kv = h // g

@@ -63,6 +63,10 @@ struct Cfg {
   static constexpr int VJOBS = kTile * NG * SPLIT;              // K8V3: expansion jobs per tile
   static_assert(!K8V3 || (VJOBS <= kThreads && (SPLIT == 1 || SPLIT == 2)), "one K8V3 job per thread");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
+  // window verify with fresh drafts: the low fp16 part of the draft keys'
+  // fp32 K, one K-sized tile per buffer after the block ids
+  static constexpr int KLO_OFF = (SMEM + 15) / 16 * 16;
+  static constexpr int SMEM_WIN = KLO_OFF + 2 * KBYTES;
 };
 
 struct VerifyArgs {
@@ -84,6 +88,12 @@ struct VerifyArgs {
   int max_context_len;
   int n_qblocks;              // 64-row query blocks per (sequence, KV head)
   int window;                 // verify_kernel<.., WIN>: only the last `window` prefix keys are visible
+  // WIN, optional: the drafts' fresh K (rotated, fp32) and V (fp16),
+  // attended in place of their cache rows (draft i of row b, head h at
+  // b * stride_b + i * stride_s + h * stride_h; head_dim contiguous)
+  const float* kd;
+  const _Float16* vd;
+  int64_t kd_stride_b, kd_stride_s, kd_stride_h, vd_stride_b, vd_stride_s, vd_stride_h;
   // dense inputs (verify_kernel<D, false, false, true>: prefill attention over
   // fresh fp16 K / V, token-major, sequences delimited by cu_seqlens)
   const int32_t* cu_q;
@@ -301,11 +311,27 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         }
       }
     };
-    // registers -> LDS buffer, converting int8 to fp16
-    auto store_tile = [&](const TileRegs& R, int buf) {
+    // Window verify with fresh drafts: whether the tile at `base` holds
+    // draft keys (wave-uniform), whose K then has a low fp16 part.
+    auto fresh_tile = [&](int base) -> bool {
+      if constexpr (WIN && !DENSE) return a.kd != nullptr && base + kTile > prefix && base < prefix + nq;
+      return false;
+    };
+    // registers -> LDS buffer, converting int8 to fp16.  With fresh drafts
+    // (WIN and a.kd set), the rows of draft keys take the drafts' fp16 K / V
+    // and unit scales instead.
+    auto store_tile = [&](const TileRegs& R, int buf, int base) {
       char* kb = smem + buf * C::BUF;
       char* vb = kb + C::KBYTES;
       float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
+      // draft index of tile key tt, or -1 when it is a prefix key / not fresh
+      auto fresh_draft = [&](int tt) -> int {
+        if constexpr (WIN && !DENSE) {
+          const int di = base + tt - prefix;
+          return (a.kd != nullptr && di >= 0 && di < nq) ? di : -1;
+        }
+        return -1;
+      };
       if constexpr (DENSE) {
 #pragma unroll
         for (int i = 0; i < C::LOADS_F16; ++i) {
@@ -324,20 +350,52 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         const int ch = tid + i * kThreads;
         if (ch < C::CHUNKS) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
-          const half8_t k0 = i8x8_to_f16(u32x2_t{R.k[i].x, R.k[i].y});
-          const half8_t k1 = i8x8_to_f16(u32x2_t{R.k[i].z, R.k[i].w});
+          const int di = fresh_draft(tt);
+          half8_t k0, k1, v0, v1;
+          if (di >= 0) {  // the draft's fresh values, dims part*16 .. +16: K as fp16 hi (+ lo below)
+            const float* kp = a.kd + (int64_t)b * a.kd_stride_b + (int64_t)di * a.kd_stride_s +
+                              (int64_t)h * a.kd_stride_h + part * 16;
+            const _Float16* vp = a.vd + (int64_t)b * a.vd_stride_b + (int64_t)di * a.vd_stride_s +
+                                 (int64_t)h * a.vd_stride_h + part * 16;
+            half8_t l0, l1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float x0 = kp[e], x1 = kp[8 + e];
+              k0[e] = (_Float16)x0;
+              k1[e] = (_Float16)x1;
+              l0[e] = (_Float16)(x0 - (float)k0[e]);
+              l1[e] = (_Float16)(x1 - (float)k1[e]);
+            }
+            char* klo = smem + C::KLO_OFF + buf * C::KBYTES + tt * C::KROW + part * 32;
+            *reinterpret_cast<half8_t*>(klo) = l0;
+            *reinterpret_cast<half8_t*>(klo + 16) = l1;
+            v0 = *reinterpret_cast<const half8_t*>(vp);
+            v1 = *reinterpret_cast<const half8_t*>(vp + 8);
+          } else {
+            if constexpr (WIN && !DENSE) {
+              if (fresh_tile(base)) {  // a prefix key in a tile holding drafts: no low part
+                char* klo = smem + C::KLO_OFF + buf * C::KBYTES + tt * C::KROW + part * 32;
+                *reinterpret_cast<half8_t*>(klo) = half8_t{};
+                *reinterpret_cast<half8_t*>(klo + 16) = half8_t{};
+              }
+            }
+            k0 = i8x8_to_f16(u32x2_t{R.k[i].x, R.k[i].y});
+            k1 = i8x8_to_f16(u32x2_t{R.k[i].z, R.k[i].w});
+            if constexpr (!K8V3) {
+              v0 = i8x8_to_f16(u32x2_t{R.v[i].x, R.v[i].y});
+              v1 = i8x8_to_f16(u32x2_t{R.v[i].z, R.v[i].w});
+            }
+          }
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = k0;
           *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = k1;
-          if constexpr (!K8V3) {
-            const half8_t v0 = i8x8_to_f16(u32x2_t{R.v[i].x, R.v[i].y});
-            const half8_t v1 = i8x8_to_f16(u32x2_t{R.v[i].z, R.v[i].w});
+          if (!K8V3 || di >= 0) {  // K8V3: prefix V rows come from the code expansion below
             *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32) = v0;
             *reinterpret_cast<half8_t*>(vb + vrow_of(tt) * C::VROW + part * 32 + 16) = v1;
           }
         }
       }
       if constexpr (K8V3) {  // 32 / SPLIT codes of one group -> fp16 codebook entries
-        if (tid < C::VJOBS) {
+        if (tid < C::VJOBS && fresh_draft((tid / C::SPLIT) / C::NG) < 0) {
           const int grp = tid / C::SPLIT, part = tid % C::SPLIT;  // part: which 32 / SPLIT values
           const int tt = grp / C::NG, gi = grp % C::NG;
           const int sh = part * (32 / C::SPLIT);
@@ -357,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           }
         }
       }
-      if (tid < (1 + C::NB) * kTile) sb[tid] = R.s;
+      if (tid < (1 + C::NB) * kTile) sb[tid] = fresh_draft(tid & (kTile - 1)) >= 0 ? 1.0f : R.s;
     };
 
     // ---- one 32-key tile from LDS buffer `buf` ----
@@ -376,6 +434,14 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           const half8_t ka = *reinterpret_cast<const half8_t*>(krow + 16 * m);
           cacc = mfma16x16x32(ka, qhi[m], cacc);
           cacc = mfma16x16x32(ka, qlo[m], cacc);
+        }
+        if constexpr (WIN && !DENSE) {  // fresh draft keys: K = hi + lo (masked or not)
+          if (fresh_tile(base)) {
+            const char* lrow = smem + C::KLO_OFF + buf * C::KBYTES + (16 * s + c) * C::KROW + g * C::KCH * 2;
+#pragma unroll
+            for (int m = 0; m < C::NQK; ++m)
+              cacc = mfma16x16x32(*reinterpret_cast<const half8_t*>(lrow + 16 * m), qhi[m], cacc);
+          }
         }
         sc[s] = cacc;
       }
@@ -473,18 +539,18 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     TileRegs ra, rb;
     load_tile(ra, u0);
     if (ntiles > 1) load_tile(rb, u0 + kTile);
-    store_tile(ra, 0);
+    store_tile(ra, 0, u0);
     __syncthreads();
     for (int t = 0; t < ntiles; t += 2) {
       const int base = u0 + t * kTile;
       if (t + 2 < ntiles) load_tile(ra, base + 2 * kTile);
       compute(0, base);
-      if (t + 1 < ntiles) store_tile(rb, 1);
+      if (t + 1 < ntiles) store_tile(rb, 1, base + kTile);
       __syncthreads();
       if (t + 1 >= ntiles) break;
       if (t + 3 < ntiles) load_tile(rb, base + 3 * kTile);
       compute(1, base + kTile);
-      if (t + 2 < ntiles) store_tile(ra, 0);
+      if (t + 2 < ntiles) store_tile(ra, 0, base + 2 * kTile);
       __syncthreads();
     }
   }
@@ -512,7 +578,7 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
   static bool attr = false;
   if (!attr) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN, DENSE>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
+                            hipFuncAttributeMaxDynamicSharedMemorySize, WIN ? C::SMEM_WIN : C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
     }
@@ -524,7 +590,8 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE>), dim3((unsigned)grid), dim3(kThreads), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE>), dim3((unsigned)grid), dim3(kThreads),
+                     WIN ? C::SMEM_WIN : C::SMEM, stream, a);
   return check_launch("s8kv_verify");
 }
 
@@ -532,6 +599,15 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
 }  // namespace s8kv
 
 using namespace s8kv;
+
+// Optional fresh fp16 drafts of the window verify: K (rotated) and V, element
+// strides per row, draft and head.
+struct FreshDrafts {
+  const void* k;
+  const void* v;
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+};
 
 // Checks and arguments shared by both layouts (everything but V).
 static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num_q_heads, int num_kv_heads,
@@ -584,7 +660,7 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
                                 const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                 int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
                                 const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream,
-                            int window) {
+                            int window, const FreshDrafts* fresh) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   verify::VerifyArgs a{};
@@ -593,6 +669,21 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
   a.window = window;
+  if (fresh != nullptr && fresh->k != nullptr) {
+    S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
+    S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
+                     fresh->k_stride[1] % 4 == 0 && fresh->k_stride[2] % 4 == 0 && fresh->v_stride[0] % 8 == 0 &&
+                     fresh->v_stride[1] % 8 == 0 && fresh->v_stride[2] % 8 == 0,
+                 S8KV_ERR_INVALID, "verify: fresh draft rows must be 16-byte aligned");
+    a.kd = (const float*)fresh->k;
+    a.vd = (const _Float16*)fresh->v;
+    a.kd_stride_b = fresh->k_stride[0];
+    a.kd_stride_s = fresh->k_stride[1];
+    a.kd_stride_h = fresh->k_stride[2];
+    a.vd_stride_b = fresh->v_stride[0];
+    a.vd_stride_s = fresh->v_stride[1];
+    a.vd_stride_h = fresh->v_stride[2];
+  }
   S8KV_REQUIRE(v_cache && v_scale, S8KV_ERR_INVALID, "verify: null pointer argument");
   a.v_cache = v_cache;
   a.v_scale = v_scale;
@@ -624,7 +715,7 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
   return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
                           block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
-                          stream, 0);
+                          stream, 0, nullptr);
 }
 
 extern "C" int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -632,13 +723,17 @@ extern "C" int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads
                                 const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
                                 const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                 int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                                const int64_t* tree_mask, int max_context_len, int window, float scale, void* out,
+                                const int64_t* tree_mask, int max_context_len, int window, const void* k_draft,
+                                int64_t kd_stride_b, int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft,
+                                int64_t vd_stride_b, int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out,
                                 void* stream) {
   S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
+  const FreshDrafts fresh{k_draft, v_draft, {kd_stride_b, kd_stride_s, kd_stride_h},
+                          {vd_stride_b, vd_stride_s, vd_stride_h}};
   return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
                           block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
-                          stream, window);
+                          stream, window, &fresh);
 }
 
 
@@ -649,7 +744,7 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
                                 int block_size, const int32_t* block_table, int64_t block_table_stride,
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
                                 int max_context_len, float scale, void* out, void* stream,
-                            int window) {
+                            int window, const FreshDrafts* fresh) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
@@ -661,6 +756,21 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
   a.window = window;
+  if (fresh != nullptr && fresh->k != nullptr) {
+    S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
+    S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
+                     fresh->k_stride[1] % 4 == 0 && fresh->k_stride[2] % 4 == 0 && fresh->v_stride[0] % 8 == 0 &&
+                     fresh->v_stride[1] % 8 == 0 && fresh->v_stride[2] % 8 == 0,
+                 S8KV_ERR_INVALID, "verify: fresh draft rows must be 16-byte aligned");
+    a.kd = (const float*)fresh->k;
+    a.vd = (const _Float16*)fresh->v;
+    a.kd_stride_b = fresh->k_stride[0];
+    a.kd_stride_s = fresh->k_stride[1];
+    a.kd_stride_h = fresh->k_stride[2];
+    a.vd_stride_b = fresh->v_stride[0];
+    a.vd_stride_s = fresh->v_stride[1];
+    a.vd_stride_h = fresh->v_stride[2];
+  }
   S8KV_REQUIRE(v_packed && v_norm && v_codebook, S8KV_ERR_INVALID, "verify: null pointer argument");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   a.v_cache = v_packed;
@@ -684,7 +794,7 @@ extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int n
   return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
                           block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
-                          max_context_len, scale, out, stream, 0);
+                          max_context_len, scale, out, stream, 0, nullptr);
 }
 
 extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -693,12 +803,16 @@ extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads
                                 const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                                 int block_size, const int32_t* block_table, int64_t block_table_stride,
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                                int max_context_len, int window, float scale, void* out, void* stream) {
+                                int max_context_len, int window, const void* k_draft, int64_t kd_stride_b,
+                                int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft, int64_t vd_stride_b,
+                                int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* stream) {
   S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
+  const FreshDrafts fresh{k_draft, v_draft, {kd_stride_b, kd_stride_s, kd_stride_h},
+                          {vd_stride_b, vd_stride_s, vd_stride_h}};
   return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
                           block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
-                          max_context_len, scale, out, stream, window);
+                          max_context_len, scale, out, stream, window, &fresh);
 }
 
 
@@ -719,6 +833,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   S8KV_REQUIRE(q && k && v && cu_seqlens_q && cu_seqlens_k && out, S8KV_ERR_INVALID,
                "attn_varlen: null pointer argument");
   S8KV_REQUIRE(window_left < 0 || causal, S8KV_ERR_UNSUPPORTED, "attn_varlen: window_left needs causal");
+  S8KV_REQUIRE(window_left != 0, S8KV_ERR_INVALID, "attn_varlen: window_left 0 would leave no key (>= 1, or -1)");
   S8KV_REQUIRE((uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && k_stride_t % 8 == 0 && k_stride_h % 8 == 0 &&
                    v_stride_t % 8 == 0 && v_stride_h % 8 == 0,
                S8KV_ERR_INVALID, "attn_varlen: K and V rows must be 16-byte aligned");
@@ -748,8 +863,8 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.causal = causal ? 1 : 0;
   a.out = (_Float16*)out;
   hipStream_t s = (hipStream_t)stream;
-  if (window_left >= 0) {  // query s sees keys [s + nk - nq - window_left, s + nk - nq]
-    a.window = window_left;
+  if (window_left > 0) {  // query s sees keys (s + nk - nq - window_left, s + nk - nq]: window_left keys
+    a.window = window_left - 1;  // the kernel's band: keys >= s + nk - nq - window
     switch (head_dim) {
       case 64: return verify::launch<64, false, true, true>(a, s);
       case 128: return verify::launch<128, false, true, true>(a, s);

@@ -448,8 +448,27 @@ def _verify_inputs(q, k_cache, k_scale, block_table, prefix_lens, block_size, qu
     return keep, head, tail, (n, hkv, bs, d), out
 
 
+def _fresh_drafts(k_draft, v_draft, b, s_, hkv, d, dev):
+    """(keep-alive tensors, C arguments) of the window verify's fresh drafts:
+    K rotated on the row kernel in fp32 (the kernel splits it into fp16
+    hi + lo), V fp16, both ``[B, S, Hkv, D]`` with 16-byte rows."""
+    if k_draft is None and v_draft is None:
+        return (), (None, 0, 0, 0, None, 0, 0, 0)
+    _require(k_draft is not None and v_draft is not None, "k_draft and v_draft go together")
+    for name, t in (("k_draft", k_draft), ("v_draft", v_draft)):
+        _on_gpu(name, t, torch.float16, dev)
+        _require(tuple(t.shape) == (b, s_, hkv, d), f"{name} must be [{b}, {s_}, {hkv}, {d}] (the layer's [B, S, Hkv, D])")
+    kr = rotate_rows(k_draft.float())  # contiguous fp32, rotated as the cache's K is
+    vd = v_draft
+    if vd.stride(3) != 1 or vd.data_ptr() % 16 or any(x % 8 for x in vd.stride()[:3]):
+        vd = vd.contiguous()
+    return (kr, vd), (kr.data_ptr(), kr.stride(0), kr.stride(1), kr.stride(2), vd.data_ptr(), vd.stride(0),
+                      vd.stride(1), vd.stride(2))
+
+
 def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix_lens, block_size, *,
-                      query_lens=None, tree_mask=None, max_context_len, scale, window=None):
+                      query_lens=None, tree_mask=None, max_context_len, scale, window=None, k_draft=None,
+                      v_draft=None):
     """Multi-query attention of draft / chunk queries over the int8 paged cache.
 
     ``q``: fp16 ``[B, Hq, S, D]`` (any strides with D contiguous, e.g. the
@@ -460,8 +479,11 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     gqa_attention.py:105-129) or when bit i of ``tree_mask[b, s]`` (int64
     ``[B, S]``) is set (tree verify).  Queries ``s >= query_lens[b]`` give
     zeros.  ``window`` (a sliding-window layer): of the prefix only the last
-    ``window`` keys are visible (gqa_attention.py:305-314).  Returns fp16
-    ``[B, Hq, S, D]``."""
+    ``window`` keys are visible (gqa_attention.py:305-314); with ``k_draft``
+    / ``v_draft`` (fp16 ``[B, S, Hkv, D]``, the layer's fresh draft K / V)
+    the drafts are attended with those values, as the reference's window
+    verify concatenates them to the dequantized prefix window
+    (gqa_attention.py:298-303).  Returns fp16 ``[B, Hq, S, D]``."""
     keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
         q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
     dev = out.device
@@ -472,11 +494,13 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     if out.shape[0] == 0 or out.shape[2] == 0:
         return out
     lib = _lib.load()
+    _require(window is not None or k_draft is None, "fresh drafts (k_draft / v_draft) need a window")
     if window is not None:
         _require(int(window) >= 1, f"window must be >= 1, got {window}")
+        alive, drafts = _fresh_drafts(k_draft, v_draft, out.shape[0], out.shape[2], hkv, d, dev)
         rc = lib.s8kv_verify_window_int8(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
-            *tail, int(window), float(scale), out.data_ptr(), _stream(keep[0]),
+            *tail, int(window), *drafts, float(scale), out.data_ptr(), _stream(keep[0]),
         )
     else:
         rc = lib.s8kv_verify_int8(
@@ -488,7 +512,8 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
 
 
 def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, prefix_lens, block_size,
-                           *, query_lens=None, tree_mask=None, max_context_len, scale, window=None):
+                           *, query_lens=None, tree_mask=None, max_context_len, scale, window=None, k_draft=None,
+                           v_draft=None):
     """``attn_paged_verify`` over the K8V3 cache (int8 K, 3-bit Lloyd-Max V
     ``codebook[code] * block norm``): one launch for what the reference
     computes on a k8v3 cache with S sequential ``attn_paged_decode_k8v3``
@@ -508,11 +533,13 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
     if out.shape[0] == 0 or out.shape[2] == 0:
         return out
     lib = _lib.load()
+    _require(window is not None or k_draft is None, "fresh drafts (k_draft / v_draft) need a window")
     if window is not None:
         _require(int(window) >= 1, f"window must be >= 1, got {window}")
+        alive, drafts = _fresh_drafts(k_draft, v_draft, out.shape[0], out.shape[2], hkv, d, dev)
         rc = lib.s8kv_verify_window_k8v3(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
-            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, int(window), float(scale), out.data_ptr(),
+            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, int(window), *drafts, float(scale), out.data_ptr(),
             _stream(keep[0]),
         )
     else:
@@ -529,10 +556,10 @@ def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
     ``superl8.attn_int8_varlen``, gqa_attention.py:81-104): ``q`` fp16
     ``[Tq, Hq, D]``, ``k``, ``v`` fp16 ``[Tk, Hkv, D]`` token-major (head_dim
     contiguous), sequences delimited by int32 ``cu_seqlens_q`` / ``cu_seqlens_k``
-    (``[B + 1]``).  ``causal``: bottom-right aligned.  ``window_left``
-    (causal only): query i also sees no key below ``i - window_left`` (the
-    flash-attention convention, i aligned bottom-right).  Returns fp16
-    ``[Tq, Hq, D]``."""
+    (``[B + 1]``).  ``causal``: bottom-right aligned.  ``window_left >= 1``
+    (causal only): query i sees only its last ``window_left`` keys, itself
+    included -- the keys the reference's sliding-window decode attends for
+    the same layer (gqa_attention.py:150-154).  Returns fp16 ``[Tq, Hq, D]``."""
     _on_gpu("q", q, torch.float16)
     dev = q.device
     _on_gpu("k", k, torch.float16, dev)
@@ -541,6 +568,7 @@ def attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
     _on_gpu("cu_seqlens_k", cu_seqlens_k, torch.int32, dev)
     _require(q.dim() == 3 and k.dim() == 3 and v.shape == k.shape and k.shape[2] == q.shape[2],
              "attn_varlen: q [Tq, Hq, D], k / v [Tk, Hkv, D]")
+    _require(window_left is None or int(window_left) >= 1, f"window_left must be >= 1, got {window_left}")
     tq, hq, d = q.shape
     hkv = k.shape[1]
     _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.shape == cu_seqlens_k.shape and cu_seqlens_q.numel() >= 1,

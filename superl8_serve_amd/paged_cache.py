@@ -517,10 +517,13 @@ class PagedKVCache:
 
     def verify_attn(self, layer: int, q: torch.Tensor, slots: list[int], prefix_lens: list[int], *, scale: float,
                     query_lens: list[int] | None = None, tree_mask: torch.Tensor | None = None,
-                    window: int | None = None) -> torch.Tensor:
+                    window: int | None = None, k_draft: torch.Tensor | None = None,
+                    v_draft: torch.Tensor | None = None) -> torch.Tensor:
         """Multi-query attention of drafts (already written at positions
         ``prefix_lens[b] ..``): chain / chunk when `tree_mask` is None, else tree.
-        ``q``: fp16 ``[B, Hq, S, D]``."""
+        ``q``: fp16 ``[B, Hq, S, D]``.  A sliding-window layer (``window``)
+        may pass the drafts' fresh K / V ``[B, S, Hkv, D]`` to attend them
+        unquantized, as the reference's window verify does."""
         row = self._layer_row(layer)
         s = q.shape[2]
         ql = query_lens if query_lens is not None else [s] * len(slots)
@@ -528,7 +531,7 @@ class PagedKVCache:
         common = dict(
             query_lens=None if query_lens is None else torch.tensor(query_lens, dtype=torch.int32, device=self.device),
             tree_mask=tree_mask, max_context_len=min(max_ctx, self.max_blocks_per_seq * self.block_size),
-            scale=scale, window=window)
+            scale=scale, window=window, k_draft=k_draft, v_draft=v_draft)
         bt = self.block_table(slots)
         pl = torch.tensor(prefix_lens, dtype=torch.int32, device=self.device)
         if self.v_quant == "lloydmax3":

@@ -89,8 +89,8 @@ def test_attn_varlen_writes_only_own_tokens():
 
 @pytest.mark.parametrize("d,qlens,klens,w", [
     (128, [300, 33, 7], [300, 33, 7], 64),      # band inside long sequences, shorter ones
-    (128, [100, 40], [400, 40], 0),             # only the diagonal key; a chunk after a prefix
-    (64, [257], [257], 31),                     # band edge off a 32-key tile
+    (128, [100, 40], [400, 40], 1),             # only the diagonal key; a chunk after a prefix
+    (64, [257], [257], 32),                     # band edge off a 32-key tile
     (256, [90, 130], [200, 130], 100),          # head_dim 256
 ])
 def test_attn_varlen_window_left(d, qlens, klens, w):

@@ -221,7 +221,54 @@ def test_window_verify_ignores_keys_before_the_window():
         for pos in range(max(0, int(p) - window)):
             blk, off = case.block_table[b, pos // case.block_size], pos % case.block_size
             kc[blk, :, off] = 127
-            ks[blk, :, off] = 1e4
+            ks[blk, :, off] = np.inf if pos % 2 else np.nan  # non-finite scales must not reach the output
             vc[blk, :, off] = -127
-            vs[blk, :, off] = 1e4
+            vs[blk, :, off] = np.nan if pos % 2 else np.inf
     assert np.array_equal(_verify(case, (kc, ks, vc, vs), q, pre, window), before)
+
+
+def _drafts(case, pre, nq):
+    """The fresh fp16 K / V of every row's drafts, [B, S, Hkv, D] (the tokens
+    the cache holds quantized at positions prefix .. prefix + S - 1)."""
+    starts = np.concatenate([[0], np.cumsum(case.lens)])
+    idx = np.stack([starts[b] + pre[b] + np.arange(nq) for b in range(case.batch)])
+    return case.k[idx], case.v[idx]
+
+
+@pytest.mark.parametrize("k8v3,hq,hkv,d,bs,prefix,nq,window", [
+    (False, 8, 2, 128, 16, [1000, 37, 300], 6, 300),
+    (False, 16, 16, 64, 4, [90, 50], 5, 33),
+    (False, 8, 2, 256, 256, [777, 64], 40, 100),
+    (True, 8, 2, 128, 16, [1000, 130], 9, 129),
+    (True, 4, 2, 256, 16, [700, 260], 4, 70),
+])
+def test_window_verify_with_fresh_drafts(k8v3, hq, hkv, d, bs, prefix, nq, window):
+    """The reference's window verify attends the prefix window read back from
+    the cache plus the drafts' fresh fp16 K / V (gqa_attention.py:298-313):
+    against the oracle in that mode, with the drafts passed as a
+    [B, Hkv, S, D] -> [B, S, Hkv, D] transpose view; and not the
+    cache-roundtripped result."""
+    case, cache, q, pre = _verify_case(700 + d + window, len(prefix), hq, hkv, d, bs, prefix, nq, k8v3)
+    kd, vd = _drafts(case, pre, nq)
+    c = [_t(x) for x in cache]
+    kw = dict(max_context_len=int(case.block_table.shape[1] * case.block_size), scale=case.scale, window=window,
+              k_draft=_t(kd.transpose(0, 2, 1, 3)).transpose(1, 2), v_draft=_t(vd.transpose(0, 2, 1, 3)).transpose(1, 2))
+    bt, pl = _t(case.block_table), _t(pre.astype(np.int32))
+    if k8v3:
+        out = ops.attn_paged_verify_k8v3(_t(q), *c, _t(CODEBOOK), bt, pl, case.block_size, **kw)
+    else:
+        out = ops.attn_paged_verify(_t(q), *c, bt, pl, case.block_size, **kw)
+    got = out.float().cpu().numpy()
+    layer = O.LayerCache(cache[0], cache[1], v_packed=cache[2], v_norm=cache[3], v_codebook=CODEBOOK) if k8v3 \
+        else O.LayerCache(*cache)
+    ref = O.paged_verify(q, layer, case.block_table, pre, case.scale, window=window, fresh_drafts=(kd, vd))
+    _close(got, ref, f"verify window {window} with fresh drafts")
+    assert not np.array_equal(got, _verify(case, cache, q, pre, window, k8v3))
+
+
+def test_fresh_drafts_need_a_window():
+    case, cache, q, pre = _verify_case(711, 1, 8, 2, 128, 16, [100], 4)
+    kd, vd = _drafts(case, pre, 4)
+    with pytest.raises(ValueError):
+        ops.attn_paged_verify(_t(q), *[_t(x) for x in cache], _t(case.block_table), _t(pre.astype(np.int32)),
+                              case.block_size, max_context_len=128, scale=0.1, k_draft=_t(kd), v_draft=_t(vd))

@@ -340,9 +340,10 @@ def _torch_decode(q, layer, bt, lens, scale):
     return out.numpy()
 
 
-@pytest.mark.parametrize("k8v3", [False, True])
-def test_paged_decode_matches_independent_torch(k8v3):
-    d = 128 if k8v3 else 64
+@pytest.mark.parametrize("k8v3,d", [(False, 64), (True, 128), (True, 256)])
+def test_paged_decode_matches_independent_torch(k8v3, d):
+    """Against a per-position torch walk; K8V3 at head_dim 256 pins the
+    norm of each 128-element block to its own half of the row."""
     layer, bt, lens, rng = _case(11, d=d, lens=(13, 1, 40, 0), k8v3=k8v3)
     q = rng.standard_normal((4, 6, d)).astype(np.float16)
     got = O.paged_decode(q, layer, bt, lens, 0.125)
@@ -490,6 +491,39 @@ def test_paged_verify_window():
     assert np.array_equal(O.paged_verify(q, layer, bt, pl, 0.125, window=w), before)
 
 
+def test_paged_verify_window_fresh_drafts_is_the_references_dense_formulation():
+    """The reference's window verify (gqa_attention.py:298-313): read the
+    prefix window back dense, concatenate the fresh fp16 drafts, run causal
+    attention with the S queries at the end.  The oracle's fresh-draft mode
+    equals that formulation restated with read_dense and the dense oracle (an
+    independent path: keys in fp16 as the reference's reader returns them, so
+    the match is to fp16 rounding of the prefix keys), and differs from
+    attending the cache-roundtripped drafts."""
+    rng = np.random.default_rng(14)
+    hq, hkv, d, bs, p, s, w = 4, 2, 64, 16, 70, 5, 24
+    n = p + s
+    k = (rng.standard_normal((n, hkv, d)) * 2).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    nb = (n + bs - 1) // bs
+    kc, ks = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    vc, vs = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    bt = np.arange(nb, dtype=np.int32)[None][:, ::-1].copy()
+    slots = (bt[0, np.arange(n) // bs] * bs + np.arange(n) % bs).astype(np.int32)
+    O.quantize_kv_write_paged(k, v, kc, ks, vc, vs, slots)
+    layer = O.LayerCache(kc, ks, vc, vs)
+    q = rng.standard_normal((1, hq, s, d)).astype(np.float16)
+    kd, vd = k[None, p:], v[None, p:]  # [1, S, Hkv, D]
+    got = O.paged_verify(q, layer, bt, np.array([p]), 0.125, window=w, fresh_drafts=(kd, vd))
+    kb, vb = O.read_dense(layer, bt[0], p, window=w)  # [1, Hkv, w, D] fp16
+    k_all = np.concatenate([kb[0].transpose(1, 0, 2), k[p:]], axis=0)  # [w + S, Hkv, D]
+    v_all = np.concatenate([vb[0].transpose(1, 0, 2), v[p:]], axis=0)
+    ref = O.dense_varlen_attention(q[0].transpose(1, 0, 2), k_all, v_all, np.array([0, s]), np.array([0, w + s]),
+                                   0.125, causal=True)
+    assert np.abs(got[0].transpose(1, 0, 2) - ref).max() < 5e-3
+    roundtrip = O.paged_verify(q, layer, bt, np.array([p]), 0.125, window=w)
+    assert np.abs(roundtrip - got).max() > 1e-4
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_dense_varlen_attention_matches_torch_sdpa(causal):
     """The dense prefill oracle against torch's float64 scaled_dot_product_attention
@@ -513,8 +547,10 @@ def test_dense_varlen_attention_matches_torch_sdpa(causal):
 
 
 def test_dense_varlen_attention_window_left_matches_torch_sdpa():
-    """window_left: query i (bottom-right aligned) sees keys i - W .. i, as a
-    torch band mask built with tril / triu."""
+    """window_left: query i (bottom-right aligned) sees its last W keys,
+    i - W + 1 .. i, as a torch band mask built with tril / triu; W = 1 is the
+    diagonal alone, and the decode-side window of the same layer (the last
+    W keys of the row, paged_decode(window=W)) sees the same keys."""
     rng = np.random.default_rng(22)
     hq, hkv, d, w = 4, 2, 16, 5
     qlens, klens = [12, 3], [12, 20]
@@ -529,8 +565,34 @@ def test_dense_varlen_attention_window_left_matches_torch_sdpa():
         kb = torch.from_numpy(k[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
         vb = torch.from_numpy(v[cu_k[b]:cu_k[b + 1]]).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
         ones = torch.ones(nq, nk, dtype=torch.bool)
-        mask = ones.tril(diagonal=nk - nq) & ones.triu(diagonal=nk - nq - w)
+        mask = ones.tril(diagonal=nk - nq) & ones.triu(diagonal=nk - nq - w + 1)
         ref = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask, scale=0.25)
         assert np.allclose(got[cu_q[b]:cu_q[b + 1]], ref.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
     full = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True)
     assert np.array_equal(O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True, window_left=100), full)
+    one = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True, window_left=1)
+    diag = np.repeat(v[cu_k[1] - qlens[0]:cu_k[1]], hq // hkv, axis=1)  # sequence 0: nk == nq, each its own V
+    assert np.allclose(one[:qlens[0]], diag, rtol=1e-12, atol=1e-12)
+    with pytest.raises(ValueError):
+        O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.25, True, window_left=0)
+
+
+def test_prefill_band_and_decode_window_see_the_same_keys():
+    """The last query of a prefill with window_left W attends exactly what the
+    decode-side window of W keys attends at that position."""
+    rng = np.random.default_rng(23)
+    hq, hkv, d, bs, n, w = 4, 2, 32, 8, 40, 9
+    k = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    q = rng.standard_normal((n, hq, d)).astype(np.float16)
+    nb = n // bs
+    kc, ks = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    vc, vs = np.zeros((nb, hkv, bs, d), np.int8), np.ones((nb, hkv, bs), np.float32)
+    bt = np.arange(nb, dtype=np.int32)[None]
+    O.quantize_kv_write_paged(k, v, kc, ks, vc, vs, np.arange(n, dtype=np.int32))
+    layer = O.LayerCache(kc, ks, vc, vs)
+    kx, vx = O.exact_kv(layer, bt[0], n)  # the cache's exact values, [Hkv, n, D]
+    band = O.dense_varlen_attention(q, kx.transpose(1, 0, 2), vx.transpose(1, 0, 2), np.array([0, n]),
+                                    np.array([0, n]), 0.2, True, window_left=w)
+    dec = O.paged_decode(q[None, -1], layer, bt, np.array([n]), 0.2, window=w)
+    assert np.allclose(band[-1], dec[0], rtol=1e-12, atol=1e-12)
