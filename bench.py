@@ -24,6 +24,7 @@ Prints one JSON line.  `value` = algorithmic bytes of one step / step time.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -193,6 +194,103 @@ def time_decode_kernel(w, reps: int, fused: bool) -> dict:
     torch.cuda.synchronize()
     launches = max(n.value, 1)
     return {"decode_s": dk.value * 1e-3 / launches, "launches": n.value}
+
+
+def decode_tiles(lens: np.ndarray, bt_np: np.ndarray, slices_per_head: int) -> np.ndarray:
+    """First storage row of every 32-token tile the decode step reads, one
+    list per KV head (rows concatenated), each cut into `slices_per_head`
+    equal slices and the slices dealt as the decode kernel deals its
+    workgroups (workgroup j * HKV + h takes slice j of head h)."""
+    per_head = []
+    for h in range(HKV):
+        rows = []
+        for b in range(BATCH):
+            t0 = np.arange(0, int(lens[b]), 32)
+            rows.append((bt_np[b, t0 // BS].astype(np.int64) * HKV + h) * BS + t0 % BS)
+        per_head.append(np.concatenate(rows))
+    out = []
+    for j in range(slices_per_head):
+        for h in range(HKV):
+            n = per_head[h].size
+            out.append(per_head[h][n * j // slices_per_head: n * (j + 1) // slices_per_head])
+    return np.concatenate(out).astype(np.int32)
+
+
+def _time_graph(fn, steps: int, warmup: int) -> float:
+    """Seconds per replay of a graph holding `fn`'s launches, from HIP events
+    around `steps` back-to-back replays."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / max(steps, 1)
+
+
+def read_ceiling(w, steps: int) -> dict:
+    """What a read-only kernel reaches on the decode step's bytes, with the
+    step's shape: 36 launches, one per layer's storage, in a graph.
+      tiles : exactly the K/V rows and scales of the decode's 32-token
+              tiles (s8kv_probe_read_tiles), for several grid sizes;
+      linear: one layer's whole int8 K tensor per launch, contiguous
+              (s8kv_probe_read_linear), for several grid sizes.
+    GB/s = the probe's own bytes per launch / its average launch time."""
+    import torch
+
+    from superl8_serve_amd import _lib
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    nrows = POOL_BLOCKS * HKV * BS
+    sink = torch.zeros(cus * 16, dtype=torch.int32, device="cuda")
+    res = {"tiles": {}, "linear": {}}
+    for per_cu in (2, 3, 4, 6):
+        nwg = cus * per_cu
+        tiles = torch.from_numpy(decode_tiles(w["lens"], w["bt_np"], nwg // HKV)).cuda()
+        nt = int(tiles.numel())
+
+        def probe(tiles=tiles, nt=nt, nwg=nwg):
+            for layer in range(NUM_LAYERS):
+                _lib.check(lib.s8kv_probe_read_tiles(
+                    w["kc"][layer].data_ptr(), w["ks"][layer].data_ptr(), w["vc"][layer].data_ptr(),
+                    w["vs"][layer].data_ptr(), nrows, D, tiles.data_ptr(), nt, nwg, sink.data_ptr(), stream()),
+                    "s8kv_probe_read_tiles")
+
+        sec = _time_graph(probe, steps, 2) / NUM_LAYERS
+        nbytes = nt * 32 * (2 * D + 8)
+        res["tiles"][f"{per_cu}/CU"] = {"gbps": round(nbytes / sec / 1e9, 1), "launch_us": round(sec * 1e6, 2),
+                                        "bytes": nbytes}
+    for per_cu in (4, 8):
+        nwg = cus * per_cu
+        nbytes = w["kc"][0].numel()
+
+        def probe(nwg=nwg, nbytes=nbytes):
+            for layer in range(NUM_LAYERS):
+                _lib.check(lib.s8kv_probe_read_linear(w["kc"][layer].data_ptr(), nbytes, nwg, sink.data_ptr(),
+                                                      stream()), "s8kv_probe_read_linear")
+
+        sec = _time_graph(probe, steps, 2) / NUM_LAYERS
+        res["linear"][f"{per_cu}/CU"] = {"gbps": round(nbytes / sec / 1e9, 1), "launch_us": round(sec * 1e6, 2),
+                                         "bytes": nbytes}
+    res["tiles_best_gbps"] = max(v["gbps"] for v in res["tiles"].values())
+    res["linear_best_gbps"] = max(v["gbps"] for v in res["linear"].values())
+    return res
 
 
 def cpu_baseline(lens: np.ndarray, bt_np: np.ndarray, layers: int) -> dict:
@@ -783,6 +881,8 @@ def main():
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
     ap.add_argument("--kernel-reps", type=int, default=3,
                     help="eager event-timed decode passes over the 36 layers (0 = skip, one-launch step only)")
+    ap.add_argument("--ceiling-steps", type=int, default=5,
+                    help="graph replays per read-ceiling probe (0 = skip the read-ceiling leg)")
     ap.add_argument("--separate-append", action="store_true",
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
@@ -915,6 +1015,11 @@ def main():
             "eager_avg_launch_us": round(kt["decode_s"] * 1e6, 2) if kt["decode_s"] else None,
         },
     }
+    if args.ceiling_steps > 0:
+        rc = read_ceiling(w, args.ceiling_steps)
+        rc["decode_frac_of_tiles_best"] = round(achieved / rc["tiles_best_gbps"], 4)
+        rc["decode_frac_of_linear_best"] = round(achieved / rc["linear_best_gbps"], 4)
+        result["read_ceiling"] = rc
     if args.cpu_layers > 0:
         result["cpu_baseline"] = cpu_baseline(w["lens"], w["bt_np"], args.cpu_layers)
     print(json.dumps(result))

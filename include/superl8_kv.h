@@ -422,6 +422,24 @@ int s8kv_timing_begin(void);
 int s8kv_timing_end(int* launches, double* decode_ms, double* merge_ms);
 
 /*
+ * Read-ceiling probes (diagnostics; no counterpart in the reference).  They
+ * read without computing, to bound what a kernel reading the same bytes
+ * with the same shape can reach; each workgroup writes one checksum word to
+ * sink[num_workgroups] so no load is dropped.
+ * s8kv_probe_read_tiles: for each entry of tiles (device int32
+ * [num_tiles], the first storage row of a 32-token tile inside one block
+ * and head, as the decode kernel reads them), the tile's 32 K rows and 32 V
+ * rows (int8, head_dim 128) and their fp32 scales; 4-wave workgroups, each
+ * taking an equal contiguous share of the list, one tile per wave with the
+ * next tile's loads in flight.  num_rows: storage rows of the cache tensors.
+ * s8kv_probe_read_linear: `bytes` contiguous bytes (16-byte aligned).
+ */
+int s8kv_probe_read_tiles(const int8_t* k_cache, const float* k_scale, const int8_t* v_cache, const float* v_scale,
+                          int64_t num_rows, int head_dim, const int32_t* tiles, int num_tiles, int num_workgroups,
+                          uint32_t* sink, void* stream);
+int s8kv_probe_read_linear(const void* buffer, int64_t bytes, int num_workgroups, uint32_t* sink, void* stream);
+
+/*
  * Copy whole physical blocks across every layer of up to 8 cache tensors
  * (copy-on-write of a shared prefix block; compaction of the pool).
  * The reference has no block copy: prefix sharing is refcounted

@@ -139,6 +139,10 @@ SIGNATURES: dict[str, tuple] = {
     ]),
     "s8kv_timing_begin": (_i32, []),
     "s8kv_timing_end": (_i32, [ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "s8kv_probe_read_tiles": (_i32, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _i32, _i32, _c_void_p, _c_void_p,
+    ]),
+    "s8kv_probe_read_linear": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p]),
     "s8kv_copy_blocks": (_i32, [
         _i32, ctypes.POINTER(_c_void_p), ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i32, _i64,
         _c_void_p, _c_void_p, _i32, _c_void_p,

@@ -988,7 +988,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       }
     }
     __syncthreads();
-    store_prefetched_bt();  // bt_lds is free: every wave left its tile loop
+    // bt_lds is free: every wave left its tile loop (the last segment stages
+    // nothing, so the workgroup's end does not wait for the prefetch's loads)
+    if (nL != 0) store_prefetched_bt();
     const int64_t slot = ((int64_t)h * a.slots + (j + b)) * G;  // (row, slice) -> unique slot j + b
     for (int i = tid; i < G * D; i += 64 * kDecWaves) {
       const int cc = i / D, d = i - cc * D;
@@ -1151,6 +1153,10 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   a.wg_per_head = plan_wg_per_head(a.num_kv_heads, resident);
   a.ghost = kGhostTokens;
   a.slot_classes = resident;
+  if (const char* env = getenv("S8KV_DECODE_CLASSES")) {  // residency classes the slices are weighted over
+    const int v = atoi(env);
+    a.slot_classes = v < 1 ? 1 : (v > kMaxResidentPerCU ? kMaxResidentPerCU : v);
+  }
   a.slot_skew = kSlotSkewPermille;
   if (const char* env = getenv("S8KV_DECODE_SLOT_SKEW")) a.slot_skew = atoi(env);
   if (const char* env = getenv("S8KV_DECODE_GHOST")) {

@@ -160,3 +160,47 @@ def test_workspace_alignment_and_limits():
     rc, _ = _decode_abi(case, cache_t, q3, ws, max_context_len=1 << 28)
     assert rc == ERR_UNSUPPORTED
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("wg,ghost", SLICINGS)
+def test_graph_replays_with_changing_lengths(wg, ghost, monkeypatch):
+    """Replays of one captured launch (one tag) with the context lengths
+    rewritten between them, as a serving loop replays its decode graph: the
+    stream's slicing changes from replay to replay (down to an empty stream
+    and back).  Every replay equals an eager call on the same lengths bit for
+    bit and stays within tolerance of the oracle."""
+    _set_slicing(monkeypatch, wg, ghost)
+    case = make_case(74, 6, 8, 2, 128, 16, [1500] * 6)
+    cache = oracle_fill_int8(case)
+    cache_t = tuple(_t(x) for x in cache)
+    bt = _t(case.block_table)
+    cl = _t(np.asarray(case.lens, dtype=np.int32))
+    q_in = _t(case.q, torch.float16)[:, :, None, :]
+
+    def run(lens_t):
+        return ops.attn_paged_decode_cached(q_in, *cache_t, bt, lens_t, case.block_size, max_context_len=1500,
+                                            scale=case.scale)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(cl)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_g = run(cl)
+    schedule = [[1500] * 6, [700, 33, 0, 1500, 64, 5], [1, 0, 2, 0, 0, 3], [1499, 1, 900, 1200, 32, 1500],
+                [0] * 6, [257, 640, 1023, 96, 1500, 31]]
+    for r, lens in enumerate(schedule):
+        lens_np = np.asarray(lens, dtype=np.int32)
+        cl.copy_(_t(lens_np))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out_g.clone()
+        eager = run(_t(lens_np))
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {r} (lengths {lens}) differs from the eager call"
+        ref = O.paged_decode(case.q, O.LayerCache(*cache), case.block_table, lens_np.astype(np.int64), case.scale)
+        mx, rel = O.attention_errors(got[:, :, 0, :].float().cpu().numpy(), ref)
+        assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"replay {r}: max err {mx:.3e}, rel rms {rel:.3e}"
