@@ -2,21 +2,26 @@
 // draft query sees the prefix plus its ancestors in the draft tree) and
 // chunked prefill / chain verify (query s sees the prefix plus drafts 0..s).
 //
-// Layout of the work: a workgroup of 4 waves owns 64 query rows of one
+// Layout of the work: a workgroup of 4 waves owns 64 * RG query rows of one
 // (sequence, KV head) pair -- row r is query position r / G of q head
 // h*G + r % G -- and streams the pair's keys in 32-key tiles.  Each tile's K
 // and V rows are loaded once per workgroup, converted int8 -> fp16 (exact) on
 // the way into LDS (double-buffered), and shared by the 4 waves (K8V3: V's
 // 3-bit codes become the fp16 codebook entries, as in the decode kernel); a
-// wave owns 16 query rows, the 16 columns of its MFMA tiles:
+// wave owns RG groups of 16 query rows (RG = 2 for head_dim 64, else 1),
+// each group the 16 columns of its own MFMA tiles, and every K and V operand a
+// wave reads from LDS feeds the MFMAs of all its groups:
 //   QK  : S^T[key][row] on MFMA 16x16x32 f16, A = K rows from LDS, B = the
 //         rotated, pre-scaled q split into fp16 hi + lo (two MFMAs).
 //   mask: keys below the prefix are visible to every row; draft key i is
 //         visible to row position s if i <= s (chain) or bit i of the row's
 //         tree mask is set (tree).
-//   softmax: online, log2 domain, lazy max (as the decode kernel).
+//   softmax: online, log2 domain, lazy max (as the decode kernel): a score
+//         enters as y = s * k_scale - m in one FMA; a tile whose y exceeds
+//         the slack recomputes the running max from the products.
 //   PV  : O^T[dim][row] on MFMA, A = V^T via ds_read_b64_tr_b16 from LDS,
-//         B = P * v_scale (K8V3: P * the key's block norm) as fp16 hi + lo.
+//         B = P * v_scale (K8V3: P * the key's block norm) as fp16 hi + lo
+//         (hi: the fp32 weight cut to fp16 precision, lo: the exact rest).
 // Rows past a sequence's query count are written as zeros.
 #include <type_traits>
 
@@ -29,7 +34,6 @@ namespace verify {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;
-constexpr int kRowsPerWg = 16 * kWaves;
 constexpr int kSubKeys = 2048;                 // block ids staged in LDS per 2048 keys
 constexpr int kMaxSubBlocks = kSubKeys / 4 + 2;  // block_size >= 4
 constexpr float kNegInf = -__builtin_inff();
@@ -41,6 +45,8 @@ constexpr float kMaxInit = -1.0e30f;
 
 template <int D, bool K8V3>
 struct Cfg {
+  static constexpr int RG = D <= 64 ? 2 : 1;         // 16-row groups per wave (as registers allow)
+  static constexpr int ROWS = 16 * RG * kWaves;      // query rows per workgroup
   static constexpr int KCH = D / 4;      // dims per lane per key row (MFMA A / B chunk of the lane group)
   static constexpr int NQK = D / 32;     // QK MFMAs per 16-key subtile
   static constexpr int NPV = D / 16;     // PV MFMAs per tile
@@ -86,7 +92,7 @@ struct VerifyArgs {
   const int64_t* tree_mask;   // nullable: chain; else [batch][max_queries] ancestor bits
   int bs_log2;
   int max_context_len;
-  int n_qblocks;              // 64-row query blocks per (sequence, KV head)
+  int n_qblocks;              // query blocks (rows_per_wg rows each) per (sequence, KV head)
   int window;                 // verify_kernel<.., WIN>: only the last `window` prefix keys are visible
   // WIN, optional: the drafts' fresh K (rotated, fp32) and V (fp16),
   // attended in place of their cache rows (draft i of row b, head h at
@@ -151,8 +157,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
     prefix = max(0, a.prefix_lens[b]);
   }
-  const int row0 = qb * kRowsPerWg;                 // first row of the workgroup
-  const int pos_hi = min(nq, (row0 + kRowsPerWg + G - 1) / G);  // positions of this block that exist
+  constexpr int RG = C::RG;
+  const int row0 = qb * C::ROWS;                    // first row of the workgroup
+  const int pos_hi = min(nq, (row0 + C::ROWS + G - 1) / G);  // positions of this block that exist
   const bool tree = a.tree_mask != nullptr;
   // keys any row of this block can see
   int kv_end = prefix + (tree ? nq : pos_hi);
@@ -164,27 +171,34 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   // block's loop starts at its first position's bound and keys from its last
   // position's bound on are visible to every row)
   const int lo_key = WIN ? max(0, prefix + (DENSE ? row0 / G : 0) - a.window) : 0;
-  const int lo_all = WIN && DENSE ? prefix + min(nq - 1, (row0 + kRowsPerWg - 1) / G) - a.window : lo_key;
+  const int lo_all = WIN && DENSE ? prefix + min(nq - 1, (row0 + C::ROWS - 1) / G) - a.window : lo_key;
   // keys below vis_all are visible to every row of the block: the prefix, and
   // for a chain / causal block also the drafts up to its first position
   const int vis_all = tree ? prefix : prefix + row0 / G + 1;
 
-  // this lane's column: query row r -> (position, q head)
-  const int r = row0 + wave * 16 + c;
-  const int pos = r / G;
-  const int head = h * G + (r - pos * G);
-  const bool row_live = pos < nq;
-  const uint64_t tmask = (tree && row_live) ? (uint64_t)a.tree_mask[(int64_t)b * a.max_queries + pos] : 0ull;
+  // this lane's column in each of its row groups: query row r -> (position, q head)
+  int pos[RG], head[RG];
+  bool row_live[RG];
+  uint64_t tmask[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    const int r = row0 + (rg * kWaves + wave) * 16 + c;
+    pos[rg] = r / G;
+    head[rg] = h * G + (r - pos[rg] * G);
+    row_live[rg] = pos[rg] < nq;
+    tmask[rg] = (tree && row_live[rg]) ? (uint64_t)a.tree_mask[(int64_t)b * a.max_queries + pos[rg]] : 0ull;
+  }
 
   // ---- q: rotate (FWHT), pre-scale, split into fp16 hi + lo ----
-  half8_t qhi[C::NQK], qlo[C::NQK];
-  {
+  half8_t qhi[RG][C::NQK], qlo[RG][C::NQK];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
     float x[C::KCH];
     const int64_t qrow = DENSE ? (int64_t)q0 * a.q_stride_s : (int64_t)b * a.q_stride_b;
-    const _Float16* qp = a.q + qrow + (int64_t)head * a.q_stride_h + (int64_t)(row_live ? pos : 0) * a.q_stride_s +
-                         g * C::KCH;
+    const _Float16* qp = a.q + qrow + (int64_t)head[rg] * a.q_stride_h +
+                         (int64_t)(row_live[rg] ? pos[rg] : 0) * a.q_stride_s + g * C::KCH;
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) x[i] = row_live ? (float)qp[i] : 0.0f;
+    for (int i = 0; i < C::KCH; ++i) x[i] = row_live[rg] ? (float)qp[i] : 0.0f;
     // dense inputs: K is not rotated, so neither is q
 #pragma unroll
     for (int hs = 1; hs < (DENSE ? 1 : C::KCH); hs <<= 1) {
@@ -211,17 +225,21 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         // fused fp16(x*s) for the lo term can differ from fp16(val) by one ulp)
         const float val = materialize(x[8 * m + e] * a.qscale);
         const _Float16 qh = (_Float16)val;
-        qhi[m][e] = qh;
-        qlo[m][e] = (_Float16)(val - (float)qh);
+        qhi[rg][m][e] = qh;
+        qlo[rg][m][e] = (_Float16)(val - (float)qh);
       }
     }
   }
 
-  float m_run = kMaxInit;
-  float l_run = 0.0f;
-  float4_t acc[C::NPV];
+  float m_run[RG], l_run[RG];
+  float4_t acc[RG][C::NPV];
 #pragma unroll
-  for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int rg = 0; rg < RG; ++rg) {
+    m_run[rg] = kMaxInit;
+    l_run[rg] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < C::NPV; ++n) acc[rg][n] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
@@ -424,26 +442,36 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       const char* kb = smem + buf * C::BUF;
       const char* vb = kb + C::KBYTES;
       const float* sb = reinterpret_cast<const float*>(vb + C::VBYTES);
-      float4_t sc[2];
+      // QK: each K operand read from LDS feeds the MFMAs of every row group
+      float4_t sc[RG][2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        float4_t cacc = float4_t{0.f, 0.f, 0.f, 0.f};
+        float4_t cacc[RG];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) cacc[rg] = float4_t{0.f, 0.f, 0.f, 0.f};
         const char* krow = kb + (16 * s + c) * C::KROW + g * C::KCH * 2;
 #pragma unroll
         for (int m = 0; m < C::NQK; ++m) {
           const half8_t ka = *reinterpret_cast<const half8_t*>(krow + 16 * m);
-          cacc = mfma16x16x32(ka, qhi[m], cacc);
-          cacc = mfma16x16x32(ka, qlo[m], cacc);
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            cacc[rg] = mfma16x16x32(ka, qhi[rg][m], cacc[rg]);
+            cacc[rg] = mfma16x16x32(ka, qlo[rg][m], cacc[rg]);
+          }
         }
         if constexpr (WIN && !DENSE) {  // fresh draft keys: K = hi + lo (masked or not)
           if (fresh_tile(base)) {
             const char* lrow = smem + C::KLO_OFF + buf * C::KBYTES + (16 * s + c) * C::KROW + g * C::KCH * 2;
 #pragma unroll
-            for (int m = 0; m < C::NQK; ++m)
-              cacc = mfma16x16x32(*reinterpret_cast<const half8_t*>(lrow + 16 * m), qhi[m], cacc);
+            for (int m = 0; m < C::NQK; ++m) {
+              const half8_t kl = *reinterpret_cast<const half8_t*>(lrow + 16 * m);
+#pragma unroll
+              for (int rg = 0; rg < RG; ++rg) cacc[rg] = mfma16x16x32(kl, qhi[rg][m], cacc[rg]);
+            }
           }
         }
-        sc[s] = cacc;
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) sc[rg][s] = cacc[rg];
       }
       float4_t ksc[2], vsc[2], vsc1[2];  // vsc1: K8V3 head_dim 256, the second block's norms
 #pragma unroll
@@ -452,61 +480,110 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         vsc[s] = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * s + 4 * g);
         if constexpr (C::NB == 2) vsc1[s] = *reinterpret_cast<const float4_t*>(sb + 2 * kTile + 16 * s + 4 * g);
       }
-      float pr[2][4];
-      bool vm[2][4];  // MASKED: key visible to this lane's row
-      float mt = kNegInf;
+      half8_t pbh[RG], pbl[RG], pbh1[RG], pbl1[RG];  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+      for (int rg = 0; rg < RG; ++rg) {
+        // key kk of the tile visible to this lane's row of group rg (MASKED only)
+        auto visible = [&](int s, int i) -> bool {
+          const int kk = base + 16 * s + 4 * g + i;
+          const int di = kk - prefix;  // draft index when >= 0
+          bool vis = kk < kv_end && row_live[rg] && (!WIN || kk >= (DENSE ? prefix + pos[rg] - a.window : lo_key));
+          if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask[rg] >> di) & 1ull)) : di <= pos[rg]);
+          return vis;
+        };
+        float y[2][4];  // score relative to the running max, log2 domain
+        float my = kNegInf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = sc[s][i] * ksc[s][i];
-          vm[s][i] = true;
-          if constexpr (MASKED) {
-            const int kk = base + 16 * s + 4 * g + i;
-            const int di = kk - prefix;  // draft index when >= 0
-            bool vis = kk < kv_end && row_live && (!WIN || kk >= (DENSE ? prefix + pos - a.window : lo_key));
-            if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask >> di) & 1ull)) : di <= pos);
-            x = vis ? x : kNegInf;
-            vm[s][i] = vis;
-          }
-          pr[s][i] = x;
-          mt = fmaxf(mt, x);
-        }
-      }
-      mt = max_x16(mt);
-      mt = max_x32(mt);
-      if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
+        for (int s = 0; s < 2; ++s) {
 #pragma unroll
-        for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
-        m_run = m_new;
-      }
-      half8_t pbh, pbl, pbh1, pbl1;  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float x = pr[s][i];
-          const float e = __builtin_amdgcn_exp2f(x - m_run);
-          l_run += e;
-          // masked keys: e = 0, but their scale (past the visible keys, or
-          // below a window) may be any value, inf and NaN included
-          float w = materialize(e * vsc[s][i]);  // one value for hi and lo
-          if constexpr (MASKED) w = vm[s][i] ? w : 0.0f;
-          const _Float16 wh = (_Float16)w;
-          pbh[4 * s + i] = wh;
-          pbl[4 * s + i] = (_Float16)(w - (float)wh);
-          if constexpr (C::NB == 2) {
-            float w1 = materialize(e * vsc1[s][i]);
-            if constexpr (MASKED) w1 = vm[s][i] ? w1 : 0.0f;
-            const _Float16 wh1 = (_Float16)w1;
-            pbh1[4 * s + i] = wh1;
-            pbl1[4 * s + i] = (_Float16)(w1 - (float)wh1);
+          for (int i = 0; i < 4; ++i) {
+            float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_run[rg]);
+            if constexpr (MASKED) v = visible(s, i) ? v : kNegInf;
+            y[s][i] = v;
+            my = fmaxf(my, v);
           }
         }
+        my = max_x16(my);
+        my = max_x32(my);
+        if (__builtin_amdgcn_ballot_w64(my > kMaxSlack) != 0) {
+          // raise the running max to the tile's (from the products, exactly),
+          // rescale, and take the scores relative to the new max
+          float mt = kNegInf;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float x = sc[rg][s][i] * ksc[s][i];
+              if constexpr (MASKED) x = visible(s, i) ? x : kNegInf;
+              mt = fmaxf(mt, x);
+            }
+          }
+          mt = max_x16(mt);
+          mt = max_x32(mt);
+          const float m_new = fmaxf(m_run[rg], mt);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
+          l_run[rg] *= alpha;
+#pragma unroll
+          for (int n = 0; n < C::NPV; ++n) acc[rg][n] *= alpha;
+          m_run[rg] = m_new;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_new);
+              if constexpr (MASKED) v = visible(s, i) ? v : kNegInf;
+              y[s][i] = v;
+            }
+          }
+        }
+        // weights p * (V scale | block norm) as fp16 hi + lo: hi keeps the
+        // weight's top 11 significant bits (exact in fp16 for weights in
+        // fp16's normal range), lo the exact fp32 rest
+        float wh[2][4], wl[2][4], wh1[2][4], wl1[2][4];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_amdgcn_exp2f(y[s][i]);  // 0 for masked keys
+            l_run[rg] += e;
+            // masked keys: e = 0, but their scale (past the visible keys, or
+            // below a window) may be any value, inf and NaN included
+            // (materialized: hi and lo must both come from this one fp32 value,
+            // not from a product the compiler contracts into the lo subtraction)
+            float w = materialize(e * vsc[s][i]);
+            if constexpr (MASKED) w = (y[s][i] != kNegInf) ? w : 0.0f;
+            wh[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & 0xFFFFE000u);
+            wl[s][i] = w - wh[s][i];
+            if constexpr (C::NB == 2) {
+              float w1 = materialize(e * vsc1[s][i]);
+              if constexpr (MASKED) w1 = (y[s][i] != kNegInf) ? w1 : 0.0f;
+              wh1[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w1) & 0xFFFFE000u);
+              wl1[s][i] = w1 - wh1[s][i];
+            }
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh[s][i], wh[s][i + 1]));
+            const half2_t l2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl[s][i], wl[s][i + 1]));
+            pbh[rg][4 * s + i] = h2[0];
+            pbh[rg][4 * s + i + 1] = h2[1];
+            pbl[rg][4 * s + i] = l2[0];
+            pbl[rg][4 * s + i + 1] = l2[1];
+            if constexpr (C::NB == 2) {
+              const half2_t h21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh1[s][i], wh1[s][i + 1]));
+              const half2_t l21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl1[s][i], wl1[s][i + 1]));
+              pbh1[rg][4 * s + i] = h21[0];
+              pbh1[rg][4 * s + i + 1] = h21[1];
+              pbl1[rg][4 * s + i] = l21[0];
+              pbl1[rg][4 * s + i + 1] = l21[1];
+            }
+          }
+        }
       }
+      // PV: each V^T operand read from LDS feeds the MFMAs of every row group
 #pragma unroll
       for (int n = 0; n < C::NPV; ++n) {
         const int r0 = 8 * g + ((lane >> 2) & 3);
@@ -517,8 +594,11 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
         const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
         const bool second = C::NB == 2 && 16 * n >= 128;  // dims 128..255 of a K8V3 head_dim-256 key
-        acc[n] = mfma16x16x32(va, second ? pbh1 : pbh, acc[n]);
-        acc[n] = mfma16x16x32(va, second ? pbl1 : pbl, acc[n]);
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+          acc[rg][n] = mfma16x16x32(va, second ? pbh1[rg] : pbh[rg], acc[rg][n]);
+          acc[rg][n] = mfma16x16x32(va, second ? pbl1[rg] : pbl[rg], acc[rg][n]);
+        }
       }
     };
 
@@ -555,25 +635,32 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     }
   }
 
-  // ---- normalize and write this wave's 16 rows ----
-  const float l_tot = sum_x32(sum_x16(l_run));
-  // (dense: only the sequence's own query tokens -- the next ones belong to the next sequence)
-  if ((DENSE ? row_live : pos < a.max_queries) && (r - pos * G) < G) {
-    const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    _Float16* op = DENSE ? a.out + (int64_t)(q0 + pos) * a.o_stride_t + (int64_t)head * a.o_stride_h
-                         : a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
+  // ---- normalize and write this wave's rows ----
 #pragma unroll
-    for (int n = 0; n < C::NPV; ++n) {
-      half4_t o;
+  for (int rg = 0; rg < RG; ++rg) {
+    const float l_tot = sum_x32(sum_x16(l_run[rg]));
+    // (dense: only the sequence's own query tokens -- the next ones belong to the next sequence)
+    if (DENSE ? row_live[rg] : pos[rg] < a.max_queries) {
+      const float inv = (row_live[rg] && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+      _Float16* op = DENSE ? a.out + (int64_t)(q0 + pos[rg]) * a.o_stride_t + (int64_t)head[rg] * a.o_stride_h
+                           : a.out + (((int64_t)b * a.num_q_heads + head[rg]) * a.max_queries + pos[rg]) * D;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(acc[n][rr] * inv);
-      *reinterpret_cast<half4_t*>(op + 16 * n + 4 * g) = o;
+      for (int n = 0; n < C::NPV; ++n) {
+        half4_t o;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(acc[rg][n][rr] * inv);
+        *reinterpret_cast<half4_t*>(op + 16 * n + 4 * g) = o;
+      }
     }
   }
 }
 
+// Query rows per workgroup at this head_dim (Cfg<D, *>::ROWS).
+static int rows_per_wg(int head_dim) { return 16 * kWaves * (head_dim <= 64 ? 2 : 1); }
+
 template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
 static int launch(VerifyArgs& a, hipStream_t stream) {
+  static_assert(Cfg<D, K8V3>::ROWS == 16 * kWaves * (D <= 64 ? 2 : 1), "rows_per_wg");
   using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
@@ -648,7 +735,8 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  a.n_qblocks = (a.group * max_queries + verify::kRowsPerWg - 1) / verify::kRowsPerWg;
+  const int rows_wg = verify::rows_per_wg(head_dim);
+  a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
   return S8KV_OK;
@@ -848,7 +936,8 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.max_queries = max_seqlen_q;
   a.max_context_len = max_seqlen_k;
   a.bs_log2 = 5;
-  a.n_qblocks = (a.group * max_seqlen_q + verify::kRowsPerWg - 1) / verify::kRowsPerWg;
+  const int rows_wg = verify::rows_per_wg(head_dim);
+  a.n_qblocks = (a.group * max_seqlen_q + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634);  // K is not rotated: no 1/sqrt(D)
   a.cu_q = cu_seqlens_q;
   a.cu_k = cu_seqlens_k;
