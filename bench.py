@@ -242,6 +242,16 @@ def _time_graph(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e-3 / max(steps, 1)
 
 
+def _spin_ahead() -> None:
+    """Keep the GPU ahead of the host for an eager timed loop: a ~0.1 s spin
+    kernel runs while the host enqueues the timed calls, so host launch
+    overhead never opens a gap between them (the start event, recorded
+    after the spin, is stamped when the spin ends)."""
+    import torch
+
+    torch.cuda._sleep(int(2e8))
+
+
 def read_ceiling(w, steps: int) -> dict:
     """What a read-only kernel reaches on the decode step's bytes, with the
     step's shape: 36 launches, one per layer's storage, in a graph.
@@ -291,6 +301,84 @@ def read_ceiling(w, steps: int) -> dict:
     res["tiles_best_gbps"] = max(v["gbps"] for v in res["tiles"].values())
     res["linear_best_gbps"] = max(v["gbps"] for v in res["linear"].values())
     return res
+
+
+TRACE_WORDS = 16  # per-workgroup record of the decode trace build
+
+
+def trace_decode(steps: int, warmup: int) -> dict:
+    """Per-launch breakdown of the one-launch decode step from the trace
+    build of the library (libsuperl8_kv_trace.so: the same kernels, the decode
+    kernel stamping the device's 100 MHz clock at fixed points of each
+    workgroup).  The 36-layer step is captured with the trace on (each layer's
+    launch writing its own slot), replayed, and the last replay's records are
+    summarised: phase times are medians over workgroups and launches, spreads
+    are per launch (then the median over launches), all in us from the
+    launch's first workgroup start."""
+    import ctypes
+
+    import torch
+
+    from superl8_serve_amd import _lib
+
+    lib = _lib.load()
+    fn = lib.s8kv_decode_trace_set
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]
+    w = build("cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stride = cus * 8 * TRACE_WORDS  # the largest grid the decode launches (8 workgroups per CU)
+    buf = torch.zeros(NUM_LAYERS * stride, dtype=torch.int64, device="cuda")
+    _lib.check(fn(buf.data_ptr(), stride, NUM_LAYERS), "s8kv_decode_trace_set")
+    step = make_step(w, True)
+    sec = _time_graph(step, steps, warmup)
+    _lib.check(fn(None, 0, 0), "s8kv_decode_trace_set")
+    rec = buf.view(NUM_LAYERS, cus * 8, TRACE_WORDS).cpu().numpy().view(np.uint64)
+    us = lambda x: x.astype(np.float64) * 0.01  # noqa: E731  (100 MHz ticks)
+    med = lambda x: float(np.median(x)) if len(x) else None  # noqa: E731
+    phases = {k: [] for k in ("lengths_staged", "first_segment_found", "first_q_and_blocks_loaded",
+                              "first_q_published", "first_full_tile_done")}
+    per_launch = {k: [] for k in ("span", "tiles_end_min", "tiles_end_median", "tiles_end_p90", "tiles_end_max",
+                                  "exit_median", "exit_p90", "exit_max", "balanced_tiles_end")}
+    tails = {"whole_row": [], "split_row": [], "split_row_combining": []}
+    starts, ends = [], []
+    for layer in range(NUM_LAYERS):
+        r = rec[layer]
+        r = r[(r[:, 9] & np.uint64(1)) == 1]
+        t0 = r[:, 0].min()
+        rel = lambda c: us(r[:, c] - t0)  # noqa: E731
+        starts.append(int(t0))
+        ends.append(int(r[:, 7].max()))
+        for i, k in enumerate(phases, start=1):
+            v = r[:, i]
+            phases[k].extend(us(v[v > 0] - r[v > 0, 0]))
+        te, ex = rel(6), rel(7)
+        per_launch["span"].append(us(r[:, 7].max() - t0))
+        for k, q in (("tiles_end_min", 0), ("tiles_end_median", 50), ("tiles_end_p90", 90), ("tiles_end_max", 100)):
+            per_launch[k].append(np.percentile(te, q))
+        for k, q in (("exit_median", 50), ("exit_p90", 90), ("exit_max", 100)):
+            per_launch[k].append(np.percentile(ex, q))
+        # finish time if every workgroup kept its measured token rate and
+        # the work were spread so that all tile loops end together
+        tok = (r[:, 8] & np.uint64(0xFFFFFFFF)).astype(np.float64)
+        start_tiles = rel(3)
+        rate = tok / np.maximum(te - start_tiles, 1e-3)
+        per_launch["balanced_tiles_end"].append(float((tok.sum() + (rate * start_tiles).sum()) / rate.sum()))
+        whole = (r[:, 9] >> np.uint64(8)) & np.uint64(1)
+        comb = (r[:, 9] >> np.uint64(9)) & np.uint64(1)
+        tails["whole_row"].extend(ex[whole == 1] - te[whole == 1])
+        tails["split_row"].extend(ex[(whole == 0) & (comb == 0)] - te[(whole == 0) & (comb == 0)])
+        tails["split_row_combining"].extend(ex[comb == 1] - te[comb == 1])
+    gaps = [us(np.uint64(starts[i + 1] - ends[i])) for i in range(NUM_LAYERS - 1)]
+    return {
+        "trace": "decode_kernel<128, int8, fused append>, Qwen3-8B batch-64 step, trace build",
+        "step_ms_trace_build": round(sec * 1e3, 4),
+        "workgroups_per_launch": int(((rec[0][:, 9] & np.uint64(1)) == 1).sum()),
+        "prologue_us_from_workgroup_start": {k: round(med(v), 2) for k, v in phases.items()},
+        "per_launch_us": {k: round(float(np.median(v)), 2) for k, v in per_launch.items()},
+        "tail_us_exit_minus_tiles_end": {k: round(med(v), 2) if len(v) else None for k, v in tails.items()},
+        "gap_between_launches_us": round(float(np.median(gaps)), 2),
+    }
 
 
 def cpu_baseline(lens: np.ndarray, bt_np: np.ndarray, layers: int) -> dict:
@@ -488,12 +576,14 @@ def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # attention alone
+    _spin_ahead()
     st.record()
     for i in range(steps * VERIFY_LAYERS):
         layer_ops(i % VERIFY_LAYERS, append=False)
     en.record()
     torch.cuda.synchronize()
     t_attn = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
+    _spin_ahead()
     st.record()
     for i in range(steps * VERIFY_LAYERS):
         layer_ops(i % VERIFY_LAYERS)
@@ -692,6 +782,7 @@ def run_append(steps: int, warmup: int, k8v3: bool = False) -> None:
         call()
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _spin_ahead()
     st.record()
     for _ in range(steps):
         call()
@@ -738,6 +829,7 @@ def run_prefill(steps: int, warmup: int) -> None:
         attend(i)
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _spin_ahead()
     st.record()
     for i in range(steps * 4):
         attend(i)
@@ -820,6 +912,7 @@ def run_window(steps: int, warmup: int) -> None:
         attend(i)
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _spin_ahead()
     st.record()
     for i in range(steps * WINDOW_LAYERS):
         attend(i)
@@ -859,6 +952,7 @@ def run_copy(steps: int) -> None:
     ops.copy_blocks(t, src, dst)
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _spin_ahead()
     st.record()
     for _ in range(steps):
         ops.copy_blocks(t, src, dst)
@@ -887,6 +981,9 @@ def main():
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0, help="only run a plain copy of this size")
+    ap.add_argument("--trace-decode", action="store_true",
+                    help="only print the per-launch breakdown of the decode step from the trace build "
+                         "(superl8_serve_amd/libsuperl8_kv_trace.so)")
     ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "window",
                                            "prefill", "copy", "append", "append_k8v3"],
                     default="decode",
@@ -909,6 +1006,12 @@ def main():
         sys.exit(1)
     from superl8_serve_amd import _lib
 
+    if args.trace_decode:
+        from superl8_serve_amd import build_ext
+
+        _lib.LIB_PATH = build_ext.TRACE_LIB_PATH
+        print(json.dumps(trace_decode(args.steps, args.warmup)))
+        return
     _lib.load()
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)

@@ -4,6 +4,11 @@ Every ``csrc/*.hip`` file is compiled for gfx950 with hipcc (in parallel) and
 linked into one shared library next to this file.  Packed-fp32 VALU ops are
 disabled (``-packed-fp32-ops``); fp16 packed math and MFMA are unaffected.
 
+A second library, ``libsuperl8_kv_trace.so``, is the same code with the
+decode kernel built with ``-DS8KV_DECODE_TRACE``: per-workgroup timestamps of
+each decode launch (a diagnostics build for ``bench.py --trace-decode``; the
+ops never load it).
+
 Usage: ``python -m superl8_serve_amd.build_ext`` or ``build()`` from Python.
 """
 
@@ -21,6 +26,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libsuperl8_kv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+TRACE_LIB_PATH = PKG_DIR / "libsuperl8_kv_trace.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -49,13 +55,17 @@ def _run(cmd: list[str]) -> None:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile all HIP sources and link ``libsuperl8_kv.so``.  Always rebuilds."""
+    """Compile all HIP sources and link ``libsuperl8_kv.so`` (and the decode
+    trace build ``libsuperl8_kv_trace.so``).  Always rebuilds."""
     hipcc = _hipcc()
     obj_dir = PKG_DIR / "_build"
     obj_dir.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     objs = [obj_dir / (s.stem + ".o") for s in sources]
     cmds = [[hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
+    decode_src = CSRC / "s8kv_decode.hip"
+    trace_obj = obj_dir / "s8kv_decode_trace.o"
+    cmds.append([hipcc, *HIPCC_FLAGS, "-DS8KV_DECODE_TRACE", "-c", str(decode_src), "-o", str(trace_obj)])
     workers = jobs or min(len(cmds), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=workers) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
@@ -65,6 +75,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB_PATH)
+    trace_objs = [trace_obj if o.stem == "s8kv_decode" else o for o in objs]
+    tmp = TRACE_LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, trace_objs)])
+    os.replace(tmp, TRACE_LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH

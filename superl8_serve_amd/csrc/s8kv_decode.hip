@@ -65,6 +65,48 @@
 
 namespace s8kv {
 
+// Diagnostics build only (libsuperl8_kv_trace.so, compiled with
+// -DS8KV_DECODE_TRACE): each workgroup stamps the device's constant 100 MHz
+// clock at fixed points of its run and writes one 16-word record at its end
+// (kTraceWords below); the product library compiles none of it.
+#ifdef S8KV_DECODE_TRACE
+enum TraceSlot {
+  kTrEntry = 0,      // workgroup start
+  kTrLens = 1,       // context lengths staged in LDS
+  kTrFound = 2,      // slice and first segment located
+  kTrStaged = 3,     // first segment's q and block ids loaded (block ids staged)
+  kTrQ = 4,          // first segment's rotated q published
+  kTrTile1 = 5,      // wave 0's first full tile done
+  kTrTilesEnd = 6,   // wave 0 left the last segment's tile loop
+  kTrExit = 7,       // workgroup end
+  kTrWork = 8,       // tokens processed | segments << 32
+  kTrFlags = 9,      // 1 | last segment whole row << 8 | last segment combined its row << 9
+};
+constexpr int kTraceWords = 16;
+#define S8KV_TRACE_STAMP(slot)                                                 \
+  do {                                                                         \
+    if (threadIdx.x == 0) trace_lds[slot] = __builtin_amdgcn_s_memrealtime();  \
+  } while (0)
+#define S8KV_TRACE_STAMP_ONCE(slot)                                                          \
+  do {                                                                                       \
+    if (threadIdx.x == 0 && trace_lds[slot] == 0) trace_lds[slot] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define S8KV_TRACE_SET(slot, value)                 \
+  do {                                              \
+    if (threadIdx.x == 0) trace_lds[slot] = (value); \
+  } while (0)
+#else
+#define S8KV_TRACE_STAMP(slot) \
+  do {                         \
+  } while (0)
+#define S8KV_TRACE_STAMP_ONCE(slot) \
+  do {                              \
+  } while (0)
+#define S8KV_TRACE_SET(slot, value) \
+  do {                              \
+  } while (0)
+#endif
+
 constexpr int kDecWaves = 4;
 constexpr int kTile = 32;
 constexpr float kNegInf = -__builtin_inff();
@@ -141,6 +183,9 @@ struct DecodeArgs {
   // its last `window` tokens (window >= 1)
   int window;
   int untimed;  // host only: never stamp this launch with timing events
+#ifdef S8KV_DECODE_TRACE
+  unsigned long long* trace;  // [grid][kTraceWords] per-workgroup records, or null
+#endif
 };
 
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
@@ -309,10 +354,18 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#ifdef S8KV_DECODE_TRACE
+  __shared__ unsigned long long trace_lds[kTraceWords];
+  if (tid < kTraceWords) trace_lds[tid] = 0;
+  __syncthreads();
+  S8KV_TRACE_STAMP(kTrEntry);
+  unsigned long long tr_tok = 0, tr_seg = 0;
+#endif
 
   // ---- context lengths -> LDS (one global round trip for the whole prologue) ----
   for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
   __syncthreads();
+  S8KV_TRACE_STAMP(kTrLens);
 
   // ---- stream positions: prefix of the rows' stream lengths (every wave) ----
   const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
@@ -478,8 +531,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       reordered = true;
     }
   }
+  S8KV_TRACE_STAMP(kTrFound);
   prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
   store_prefetched_bt();
+  S8KV_TRACE_STAMP(kTrStaged);
 
   // ---- segments: rows overlapping [lo, hi) ----
   for (;;) {
@@ -535,6 +590,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       }
     }
     __syncthreads();  // every head of q published
+    S8KV_TRACE_STAMP_ONCE(kTrQ);
     half8_t qhi[C::NQK], qlo[C::NQK];
 #pragma unroll
     for (int m = 0; m < C::NQK; ++m) {
@@ -881,6 +937,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         }
         while (tb + kTile * kDecWaves < t1) {  // a next tile exists, so this one is full
           process(tb, std::false_type{}, std::true_type{});
+          S8KV_TRACE_STAMP_ONCE(kTrTile1);
           tb += kTile * kDecWaves;
         }
         if constexpr (FUSE) {
@@ -948,6 +1005,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       }
     }
 
+    S8KV_TRACE_STAMP(kTrTilesEnd);
+#ifdef S8KV_DECODE_TRACE
+    tr_tok += (unsigned long long)(s1 - s0);
+    tr_seg += 1;
+    S8KV_TRACE_SET(kTrFlags, 1ull | ((unsigned long long)whole_row << 8));
+#endif
     // ---- next segment: its set-up loads overlap this segment's merge ----
     int nb, npb, nL;
     if (reordered) {  // the reordered last segment is done: continue from the first
@@ -1025,6 +1088,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         completes_row = arrive(a.ws_cnt + (int64_t)h * a.batch + b, a.tag, (uint32_t)(s1 - s0) >> 5,
                                (uint32_t)padL >> 5);
       __syncthreads();
+#ifdef S8KV_DECODE_TRACE
+      if (completes_row) S8KV_TRACE_SET(kTrFlags, trace_lds[kTrFlags] | (1ull << 9));
+#endif
       if (completes_row) {
         // slices jf..jl hold the row's segments; their partials are at slots j + b
         // (recomputed here from opaque copies of its inputs, so that no part of
@@ -1070,6 +1136,13 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     pb = npb;
     L = nL;
   }
+#ifdef S8KV_DECODE_TRACE
+  S8KV_TRACE_STAMP(kTrExit);
+  S8KV_TRACE_SET(kTrWork, tr_tok | (tr_seg << 32));
+  __syncthreads();
+  if (a.trace != nullptr && threadIdx.x < kTraceWords)
+    a.trace[(int64_t)blockIdx.x * kTraceWords + threadIdx.x] = trace_lds[threadIdx.x];
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1079,6 +1152,21 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 // Kernel timing (diagnostics): while enabled, every decode call launches its
 // kernel with HIP events stamped with the kernel's start and end time
 // (hipExtLaunchKernelGGL).  Calls under graph capture are not timed.
+#ifdef S8KV_DECODE_TRACE
+// Trace buffer of the diagnostics build: consecutive launches take
+// consecutive slots of the caller's buffer (modulo its slot count), each
+// `stride` words; launches that need more than a slot are not traced.
+struct TraceState {
+  unsigned long long* buf = nullptr;
+  int64_t stride = 0, slots = 0, next = 0;
+};
+static TraceState g_trace;
+static unsigned long long* trace_slot(int64_t words) {
+  if (g_trace.buf == nullptr || g_trace.slots <= 0 || words > g_trace.stride) return nullptr;
+  return g_trace.buf + (g_trace.next++ % g_trace.slots) * g_trace.stride;
+}
+#endif
+
 struct TimingState {
   bool on = false;
   std::vector<std::array<hipEvent_t, 2>> events;
@@ -1171,6 +1259,9 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   }
   a.slots = a.batch + a.wg_per_head;
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
+#ifdef S8KV_DECODE_TRACE
+  a.trace = trace_slot((int64_t)grid.x * kTraceWords);
+#endif
   hipEvent_t* ev = a.untimed ? nullptr : timing_slot(stream);
   if (ev) {  // events stamped with the kernel's own start and end times
     hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
@@ -1317,6 +1408,18 @@ static int scratch_for_current_device(void** out) {
 }  // namespace s8kv
 
 using namespace s8kv;
+
+#ifdef S8KV_DECODE_TRACE
+// Diagnostics build only: route the records of the next decode launches to a
+// device buffer of `slots` x `stride` 64-bit words (null: stop tracing).
+extern "C" int s8kv_decode_trace_set(void* buffer, int64_t stride_words, int64_t slots) {
+  g_trace.buf = static_cast<unsigned long long*>(buffer);
+  g_trace.stride = stride_words;
+  g_trace.slots = slots;
+  g_trace.next = 0;
+  return S8KV_OK;
+}
+#endif
 
 extern "C" int s8kv_timing_begin(void) {
   g_timing.on = true;
