@@ -617,8 +617,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       }
     }
 
-    float m_run = kNegInf;
+    float m_ref = kNegInf;  // running max - esh (WeightShift)
     float l_run = 0.0f;
+    WeightShift ws(kMaxSlack);
     float4_t acc[C::NPV];
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -836,8 +837,35 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
         // 4. online softmax (log2 domain; q carries scale*log2e).  The running
         // max is raised lazily: only when some head's tile max exceeds it by
-        // more than kMaxSlack, so p <= 2^kMaxSlack and most tiles skip the
-        // accumulator rescale.
+        // more than kMaxSlack, so p <= 2^(kMaxSlack + esh) and most tiles skip
+        // the accumulator rescale.  First the weight shift: a V scale above
+        // the bound lowers esh (WeightShift).
+        {
+          float vmx = 0.0f;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int nb = 0; nb < C::NB; ++nb) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float v = io.vs[s][nb][i];
+                if constexpr (MASKED) {  // scales past the row end may be any value
+                  const int tok = tb + 16 * s + 4 * g + i;
+                  v = (tok < t1 && (!WIN || tok >= lo_tok)) ? v : 0.0f;
+                }
+                vmx = fmaxf(vmx, v);
+              }
+            }
+          }
+          if (__builtin_amdgcn_ballot_w64(vmx > ws.vbound()) != 0) {
+            const int d = ws.raise(max_x32(max_x16(vmx)), kMaxSlack);
+            const float f = __builtin_ldexpf(1.0f, d);
+            l_run *= f;
+#pragma unroll
+            for (int n = 0; n < C::NPV; ++n) acc[n] *= f;
+            m_ref -= (float)d;
+          }
+        }
         float p[2][4];
         float mt = kNegInf;
 #pragma unroll
@@ -855,19 +883,19 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         }
         mt = max_x16(mt);
         mt = max_x32(mt);
-        if (__builtin_amdgcn_ballot_w64(mt > m_run + kMaxSlack) != 0) {
-          const float m_new = fmaxf(m_run, mt);
-          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+        if (__builtin_amdgcn_ballot_w64(mt > m_ref + ws.thr()) != 0) {
+          const float m_new = fmaxf(m_ref, mt - (float)ws.esh);
+          const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);  // 0 when m_ref = -inf
           l_run *= alpha;
 #pragma unroll
           for (int n = 0; n < C::NPV; ++n) acc[n] *= alpha;
-          m_run = m_new;
+          m_ref = m_new;
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(p[s][i] - m_run);  // exp2(-inf) = 0 for masked tokens
+            const float e = __builtin_amdgcn_exp2f(p[s][i] - m_ref);  // exp2(-inf) = 0 for masked tokens
             p[s][i] = e;
             l_run += e;
           }
@@ -1046,7 +1074,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         for (int r = 0; r < 4; ++r) w_acc[c * D + 16 * n + 4 * g + r] = acc[n][r];
       }
       if (g == 0) {
-        w_acc[G * D + c] = m_run;
+        w_acc[G * D + c] = m_ref;  // l and acc are relative to 2^m_ref
         w_acc[G * D + 16 + c] = l_tot;
       }
     }

@@ -178,6 +178,47 @@ __device__ __forceinline__ int opaque_int(int x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------
+// Exponent shift of the fp16 softmax weights
+// ---------------------------------------------------------------------------
+// The PV MFMAs take the weights p * (V scale | block norm) as fp16 hi + lo,
+// whose range (2^-24 .. 65504) is far narrower than fp32's.  With p relative
+// to the running max and scales near 2^-6, weights below ~2^-18 of the
+// largest would underflow to zero -- and tens of thousands of such keys hold a
+// visible share of the softmax mass.  A wave-uniform power-of-two shift
+// `esh`, folded into the running max (the kernels keep m_ref = max - esh),
+// scales every p by 2^esh such that the largest weight the lazy max allows,
+// 2^(kMaxSlack + esh), times `vbound` (a power of two above every scale seen)
+// is 2^15.  l and the accumulators carry the same factor, which cancels in
+// acc / l and in the combine of partials (each is relative to its own m_ref).
+//
+// WeightShift holds esh and vbound (and the lazy-max threshold esh + slack)
+// as integers and float bit patterns read back with readfirstlane, so that
+// the loop-carried state stays in scalar registers.  raise(vmax): the tile's
+// largest scale `vmax` (> vbound, finite, equal in every lane) raises the
+// bound; returns the change of esh, by which l and acc are multiplied
+// (2^change) and m_ref lowered.  esh stays within [-16, 64], which keeps
+// l <= 2^28 keys * 2^(8 + 64) inside fp32.
+struct WeightShift {
+  int esh;
+  uint32_t vbound_bits;  // 0: no scale seen yet
+  uint32_t thr_bits;     // float(esh) + slack
+  __device__ __forceinline__ explicit WeightShift(float slack)
+      : esh(0), vbound_bits(0), thr_bits(__builtin_bit_cast(uint32_t, slack)) {}
+  __device__ __forceinline__ float vbound() const { return __builtin_bit_cast(float, vbound_bits); }
+  __device__ __forceinline__ float thr() const { return __builtin_bit_cast(float, thr_bits); }
+  __device__ __forceinline__ int raise(float vmax, float slack) {
+    const uint32_t vb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__builtin_bit_cast(uint32_t, vmax));
+    const int k = min((int)((vb >> 23) & 0xFFu) - 126, 128);  // vbound = 2^k > vmax (k = 128: +inf)
+    const int sh = max(-16, min(64, 15 - (int)slack - k));
+    const int d = sh - esh;
+    esh = sh;
+    vbound_bits = (uint32_t)(k + 127) << 23;
+    thr_bits = (uint32_t)__builtin_amdgcn_readfirstlane((int)__builtin_bit_cast(uint32_t, (float)sh + slack));
+    return d;
+  }
+};
+
 // Round-half-even to int, clamped to [-127, 127].  `y` and `scale` are fp32;
 // the division is IEEE correctly rounded (HIP's default fp32 divide).
 __device__ __forceinline__ int rtn_i8(float y, float scale) {

@@ -40,7 +40,7 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kMaxSlack = 8.0f;
 // Running max before any key: finite, so exp2(score - max) is 0 for a masked
 // score (-inf) and never NaN, with no test per score; any real score exceeds
-// it by more than kMaxSlack, which makes the first visible tile rescale (by 0).
+// it by more than kMaxSlack + esh, which makes the first visible tile rescale (by 0).
 constexpr float kMaxInit = -1.0e30f;
 
 template <int D, bool K8V3>
@@ -231,11 +231,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     }
   }
 
-  float m_run[RG], l_run[RG];
+  float m_ref[RG], l_run[RG];  // m_ref: running max - esh (WeightShift)
   float4_t acc[RG][C::NPV];
+  WeightShift ws(kMaxSlack);
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
-    m_run[rg] = kMaxInit;
+    m_ref[rg] = kMaxInit;
     l_run[rg] = 0.0f;
 #pragma unroll
     for (int n = 0; n < C::NPV; ++n) acc[rg][n] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -480,6 +481,30 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         vsc[s] = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * s + 4 * g);
         if constexpr (C::NB == 2) vsc1[s] = *reinterpret_cast<const float4_t*>(sb + 2 * kTile + 16 * s + 4 * g);
       }
+      // The weight shift: a V scale above the bound lowers esh (WeightShift),
+      // tested with the running max's (row group 0's branch).  Each lane tests
+      // one of the tile's (1 + NB) * 32 staged scales -- lane (g, c) the scale
+      // of key 16 ((c >> 2) & 1) + 4 g + (c & 3), of block c >> 3 when there
+      // are two -- so the 64 lanes cover them all.
+      const int pk = 16 * ((c >> 2) & 1) + 4 * g + (c & 3);
+      float vp = sb[kTile * (1 + ((c >> 3) & (C::NB - 1))) + pk];
+      if constexpr (MASKED && WIN && !DENSE) vp = base + pk >= lo_key ? vp : 0.0f;  // below the window: any value
+      auto shift_weights = [&]() {
+        if (__builtin_amdgcn_ballot_w64(vp > ws.vbound()) == 0) return;
+        float vmx = fmaxf(vp, shfl_xor_f(vp, 1));
+        vmx = fmaxf(vmx, shfl_xor_f(vmx, 2));
+        vmx = fmaxf(vmx, shfl_xor_f(vmx, 4));
+        vmx = fmaxf(vmx, shfl_xor_f(vmx, 8));
+        const int d = ws.raise(max_x32(max_x16(vmx)), kMaxSlack);
+        const float f = __builtin_ldexpf(1.0f, d);
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          l_run[r] *= f;
+#pragma unroll
+          for (int n = 0; n < C::NPV; ++n) acc[r][n] *= f;
+          m_ref[r] -= (float)d;
+        }
+      };
       half8_t pbh[RG], pbl[RG], pbh1[RG], pbl1[RG];  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
@@ -497,7 +522,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         for (int s = 0; s < 2; ++s) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_run[rg]);
+            float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_ref[rg]);
             if constexpr (MASKED) v = visible(s, i) ? v : kNegInf;
             y[s][i] = v;
             my = fmaxf(my, v);
@@ -505,7 +530,8 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         }
         my = max_x16(my);
         my = max_x32(my);
-        if (__builtin_amdgcn_ballot_w64(my > kMaxSlack) != 0) {
+        if (__builtin_amdgcn_ballot_w64(my > ws.thr() || (rg == 0 && vp > ws.vbound())) != 0) {
+          if (rg == 0) shift_weights();
           // raise the running max to the tile's (from the products, exactly),
           // rescale, and take the scores relative to the new max
           float mt = kNegInf;
@@ -520,12 +546,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           }
           mt = max_x16(mt);
           mt = max_x32(mt);
-          const float m_new = fmaxf(m_run[rg], mt);
-          const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
+          const float m_new = fmaxf(m_ref[rg], mt - (float)ws.esh);
+          const float alpha = __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
           l_run[rg] *= alpha;
 #pragma unroll
           for (int n = 0; n < C::NPV; ++n) acc[rg][n] *= alpha;
-          m_run[rg] = m_new;
+          m_ref[rg] = m_new;
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
 #pragma unroll
