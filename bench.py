@@ -450,14 +450,15 @@ def verify_workload(kind: str, device, k8v3: bool = False, layers: int = VERIFY_
     blocks appear in every block table) each append a 512-token chunk and
     attend bottom-right causally.  Tree verify: 32 sequences with 8192-token
     prefixes each append 16..64 draft nodes of a random tree (BFS, 1-4
-    children per expanded node) and attend prefix + ancestors.  Seeds 3 / 4.
+    children per expanded node) and attend prefix + ancestors; tree_b1: one
+    sequence, a 32768-token prefix and a 32-node tree.  Seeds 3 / 4 / 5.
     `k8v3`: the same over the K8V3 cache (int8 K, 3-bit Lloyd-Max V)."""
     import torch
 
     from superl8_serve_amd import ops
     from superl8_serve_amd.codebook import gaussian_codebook
 
-    rng = np.random.default_rng(3 if kind == "chunk" else 4)
+    rng = np.random.default_rng({"chunk": 3, "tree": 4}.get(kind, 5))
     if kind == "chunk":
         b_, prefix_len, nq_max = 16, 4096, 512
         nq = np.full(b_, nq_max)
@@ -472,10 +473,15 @@ def verify_workload(kind: str, device, k8v3: bool = False, layers: int = VERIFY_
         prefix = np.full(b_, prefix_len)
         tree = None
     else:
-        b_, prefix_len = 32, 8192
-        nq = rng.integers(16, 65, size=b_)
-        nq_max = 64
-        per = (prefix_len + 64 + BS - 1) // BS
+        if kind == "tree_b1":  # batch-1 speculative decoding: one long context, one 32-node tree
+            b_, prefix_len = 1, 32768
+            nq = np.full(1, 32)
+            nq_max = 32
+        else:
+            b_, prefix_len = 32, 8192
+            nq = rng.integers(16, 65, size=b_)
+            nq_max = 64
+        per = (prefix_len + nq_max + BS - 1) // BS
         n_blocks = b_ * per + 4
         perm = rng.permutation(n_blocks)
         bt = perm[: b_ * per].reshape(b_, per).astype(np.int32)
@@ -510,7 +516,7 @@ def verify_workload(kind: str, device, k8v3: bool = False, layers: int = VERIFY_
         else:
             ops.quantize_kv_write_paged(k, v, kc[layer], ks[layer], vc[layer], vs[layer], slots)
     gen = torch.Generator(device=device)
-    gen.manual_seed(3 if kind == "chunk" else 4)
+    gen.manual_seed({"chunk": 3, "tree": 4}.get(kind, 5))
     # prefix tokens (the shared prefix once for the chunk workload)
     rows = range(1) if kind == "chunk" else range(b_)
     pre_slots = np.concatenate([bt[i, np.arange(prefix_len) // BS] * BS + np.arange(prefix_len) % BS for i in rows])
@@ -592,13 +598,26 @@ def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
     t_layer = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
     tflops = info["flops_layer"] / t_attn / 1e12
     gbps = info["kv_bytes_layer"] / t_attn / 1e9
-    name = "chunked prefill (16 x (4096 shared prefix + 512 chunk))" if kind == "chunk" else \
-        "tree verify (32 x (8192 prefix + 16..64 draft tree))"
+    name = {"chunk": "chunked prefill (16 x (4096 shared prefix + 512 chunk))",
+            "tree": "tree verify (32 x (8192 prefix + 16..64 draft tree))",
+            "tree_b1": "tree verify (1 x (32768 prefix + 32 draft tree))"}[kind]
+    split = {}
+    if kind == "tree_b1":  # the same call with the key-range split switched off
+        os.environ["S8KV_VERIFY_SPLITS"] = "1"
+        _spin_ahead()
+        st.record()
+        for i in range(steps * VERIFY_LAYERS):
+            layer_ops(i % VERIFY_LAYERS, append=False)
+        en.record()
+        torch.cuda.synchronize()
+        del os.environ["S8KV_VERIFY_SPLITS"]
+        t_one = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
+        split = {"ms_per_layer_attention_unsplit": round(t_one * 1e3, 4), "split_speedup": round(t_one / t_attn, 2)}
     print(json.dumps({
         "metric": f"paged {'k8v3' if k8v3 else 'int8'} verify attention TFLOP/s, {name}, Qwen3-8B heads",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_layer_attention": round(t_attn * 1e3, 4), "ms_per_layer_append_plus_attention": round(t_layer * 1e3, 4),
-        "higher_is_better": True,
+        **split, "higher_is_better": True,
         "dtype": f"{'int8 K / 3-bit V' if k8v3 else 'int8'} cache, fp16 MFMA (hi+lo split operands)",
         "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20)",
         "config": {"workload": name, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
@@ -984,11 +1003,12 @@ def main():
     ap.add_argument("--trace-decode", action="store_true",
                     help="only print the per-launch breakdown of the decode step from the trace build "
                          "(superl8_serve_amd/libsuperl8_kv_trace.so)")
-    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "chunk_k8v3", "tree_k8v3", "k8v3", "window",
-                                           "prefill", "copy", "append", "append_k8v3"],
+    ap.add_argument("--workload", choices=["decode", "chunk", "tree", "tree_b1", "chunk_k8v3", "tree_k8v3", "k8v3",
+                                           "window", "prefill", "copy", "append", "append_k8v3"],
                     default="decode",
                     help="decode: the Qwen3-8B batch-64 int8 decode step (headline); chunk / tree: verify "
-                         "attention (chunk_k8v3 / tree_k8v3: over the K8V3 cache); k8v3: the K8V3 decode step "
+                         "attention (chunk_k8v3 / tree_k8v3: over the K8V3 cache; tree_b1: one sequence, "
+                         "32768-token prefix, 32-node tree); k8v3: the K8V3 decode step "
                          "(batch 32, 8k-32k); window: sliding-window decode (batch 64, window 4096); prefill: dense "
                          "causal prefill attention (16 x 4096 tokens); copy: "
                          "copy_blocks; append / append_k8v3: prefill append of 131,072 tokens")
@@ -1016,8 +1036,8 @@ def main():
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
         return
-    if args.workload in ("chunk", "tree", "chunk_k8v3", "tree_k8v3"):
-        run_verify(args.workload.split("_")[0], args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
+    if args.workload in ("chunk", "tree", "tree_b1", "chunk_k8v3", "tree_k8v3"):
+        run_verify(args.workload.removesuffix("_k8v3"), args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
         return
     if args.workload == "k8v3":
         run_k8v3(args.steps, args.warmup, not args.separate_append)

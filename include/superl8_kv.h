@@ -233,13 +233,22 @@ int s8kv_decode_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * at most 64 drafts).  Keys at positions >= max_context_len are not read.
  * out: fp16 [batch, num_q_heads, max_queries, head_dim] contiguous; queries
  * s >= query_lens[b] produce zeros.  head_dim 64, 128 or 256.
+ *
+ * workspace (16-byte aligned, s8kv_verify_workspace_size bytes; NULL or
+ * smaller: no split) lets a call with fewer (sequence, KV head, query block)
+ * units than the GPU keeps resident, or with more than 2^20 keys per unit,
+ * split each unit's keys across workgroups and combine their partials in a
+ * second kernel on the same stream.  Calls that overlap on one workspace race.
  */
+int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
+                                   int max_context_len);
 int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
                      int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s, const int8_t* k_cache,
                      const float* k_scale, const int8_t* v_cache, const float* v_scale, int64_t num_blocks,
                      int block_size, const int32_t* block_table, int64_t block_table_stride,
                      const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                     int max_context_len, float scale, void* out, void* stream);
+                     int max_context_len, float scale, void* out, void* workspace, int64_t workspace_bytes,
+                     void* stream);
 
 /*
  * s8kv_verify_int8 over the K8V3 cache (int8 K, 3-bit Lloyd-Max V): the
@@ -257,7 +266,8 @@ int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads
                      const float* k_scale, const int32_t* v_packed, const float* v_norm, const float* v_codebook,
                      int lloyd_block, int64_t num_blocks, int block_size, const int32_t* block_table,
                      int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                     const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream);
+                     const int64_t* tree_mask, int max_context_len, float scale, void* out, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /*
  * Verify attention of a sliding-window layer: as s8kv_verify_int8 /
@@ -280,7 +290,7 @@ int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_k
                             const int64_t* tree_mask, int max_context_len, int window, const void* k_draft,
                             int64_t kd_stride_b, int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft,
                             int64_t vd_stride_b, int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out,
-                            void* stream);
+                            void* workspace, int64_t workspace_bytes, void* stream);
 int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                             int max_queries, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
                             const int8_t* k_cache, const float* k_scale, const int32_t* v_packed,
@@ -289,7 +299,8 @@ int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
                             const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
                             int max_context_len, int window, const void* k_draft, int64_t kd_stride_b,
                             int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft, int64_t vd_stride_b,
-                            int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* stream);
+                            int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /*
  * Prefill attention over fresh fp16 K / V (not the cache), varlen batched:

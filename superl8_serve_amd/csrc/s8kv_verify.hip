@@ -23,6 +23,8 @@
 //         B = P * v_scale (K8V3: P * the key's block norm) as fp16 hi + lo
 //         (hi: the fp32 weight cut to fp16 precision, lo: the exact rest).
 // Rows past a sequence's query count are written as zeros.
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "s8kv_device.h"
@@ -93,6 +95,12 @@ struct VerifyArgs {
   int bs_log2;
   int max_context_len;
   int n_qblocks;              // query blocks (rows_per_wg rows each) per (sequence, KV head)
+  // split of the key range: workgroup split sp of a (sequence, KV head, query
+  // block) attends its share of the keys and writes unnormalized partials
+  // (acc[D], m_ref, l per row, pitch D + 4 floats) to part; a second kernel
+  // combines them.  splits == 1: the workgroup writes the output itself.
+  int splits;
+  float* part;
   int window;                 // verify_kernel<.., WIN>: only the last `window` prefix keys are visible
   // WIN, optional: the drafts' fresh K (rotated, fp32) and V (fp16),
   // attended in place of their cache rows (draft i of row b, head h at
@@ -128,7 +136,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   const int xcd = blockIdx.x & 7;
   const int rest = blockIdx.x >> 3;
   const int qb = rest % a.n_qblocks;
-  const int p = (rest / a.n_qblocks) * 8 + xcd;
+  const int rest2 = rest / a.n_qblocks;
+  const int sp = rest2 % a.splits;
+  const int p = (rest2 / a.splits) * 8 + xcd;
   if (p >= P) return;
   const int b = p / a.num_kv_heads;
   const int h = p - b * a.num_kv_heads;
@@ -262,8 +272,15 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   const uint32_t hkv = (uint32_t)a.num_kv_heads;
   const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
 
-  for (int u0 = lo_key & ~(kTile - 1); u0 < kv_end; u0 += kSubKeys) {
-    const int u1 = min(kv_end, u0 + kSubKeys);
+  // this workgroup's keys: split sp of the block's tile-aligned key range
+  int k_lo = lo_key & ~(kTile - 1), k_hi = kv_end;
+  if (a.splits > 1) {
+    const int chunk = ((max(0, kv_end - k_lo) + a.splits - 1) / a.splits + kTile - 1) & ~(kTile - 1);
+    k_lo += sp * chunk;
+    k_hi = min(kv_end, k_lo + chunk);
+  }
+  for (int u0 = k_lo; u0 < k_hi; u0 += kSubKeys) {
+    const int u1 = min(k_hi, u0 + kSubKeys);
     const int fb = u0 >> bs_log2;
     const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
     __syncthreads();  // previous users of bt_lds and the tile buffers are done
@@ -661,6 +678,23 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     }
   }
 
+  // ---- split: this wave's unnormalized rows to the partials ----
+  if (a.splits > 1) {
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      const float l_tot = sum_x32(sum_x16(l_run[rg]));
+      const int rl = (rg * kWaves + wave) * 16 + c;  // row within the block
+      float* pr = a.part + ((((int64_t)p * a.n_qblocks + qb) * a.splits + sp) * C::ROWS + rl) * (D + 4);
+#pragma unroll
+      for (int n = 0; n < C::NPV; ++n) *reinterpret_cast<float4_t*>(pr + 16 * n + 4 * g) = acc[rg][n];
+      if (g == 0) {
+        pr[D] = m_ref[rg];
+        pr[D + 1] = l_tot;
+      }
+    }
+    return;
+  }
+
   // ---- normalize and write this wave's rows ----
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
@@ -684,6 +718,70 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 // Query rows per workgroup at this head_dim (Cfg<D, *>::ROWS).
 static int rows_per_wg(int head_dim) { return 16 * kWaves * (head_dim <= 64 ? 2 : 1); }
 
+// Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
+// KV head, query block) merges the row's `splits` partials -- each relative to
+// its own running max, so weighted by 2^(m_s - max_s m_s) -- and writes the
+// normalized fp16 dims.  Workgroup x covers items kCombineThreads * (x %
+// blocks_per_unit) .. of unit x / blocks_per_unit.
+constexpr int kCombineThreads = 256;
+template <int D>
+__global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyArgs a) {
+  constexpr int ROWS = 16 * kWaves * (D <= 64 ? 2 : 1);
+  constexpr int V4 = D / 4;
+  constexpr int BLOCKS = ROWS * V4 / kCombineThreads;  // workgroups per unit
+  static_assert(ROWS * V4 % kCombineThreads == 0, "whole workgroups per unit");
+  const int pq = blockIdx.x / BLOCKS;  // (sequence, KV head) * n_qblocks + query block
+  const int it = (blockIdx.x - pq * BLOCKS) * kCombineThreads + threadIdx.x;
+  const int p = pq / a.n_qblocks;
+  const int qb = pq - p * a.n_qblocks;
+  const int b = p / a.num_kv_heads;
+  const int h = p - b * a.num_kv_heads;
+  const int G = a.group;
+  const int rl = it / V4;
+  const int c4 = it - rl * V4;
+  const int r = qb * ROWS + rl;
+  const int pos = r / G;
+  if (pos >= a.max_queries) return;
+  const int head = h * G + (r - pos * G);
+  const int S = a.splits;
+  const int64_t stride = (int64_t)ROWS * (D + 4);  // between splits of one row
+  const float* row = a.part + ((int64_t)pq * S * ROWS + rl) * (D + 4);
+  constexpr int U = 8;  // partials in flight
+  float M = -__builtin_inff();
+  for (int s0 = 0; s0 < S; s0 += U) {
+    float m[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) m[u] = s0 + u < S ? row[(s0 + u) * stride + D] : -__builtin_inff();
+#pragma unroll
+    for (int u = 0; u < U; ++u) M = fmaxf(M, m[u]);
+  }
+  float4_t num = float4_t{0.f, 0.f, 0.f, 0.f};
+  float den = 0.0f;
+  for (int s0 = 0; s0 < S; s0 += U) {
+    float m[U], l[U];
+    float4_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = min(s0 + u, S - 1);
+      const float* pr = row + s * stride;
+      m[u] = pr[D];
+      l[u] = pr[D + 1];
+      x[u] = *reinterpret_cast<const float4_t*>(pr + 4 * c4);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float f = s0 + u < S ? __builtin_amdgcn_exp2f(m[u] - M) : 0.0f;
+      num += f * x[u];
+      den += f * l[u];
+    }
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  half4_t o;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(num[rr] * inv);
+  *reinterpret_cast<half4_t*>(a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D + 4 * c4) = o;
+}
+
 template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
 static int launch(VerifyArgs& a, hipStream_t stream) {
   static_assert(Cfg<D, K8V3>::ROWS == 16 * kWaves * (D <= 64 ? 2 : 1), "rows_per_wg");
@@ -698,13 +796,21 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     attr = true;
   }
   const int P = a.batch * a.num_kv_heads;
-  const int64_t grid = (int64_t)8 * a.n_qblocks * ((P + 7) / 8);
+  const int64_t grid = (int64_t)8 * a.n_qblocks * a.splits * ((P + 7) / 8);
   if (grid > INT32_MAX) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
   hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE>), dim3((unsigned)grid), dim3(kThreads),
                      WIN ? C::SMEM_WIN : C::SMEM, stream, a);
+  if (a.splits > 1) {
+    const int rc = check_launch("s8kv_verify");
+    if (rc != S8KV_OK) return rc;
+    const int64_t units = (int64_t)P * a.n_qblocks;
+    hipLaunchKernelGGL((verify_combine_kernel<D>), dim3((unsigned)(units * (C::ROWS * (D / 4) / kCombineThreads))),
+                       dim3(kCombineThreads), 0, stream, a);
+    return check_launch("s8kv_verify_combine");
+  }
   return check_launch("s8kv_verify");
 }
 
@@ -721,6 +827,59 @@ struct FreshDrafts {
   int64_t k_stride[3];
   int64_t v_stride[3];
 };
+
+// Key-range split of the paged verify.  A launch with fewer workgroups than
+// the GPU keeps resident (two per CU) leaves CUs idle for the whole call --
+// batch-1 speculative decoding with a long context is the common case -- so
+// each (sequence, KV head, query block) is split until about that many
+// exist, down to kMinSplitKeys keys per split; and one workgroup never
+// accumulates more than kMaxSplitKeys keys, which bounds the rounding of its
+// fp32 sums.  S8KV_VERIFY_SPLITS overrides the count (tests).
+constexpr int kMinSplitKeys = 1024;
+constexpr int kMaxSplitKeys = 1 << 20;
+constexpr int kMaxSplits = 1024;
+static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys) {
+  const int64_t natural = (int64_t)batch * num_kv_heads * n_qblocks;
+  const int64_t resident = (int64_t)2 * device_cus();
+  int64_t s = natural < resident ? (resident + natural - 1) / natural : 1;
+  s = std::min<int64_t>(s, std::max(1, keys / kMinSplitKeys));
+  s = std::max<int64_t>(s, ((int64_t)keys + kMaxSplitKeys - 1) / kMaxSplitKeys);
+  if (const char* env = getenv("S8KV_VERIFY_SPLITS")) {
+    const int v = atoi(env);
+    if (v > 0) s = v;
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
+}
+static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits) {
+  if (splits <= 1) return 0;
+  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim) * (head_dim + 4) * 4;
+}
+
+extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                              int max_queries, int max_context_len) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_queries <= 0 ||
+      max_context_len < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return 0;
+  const int rows_wg = verify::rows_per_wg(head_dim);
+  const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
+  return verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
+                           verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len));
+}
+
+// The split for this call (keys: the most any block reads -- a window layer's
+// window and drafts), used when the caller's workspace holds its partials;
+// never more than s8kv_verify_workspace_size plans for, which counts
+// max_context_len keys.
+static void verify_use_workspace(verify::VerifyArgs& a, int head_dim, void* workspace, int64_t workspace_bytes) {
+  const int keys = a.window > 0 ? (int)std::min<int64_t>(a.max_context_len, (int64_t)a.window + a.max_queries)
+                                : a.max_context_len;
+  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys);
+  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s);
+  if (s > 1 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0) {
+    a.splits = s;
+    a.part = (float*)workspace;
+  }
+}
 
 // Checks and arguments shared by both layouts (everything but V).
 static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num_q_heads, int num_kv_heads,
@@ -773,16 +932,19 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
                                 const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
                                 const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                 int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream,
-                            int window, const FreshDrafts* fresh) {
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out,
+                                void* workspace, int64_t workspace_bytes, void* stream, int window,
+                                const FreshDrafts* fresh) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   verify::VerifyArgs a{};
+  a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
   a.window = window;
+  verify_use_workspace(a, head_dim, workspace, workspace_bytes);
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -825,11 +987,12 @@ extern "C" int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int n
                                 const int8_t* k_cache, const float* k_scale, const int8_t* v_cache,
                                 const float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                 int64_t block_table_stride, const int32_t* prefix_lens, const int32_t* query_lens,
-                                const int64_t* tree_mask, int max_context_len, float scale, void* out, void* stream) {
+                                const int64_t* tree_mask, int max_context_len, float scale, void* out,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
                           block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
-                          stream, 0, nullptr);
+                          workspace, workspace_bytes, stream, 0, nullptr);
 }
 
 extern "C" int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -840,14 +1003,14 @@ extern "C" int s8kv_verify_window_int8(const void* q, int batch, int num_q_heads
                                 const int64_t* tree_mask, int max_context_len, int window, const void* k_draft,
                                 int64_t kd_stride_b, int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft,
                                 int64_t vd_stride_b, int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
   const FreshDrafts fresh{k_draft, v_draft, {kd_stride_b, kd_stride_s, kd_stride_h},
                           {vd_stride_b, vd_stride_s, vd_stride_h}};
   return verify_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_cache, v_scale, num_blocks, block_size, block_table,
                           block_table_stride, prefix_lens, query_lens, tree_mask, max_context_len, scale, out,
-                          stream, window, &fresh);
+                          workspace, workspace_bytes, stream, window, &fresh);
 }
 
 
@@ -857,19 +1020,21 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
                                 const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                                 int block_size, const int32_t* block_table, int64_t block_table_stride,
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                                int max_context_len, float scale, void* out, void* stream,
-                            int window, const FreshDrafts* fresh) {
+                                int max_context_len, float scale, void* out, void* workspace,
+                                int64_t workspace_bytes, void* stream, int window, const FreshDrafts* fresh) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
   S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
                "verify k8v3: head_dim %d not in {128, 256}", head_dim);
   S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "verify k8v3: lloyd_block %d != 128", lloyd_block);
   verify::VerifyArgs a{};
+  a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
   if (rc != S8KV_OK) return rc;
   a.window = window;
+  verify_use_workspace(a, head_dim, workspace, workspace_bytes);
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -904,11 +1069,12 @@ extern "C" int s8kv_verify_k8v3(const void* q, int batch, int num_q_heads, int n
                                 const float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                                 int block_size, const int32_t* block_table, int64_t block_table_stride,
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
-                                int max_context_len, float scale, void* out, void* stream) {
+                                int max_context_len, float scale, void* out, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
   return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
                           block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
-                          max_context_len, scale, out, stream, 0, nullptr);
+                          max_context_len, scale, out, workspace, workspace_bytes, stream, 0, nullptr);
 }
 
 extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -919,14 +1085,15 @@ extern "C" int s8kv_verify_window_k8v3(const void* q, int batch, int num_q_heads
                                 const int32_t* prefix_lens, const int32_t* query_lens, const int64_t* tree_mask,
                                 int max_context_len, int window, const void* k_draft, int64_t kd_stride_b,
                                 int64_t kd_stride_s, int64_t kd_stride_h, const void* v_draft, int64_t vd_stride_b,
-                                int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* stream) {
+                                int64_t vd_stride_s, int64_t vd_stride_h, float scale, void* out, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
   S8KV_REQUIRE(window >= 1, S8KV_ERR_INVALID, "verify_window: window %d < 1", window);
   const FreshDrafts fresh{k_draft, v_draft, {kd_stride_b, kd_stride_s, kd_stride_h},
                           {vd_stride_b, vd_stride_s, vd_stride_h}};
   return verify_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                           q_stride_s, k_cache, k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks,
                           block_size, block_table, block_table_stride, prefix_lens, query_lens, tree_mask,
-                          max_context_len, scale, out, stream, window, &fresh);
+                          max_context_len, scale, out, workspace, workspace_bytes, stream, window, &fresh);
 }
 
 
@@ -952,6 +1119,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
                    v_stride_t % 8 == 0 && v_stride_h % 8 == 0,
                S8KV_ERR_INVALID, "attn_varlen: K and V rows must be 16-byte aligned");
   verify::VerifyArgs a{};
+  a.splits = 1;
   a.q = (const _Float16*)q;
   a.q_stride_s = q_stride_t;
   a.q_stride_h = q_stride_h;

@@ -441,11 +441,15 @@ def _verify_inputs(q, k_cache, k_scale, block_table, prefix_lens, block_size, qu
     _require(0 <= max_context_len <= block_table.shape[1] * bs,
              f"max_context_len {max_context_len} exceeds the block table capacity {block_table.shape[1] * bs}")
     out = torch.empty((b, hq, s_, d), dtype=torch.float16, device=dev)
+    # partials of a key-range split (few query blocks or very long rows)
+    ws_bytes = int(_lib.load().s8kv_verify_workspace_size(b, hq, hkv, d, s_, max_context_len)) if b and s_ else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     # keep the contiguous copies alive until the launch is enqueued
-    keep = (q, block_table, prefix_lens, query_lens, tree_mask)
+    keep = (q, block_table, prefix_lens, query_lens, tree_mask, ws)
     head = (q.data_ptr(), b, hq, hkv, d, s_, q.stride(0), q.stride(1), q.stride(2))
     tail = (block_table.data_ptr(), block_table.stride(0), prefix_lens.data_ptr(), ql_ptr, tm_ptr, max_context_len)
-    return keep, head, tail, (n, hkv, bs, d), out
+    workspace = (ws.data_ptr() if ws is not None else None, ws_bytes)
+    return keep, head, tail, workspace, (n, hkv, bs, d), out
 
 
 def _fresh_drafts(k_draft, v_draft, b, s_, hkv, d, dev):
@@ -484,7 +488,7 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
     the drafts are attended with those values, as the reference's window
     verify concatenates them to the dequantized prefix window
     (gqa_attention.py:298-303).  Returns fp16 ``[B, Hq, S, D]``."""
-    keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
+    keep, head, tail, workspace, (n, hkv, bs, d), out = _verify_inputs(
         q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
     dev = out.device
     _on_gpu("v_cache", v_cache, torch.int8, dev)
@@ -500,12 +504,12 @@ def attn_paged_verify(q, k_cache, k_scale, v_cache, v_scale, block_table, prefix
         alive, drafts = _fresh_drafts(k_draft, v_draft, out.shape[0], out.shape[2], hkv, d, dev)
         rc = lib.s8kv_verify_window_int8(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
-            *tail, int(window), *drafts, float(scale), out.data_ptr(), _stream(keep[0]),
+            *tail, int(window), *drafts, float(scale), out.data_ptr(), *workspace, _stream(keep[0]),
         )
     else:
         rc = lib.s8kv_verify_int8(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
-            *tail, float(scale), out.data_ptr(), _stream(keep[0]),
+            *tail, float(scale), out.data_ptr(), *workspace, _stream(keep[0]),
         )
     _lib.check(rc, "attn_paged_verify")
     return out
@@ -519,7 +523,7 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
     computes on a k8v3 cache with S sequential ``attn_paged_decode_k8v3``
     calls (chain verify, gqa_attention.py:259-277) or ``read_dense`` plus
     dense attention (chunked prefill).  head_dim 128 or 256, lloyd_block 128."""
-    keep, head, tail, (n, hkv, bs, d), out = _verify_inputs(
+    keep, head, tail, workspace, (n, hkv, bs, d), out = _verify_inputs(
         q, k_cache, k_scale, block_table, prefix_lens, block_size, query_lens, tree_mask, max_context_len)
     dev = out.device
     _on_gpu("v_packed", v_packed, torch.int32, dev)
@@ -540,12 +544,13 @@ def attn_paged_verify_k8v3(q, k_cache, k_scale, v_packed, v_norm, v_codebook, bl
         rc = lib.s8kv_verify_window_k8v3(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
             v_codebook.data_ptr(), lloyd_block, n, bs, *tail, int(window), *drafts, float(scale), out.data_ptr(),
-            _stream(keep[0]),
+            *workspace, _stream(keep[0]),
         )
     else:
         rc = lib.s8kv_verify_k8v3(
             *head, k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(),
-            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, float(scale), out.data_ptr(), _stream(keep[0]),
+            v_codebook.data_ptr(), lloyd_block, n, bs, *tail, float(scale), out.data_ptr(), *workspace,
+            _stream(keep[0]),
         )
     _lib.check(rc, "attn_paged_verify_k8v3")
     return out

@@ -1,0 +1,121 @@
+"""GPU parity of the verify's key-range split against the oracle, through the
+C ABI: each (sequence, KV head, query block) split across workgroups whose
+partials a second kernel combines.  The split is taken when a call has fewer
+units than the GPU keeps resident (batch-1 speculative decoding) or more than
+2^20 keys per unit; S8KV_VERIFY_SPLITS forces a count here, including counts
+that leave splits without keys."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from superl8_serve_amd import _lib, ops
+from tests.kvcase import make_case
+from tests.kvgpu import CODEBOOK, alloc, append, assert_close, layer, t, to_np, verify
+
+pytestmark = pytest.mark.gpu
+
+
+def _random_tree(rng, n):
+    """Ancestor bit masks of a random tree over n drafts (node i's parent < i)."""
+    masks = np.zeros(n, np.int64)
+    for i in range(n):
+        par = int(rng.integers(-1, i)) if i else -1
+        masks[i] = (masks[par] if par >= 0 else 0) | (1 << i)
+    return masks
+
+
+def _case(seed, kind, hq, hkv, d, bs, prefix, nq):
+    prefix = np.asarray(prefix)
+    case = make_case(seed, len(prefix), hq, hkv, d, bs, prefix + nq, outlier_channels=2 if d >= 128 else 0)
+    cache = alloc(kind, case.num_blocks, hkv, bs, d)
+    append(kind, t(case.k), t(case.v), cache, t(case.slots))
+    qv = np.random.default_rng(seed + 1).standard_normal((len(prefix), hq, nq, d)).astype(np.float16)
+    return case, cache, tuple(to_np(x) for x in cache), qv, prefix
+
+
+def _run(kind, case, cache, qv, prefix, tree_mask=None, window=None):
+    fn = ops.attn_paged_verify if kind == "int8" else ops.attn_paged_verify_k8v3
+    extra = () if kind == "int8" else (t(CODEBOOK),)
+    out = fn(t(qv), *cache, *extra, t(case.block_table), t(prefix.astype(np.int32)), case.block_size,
+             tree_mask=None if tree_mask is None else t(tree_mask), max_context_len=int(case.lens.max()),
+             scale=case.scale, window=window)
+    torch.cuda.synchronize()
+    return to_np(out.float())
+
+
+@pytest.mark.parametrize("kind,d,splits", [
+    ("int8", 128, 5), ("int8", 64, 3), ("int8", 256, 9), ("k8v3", 128, 7), ("k8v3", 256, 4),
+])
+def test_forced_split_matches_oracle_and_unsplit(kind, d, splits, monkeypatch):
+    case, cache, host, qv, prefix = _case(900 + d + splits, kind, 8, 2, d, 16, [3000, 517, 40], 6)
+    ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale)
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "1")
+    whole = _run(kind, case, cache, qv, prefix)
+    assert_close(whole, ref, f"{kind} D={d} unsplit")
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    split = _run(kind, case, cache, qv, prefix)
+    assert_close(split, ref, f"{kind} D={d} {splits} splits")
+    assert_close(split, whole.astype(np.float64), f"{kind} D={d} {splits} splits vs unsplit")
+
+
+@pytest.mark.parametrize("splits", [2, 31, 200])
+def test_split_tree_and_empty_splits(splits, monkeypatch):
+    """Tree masks across splits; 200 splits of a few hundred keys leave most
+    splits of the short rows without keys."""
+    nq = 12
+    case, cache, host, qv, prefix = _case(950 + splits, "int8", 16, 4, 128, 32, [4096, 33, 0, 700], nq)
+    rng = np.random.default_rng(951)
+    tm = np.stack([_random_tree(rng, nq) for _ in range(len(prefix))])
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    got = _run("int8", case, cache, qv, prefix, tree_mask=tm)
+    ref = O.paged_verify(qv, layer("int8", host), case.block_table, prefix, case.scale, tree_mask=tm)
+    assert_close(got, ref, f"tree verify, {splits} splits")
+
+
+@pytest.mark.parametrize("kind", ["int8", "k8v3"])
+def test_split_window_verify(kind, monkeypatch):
+    case, cache, host, qv, prefix = _case(960, kind, 8, 2, 128, 16, [5000, 300], 5)
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "6")
+    got = _run(kind, case, cache, qv, prefix, window=1024)
+    ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, window=1024)
+    assert_close(got, ref, f"{kind} window verify, 6 splits")
+
+
+def test_batch_one_long_context_plans_a_split():
+    """Batch 1 with a 32K prefix and a 32-node tree at Qwen3-8B heads has 16
+    units: the default plan splits them and the result matches the oracle."""
+    nq = 32
+    ws = _lib.load().s8kv_verify_workspace_size(1, 32, 8, 128, nq, 32768 + nq)
+    assert ws > 0
+    case, cache, host, qv, prefix = _case(970, "int8", 32, 8, 128, 256, [32768], nq)
+    tm = _random_tree(np.random.default_rng(971), nq)[None]
+    got = _run("int8", case, cache, qv, prefix, tree_mask=tm)
+    ref = O.paged_verify(qv, layer("int8", host), case.block_table, prefix, case.scale, tree_mask=tm)
+    assert_close(got, ref, "batch-1 tree verify (planned split)")
+
+
+def test_split_graph_replays(monkeypatch):
+    """Both launches of a split verify captured in a HIP graph: every replay
+    returns the eager result."""
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "8")
+    case, cache, host, qv, prefix = _case(980, "int8", 8, 2, 128, 16, [2000, 900], 4)
+    eager = _run("int8", case, cache, qv, prefix)
+    q, bt, pl = t(qv), t(case.block_table), t(prefix.astype(np.int32))
+    mc = int(case.lens.max())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.attn_paged_verify(q, *cache, bt, pl, case.block_size, max_context_len=mc, scale=case.scale)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.attn_paged_verify(q, *cache, bt, pl, case.block_size, max_context_len=mc, scale=case.scale)
+    for _ in range(3):
+        torch.zeros(1 << 20, device="cuda").add_(1.0)  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_np(out.float()), eager)
