@@ -498,8 +498,12 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         vsc[s] = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * s + 4 * g);
         if constexpr (C::NB == 2) vsc1[s] = *reinterpret_cast<const float4_t*>(sb + 2 * kTile + 16 * s + 4 * g);
       }
-      // The weight shift: a V scale above the bound lowers esh (WeightShift),
-      // tested with the running max's (row group 0's branch).  Each lane tests
+      // Rescales are rare: a V scale above the bound lowers esh (WeightShift),
+      // a tile max past the running max by more than the slack raises it.
+      // Both are decided first, and the rest of the tile (weights, PV) is
+      // instantiated with and without the rescale: as a branch inside one
+      // instance, the compiler copied every accumulator register on the
+      // common path to merge the two.  For the V-scale test each lane checks
       // one of the tile's (1 + NB) * 32 staged scales -- lane (g, c) the scale
       // of key 16 ((c >> 2) & 1) + 4 g + (c & 3), of block c >> 3 when there
       // are two -- so the 64 lanes cover them all.
@@ -522,127 +526,143 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           m_ref[r] -= (float)d;
         }
       };
-      half8_t pbh[RG], pbl[RG], pbh1[RG], pbl1[RG];  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
+      // key kk of the tile visible to this lane's row of group rg (MASKED only)
+      auto visible = [&](int rg, int s, int i) -> bool {
+        const int kk = base + 16 * s + 4 * g + i;
+        const int di = kk - prefix;  // draft index when >= 0
+        bool vis = kk < kv_end && row_live[rg] && (!WIN || kk >= (DENSE ? prefix + pos[rg] - a.window : lo_key));
+        if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask[rg] >> di) & 1ull)) : di <= pos[rg]);
+        return vis;
+      };
+      float y[RG][2][4];  // score relative to the running max, log2 domain
+      bool any = false;   // some row group (or the V-scale bound) needs a rescale
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
-        // key kk of the tile visible to this lane's row of group rg (MASKED only)
-        auto visible = [&](int s, int i) -> bool {
-          const int kk = base + 16 * s + 4 * g + i;
-          const int di = kk - prefix;  // draft index when >= 0
-          bool vis = kk < kv_end && row_live[rg] && (!WIN || kk >= (DENSE ? prefix + pos[rg] - a.window : lo_key));
-          if (di >= 0) vis = vis && (tree ? (di < 64 && ((tmask[rg] >> di) & 1ull)) : di <= pos[rg]);
-          return vis;
-        };
-        float y[2][4];  // score relative to the running max, log2 domain
         float my = kNegInf;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_ref[rg]);
-            if constexpr (MASKED) v = visible(s, i) ? v : kNegInf;
-            y[s][i] = v;
+            if constexpr (MASKED) v = visible(rg, s, i) ? v : kNegInf;
+            y[rg][s][i] = v;
             my = fmaxf(my, v);
           }
         }
         my = max_x16(my);
         my = max_x32(my);
-        if (__builtin_amdgcn_ballot_w64(my > ws.thr() || (rg == 0 && vp > ws.vbound())) != 0) {
-          if (rg == 0) shift_weights();
-          // raise the running max to the tile's (from the products, exactly),
-          // rescale, and take the scores relative to the new max
-          float mt = kNegInf;
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float x = sc[rg][s][i] * ksc[s][i];
-              if constexpr (MASKED) x = visible(s, i) ? x : kNegInf;
-              mt = fmaxf(mt, x);
-            }
-          }
-          mt = max_x16(mt);
-          mt = max_x32(mt);
-          const float m_new = fmaxf(m_ref[rg], mt - (float)ws.esh);
-          const float alpha = __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
-          l_run[rg] *= alpha;
-#pragma unroll
-          for (int n = 0; n < C::NPV; ++n) acc[rg][n] *= alpha;
-          m_ref[rg] = m_new;
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_new);
-              if constexpr (MASKED) v = visible(s, i) ? v : kNegInf;
-              y[s][i] = v;
-            }
-          }
-        }
-        // weights p * (V scale | block norm) as fp16 hi + lo: hi keeps the
-        // weight's top 11 significant bits (exact in fp16 for weights in
-        // fp16's normal range), lo the exact fp32 rest
-        float wh[2][4], wl[2][4], wh1[2][4], wl1[2][4];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(y[s][i]);  // 0 for masked keys
-            l_run[rg] += e;
-            // masked keys: e = 0, but their scale (past the visible keys, or
-            // below a window) may be any value, inf and NaN included
-            // (materialized: hi and lo must both come from this one fp32 value,
-            // not from a product the compiler contracts into the lo subtraction)
-            float w = materialize(e * vsc[s][i]);
-            if constexpr (MASKED) w = (y[s][i] != kNegInf) ? w : 0.0f;
-            wh[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & 0xFFFFE000u);
-            wl[s][i] = w - wh[s][i];
-            if constexpr (C::NB == 2) {
-              float w1 = materialize(e * vsc1[s][i]);
-              if constexpr (MASKED) w1 = (y[s][i] != kNegInf) ? w1 : 0.0f;
-              wh1[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w1) & 0xFFFFE000u);
-              wl1[s][i] = w1 - wh1[s][i];
-            }
-          }
-        }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-#pragma unroll
-          for (int i = 0; i < 4; i += 2) {
-            const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh[s][i], wh[s][i + 1]));
-            const half2_t l2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl[s][i], wl[s][i + 1]));
-            pbh[rg][4 * s + i] = h2[0];
-            pbh[rg][4 * s + i + 1] = h2[1];
-            pbl[rg][4 * s + i] = l2[0];
-            pbl[rg][4 * s + i + 1] = l2[1];
-            if constexpr (C::NB == 2) {
-              const half2_t h21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh1[s][i], wh1[s][i + 1]));
-              const half2_t l21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl1[s][i], wl1[s][i + 1]));
-              pbh1[rg][4 * s + i] = h21[0];
-              pbh1[rg][4 * s + i + 1] = h21[1];
-              pbl1[rg][4 * s + i] = l21[0];
-              pbl1[rg][4 * s + i + 1] = l21[1];
-            }
-          }
-        }
+        any = any || __builtin_amdgcn_ballot_w64(my > ws.thr() || (rg == 0 && vp > ws.vbound())) != 0;
       }
-      // PV: each V^T operand read from LDS feeds the MFMAs of every row group
+      auto tail = [&](auto resc_tag) {
+        constexpr bool RESC = decltype(resc_tag)::value;
+        if constexpr (RESC) {
+          shift_weights();
 #pragma unroll
-      for (int n = 0; n < C::NPV; ++n) {
-        const int r0 = 8 * g + ((lane >> 2) & 3);
-        const int colb = (16 * n + 4 * (lane & 3)) * 2;
-        const i16x4_t lw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + r0 * C::VROW + colb));
-        const i16x4_t hw =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + (r0 + 4) * C::VROW + colb));
-        const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
-        const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-        const bool second = C::NB == 2 && 16 * n >= 128;  // dims 128..255 of a K8V3 head_dim-256 key
+          for (int rg = 0; rg < RG; ++rg) {
+            // raise the running max to the tile's (from the products, exactly;
+            // every row group, also one within the slack), rescale, and take
+            // the scores relative to the new max
+            float mt = kNegInf;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float x = sc[rg][s][i] * ksc[s][i];
+                if constexpr (MASKED) x = visible(rg, s, i) ? x : kNegInf;
+                mt = fmaxf(mt, x);
+              }
+            }
+            mt = max_x16(mt);
+            mt = max_x32(mt);
+            const float m_new = fmaxf(m_ref[rg], mt - (float)ws.esh);
+            const float alpha = __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
+            l_run[rg] *= alpha;
+#pragma unroll
+            for (int n = 0; n < C::NPV; ++n) acc[rg][n] *= alpha;
+            m_ref[rg] = m_new;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float v = __builtin_fmaf(sc[rg][s][i], ksc[s][i], -m_new);
+                if constexpr (MASKED) v = visible(rg, s, i) ? v : kNegInf;
+                y[rg][s][i] = v;
+              }
+            }
+          }
+        }
+        half8_t pbh[RG], pbl[RG], pbh1[RG], pbl1[RG];  // B of the PV MFMAs (pbh1 / pbl1: the second V block)
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
-          acc[rg][n] = mfma16x16x32(va, second ? pbh1[rg] : pbh[rg], acc[rg][n]);
-          acc[rg][n] = mfma16x16x32(va, second ? pbl1[rg] : pbl[rg], acc[rg][n]);
+          // weights p * (V scale | block norm) as fp16 hi + lo: hi keeps the
+          // weight's top 11 significant bits (exact in fp16 for weights in
+          // fp16's normal range), lo the exact fp32 rest
+          float wh[2][4], wl[2][4], wh1[2][4], wl1[2][4];
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float e = __builtin_amdgcn_exp2f(y[rg][s][i]);  // 0 for masked keys
+              l_run[rg] += e;
+              // masked keys: e = 0, but their scale (past the visible keys, or
+              // below a window) may be any value, inf and NaN included
+              // (materialized: hi and lo must both come from this one fp32 value,
+              // not from a product the compiler contracts into the lo subtraction)
+              float w = materialize(e * vsc[s][i]);
+              if constexpr (MASKED) w = (y[rg][s][i] != kNegInf) ? w : 0.0f;
+              wh[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & 0xFFFFE000u);
+              wl[s][i] = w - wh[s][i];
+              if constexpr (C::NB == 2) {
+                float w1 = materialize(e * vsc1[s][i]);
+                if constexpr (MASKED) w1 = (y[rg][s][i] != kNegInf) ? w1 : 0.0f;
+                wh1[s][i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w1) & 0xFFFFE000u);
+                wl1[s][i] = w1 - wh1[s][i];
+              }
+            }
+          }
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+              const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh[s][i], wh[s][i + 1]));
+              const half2_t l2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl[s][i], wl[s][i + 1]));
+              pbh[rg][4 * s + i] = h2[0];
+              pbh[rg][4 * s + i + 1] = h2[1];
+              pbl[rg][4 * s + i] = l2[0];
+              pbl[rg][4 * s + i + 1] = l2[1];
+              if constexpr (C::NB == 2) {
+                const half2_t h21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh1[s][i], wh1[s][i + 1]));
+                const half2_t l21 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl1[s][i], wl1[s][i + 1]));
+                pbh1[rg][4 * s + i] = h21[0];
+                pbh1[rg][4 * s + i + 1] = h21[1];
+                pbl1[rg][4 * s + i] = l21[0];
+                pbl1[rg][4 * s + i + 1] = l21[1];
+              }
+            }
+          }
         }
-      }
+        // PV: each V^T operand read from LDS feeds the MFMAs of every row group
+#pragma unroll
+        for (int n = 0; n < C::NPV; ++n) {
+          const int r0 = 8 * g + ((lane >> 2) & 3);
+          const int colb = (16 * n + 4 * (lane & 3)) * 2;
+          const i16x4_t lw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + r0 * C::VROW + colb));
+          const i16x4_t hw =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(vb + (r0 + 4) * C::VROW + colb));
+          const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
+          const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+          const bool second = C::NB == 2 && 16 * n >= 128;  // dims 128..255 of a K8V3 head_dim-256 key
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            acc[rg][n] = mfma16x16x32(va, second ? pbh1[rg] : pbh[rg], acc[rg][n]);
+            acc[rg][n] = mfma16x16x32(va, second ? pbl1[rg] : pbl[rg], acc[rg][n]);
+          }
+        }
+      };
+      if (any)
+        tail(std::true_type{});
+      else
+        tail(std::false_type{});
     };
 
     // Tiles alternate between two LDS buffers; their global loads are issued
