@@ -244,6 +244,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   float m_ref[RG], l_run[RG];  // m_ref: running max - esh (WeightShift)
   float4_t acc[RG][C::NPV];
   WeightShift ws(kMaxSlack);
+  if constexpr (DENSE) ws.raise(1.0f, kMaxSlack);  // fp16 K / V: every V scale is 1
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
     m_ref[rg] = kMaxInit;
@@ -507,8 +508,9 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       // one of the tile's (1 + NB) * 32 staged scales -- lane (g, c) the scale
       // of key 16 ((c >> 2) & 1) + 4 g + (c & 3), of block c >> 3 when there
       // are two -- so the 64 lanes cover them all.
+      // (dense inputs: unit scales, the shift set once before the key loop)
       const int pk = 16 * ((c >> 2) & 1) + 4 * g + (c & 3);
-      float vp = sb[kTile * (1 + ((c >> 3) & (C::NB - 1))) + pk];
+      float vp = DENSE ? 0.0f : sb[kTile * (1 + ((c >> 3) & (C::NB - 1))) + pk];
       if constexpr (MASKED && WIN && !DENSE) vp = base + pk >= lo_key ? vp : 0.0f;  // below the window: any value
       auto shift_weights = [&]() {
         if (__builtin_amdgcn_ballot_w64(vp > ws.vbound()) == 0) return;
