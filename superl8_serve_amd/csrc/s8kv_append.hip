@@ -12,18 +12,43 @@ namespace s8kv {
 
 constexpr int kAppendWaves = 4;  // waves per workgroup
 
+// Where a row's bytes go: through the tensor's buffer descriptor at a 32-bit
+// offset (per-layer tensors up to 4 GiB), or through a 64-bit pointer (the
+// <.., BIG> kernels, a tensor past 4 GiB; rows are checked against the pool
+// before any store).  `off` is relative to the row's first byte.
+struct BufOut {
+  rsrc_t r;
+  uint32_t base;
+  __device__ void st128(uint32_t off, u32x4_t v) const { bstore128(v, r, base + off); }
+  __device__ void st32(uint32_t off, uint32_t v) const { bstore32(v, r, base + off); }
+  __device__ void st8(uint32_t off, uint8_t v) const { bstore8(v, r, base + off); }
+};
+struct PtrOut {
+  char* p;
+  __device__ void st128(uint32_t off, u32x4_t v) const { *reinterpret_cast<u32x4_t*>(p + off) = v; }
+  __device__ void st32(uint32_t off, uint32_t v) const { *reinterpret_cast<uint32_t*>(p + off) = v; }
+  __device__ void st8(uint32_t off, uint8_t v) const { p[off] = (char)v; }
+};
+template <bool BIG>
+__device__ __forceinline__ auto row_out(void* base, uint32_t bytes, uint64_t off) {
+  if constexpr (BIG)
+    return PtrOut{static_cast<char*>(base) + off};
+  else
+    return BufOut{make_rsrc(base, bytes), (uint32_t)off};
+}
+
 // Per-row RTN int8 of the wave's row; writes D bytes at `byte_off` and the scale.
-template <int D>
-__device__ __forceinline__ void rtn_store_row(const float (&y)[RowLayout<D>::E], int lane, rsrc_t qbuf,
-                                              uint32_t byte_off, rsrc_t sbuf, uint32_t scale_off) {
+template <int D, class QOut, class SOut>
+__device__ __forceinline__ void rtn_store_row(const float (&y)[RowLayout<D>::E], int lane, const QOut& qout,
+                                              const SOut& sout) {
   constexpr int E = RowLayout<D>::E;
   int q[E];
   const float scale = rtn_row<D>(y, q);
   if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
-    for (int j = 0; j < E; ++j) bstore8((uint8_t)(int8_t)q[j], qbuf, byte_off + lane + 64 * j);
+    for (int j = 0; j < E; ++j) qout.st8((uint32_t)(lane + 64 * j), (uint8_t)(int8_t)q[j]);
   }
-  if (lane == 0) bstore32(__builtin_bit_cast(uint32_t, scale), sbuf, scale_off);
+  if (lane == 0) sout.st32(0u, __builtin_bit_cast(uint32_t, scale));
 }
 
 struct AppendArgs {
@@ -39,12 +64,13 @@ struct AppendArgs {
   void* v_scale;   // fp32 V scale (int8) or fp32 V norms (k8v3)
   const float* v_codebook;
   uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
+  int big;  // a tensor past 4 GiB: the <.., BIG> kernels store through 64-bit pointers
   int64_t num_blocks;
   int block_size_log2;
   float rot_norm;  // float32(1/sqrt(D))
 };
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool BIG>
 __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a) {
   constexpr int E = RowLayout<D>::E;
   const int lane = threadIdx.x & 63;
@@ -61,11 +87,6 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
   const uint32_t off = (uint32_t)slot & (uint32_t)(bs - 1);
   const uint32_t row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) + off;
 
-  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
-  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
-  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
-  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
-
   // both rows' loads in flight together
   float x[E], y[E];
   load_row_f16<D>(a.k + t * a.k_stride_t + h * a.k_stride_h, x, lane);
@@ -75,11 +96,13 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
   fwht_row<D>(x, lane);
 #pragma unroll
   for (int j = 0; j < E; ++j) x[j] = (float)(_Float16)materialize(x[j] * a.rot_norm);
-  rtn_store_row<D>(x, lane, kc, row * (uint32_t)D, ks, row * 4u);
+  rtn_store_row<D>(x, lane, row_out<BIG>(a.k_cache, a.kc_bytes, (uint64_t)row * D),
+                   row_out<BIG>(a.k_scale, a.ks_bytes, (uint64_t)row * 4u));
 
   // ---- V ----
   if constexpr (!K8V3) {
-    rtn_store_row<D>(y, lane, vc, row * (uint32_t)D, vs, row * 4u);
+    rtn_store_row<D>(y, lane, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * D),
+                     row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * 4u));
   } else {
     static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
     constexpr int NB = D / 128;   // Lloyd-Max blocks per row (lloyd_block = 128)
@@ -90,8 +113,9 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
     uint32_t w;
     float nv;
     lloydmax3_encode_row<D>(y, cb, lane, w, nv);
-    if (lane < WORDS) bstore32(w, vc, row * (uint32_t)(WORDS * 4) + lane * 4u);
-    if (lane < NB) bstore32(__builtin_bit_cast(uint32_t, nv), vs, row * (uint32_t)(NB * 4) + lane * 4u);
+    if (lane < WORDS) row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * (WORDS * 4)).st32(lane * 4u, w);
+    if (lane < NB)
+      row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * (NB * 4)).st32(lane * 4u, __builtin_bit_cast(uint32_t, nv));
   }
 }
 
@@ -103,9 +127,9 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
 // in-lane and h = 16 .. D/2 as lane ^ (h/16) butterflies: the stage order and
 // arithmetic of fwht_row, so the bytes equal the one-row-per-wave kernel's.
 // Needs 16-byte aligned K and V rows.
-template <int D>
-__device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, int li, rsrc_t qbuf,
-                                               uint32_t byte_off, rsrc_t sbuf, uint32_t scale_off) {
+template <int D, class QOut, class SOut>
+__device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, int li, const QOut& qout,
+                                               const SOut& sout) {
   constexpr int LPR = D / 16;
   float amax = 0.0f;
 #pragma unroll
@@ -123,8 +147,8 @@ __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, 
                           rtn_i8_biased(y[4 * k + 2], scale, rscale), rtn_i8_biased(y[4 * k + 3], scale, rscale));
   }
   if (live) {
-    bstore128(u32x4_t{w[0], w[1], w[2], w[3]}, qbuf, byte_off);
-    if (li == 0) bstore32(__builtin_bit_cast(uint32_t, scale), sbuf, scale_off);
+    qout.st128((uint32_t)li * 16u, u32x4_t{w[0], w[1], w[2], w[3]});
+    if (li == 0) sout.st32(0u, __builtin_bit_cast(uint32_t, scale));
   }
 }
 
@@ -147,9 +171,9 @@ __device__ __forceinline__ uint32_t shift_in_bit(uint32_t w, bool b) {
 // lloyd3_search when the codebook allows it, else by the sequential scan.
 // Lanes 2g and 2g + 1 hold elements 32g .. 32g + 31: each builds 16 bits of
 // the three bit-plane words 3g + b, and the even lane stores them.
-template <int D>
+template <int D, class VOut, class NOut>
 __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool live, int li, const float (&cb)[8],
-                                                     rsrc_t vbuf, uint32_t word_off, rsrc_t nbuf, uint32_t norm_off) {
+                                                     const VOut& vout, const NOut& nout) {
   float s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) s[i] = x[i] * x[i];
@@ -207,12 +231,12 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
   }
   if (live && (li & 1) == 0) {
 #pragma unroll
-    for (int b = 0; b < 3; ++b) bstore32(w[b], vbuf, word_off + (uint32_t)(li / 2) * 12u + 4u * b);
+    for (int b = 0; b < 3; ++b) vout.st32((uint32_t)(li / 2) * 12u + 4u * b, w[b]);
   }
-  if (live && (li & 7) == 0) bstore32(__builtin_bit_cast(uint32_t, nrm), nbuf, norm_off + (uint32_t)(li / 8) * 4u);
+  if (live && (li & 7) == 0) nout.st32((uint32_t)(li / 8) * 4u, __builtin_bit_cast(uint32_t, nrm));
 }
 
-template <int D, bool K8V3>
+template <int D, bool K8V3, bool BIG>
 __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendArgs a) {
   constexpr int LPR = D / 16;  // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave
@@ -232,11 +256,6 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendAr
     row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) +
           ((uint32_t)slot & ((1u << a.block_size_log2) - 1u));
   }
-  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
-  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
-  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
-  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
-
   // both row parts' loads in flight together
   float x[16], y[16];
   {
@@ -288,22 +307,25 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendAr
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) x[i] = (float)(_Float16)materialize(x[i] * a.rot_norm);
-  rows_rtn_store<D>(x, live, li, kc, row * (uint32_t)D + (uint32_t)li * 16u, ks, row * 4u);
+  rows_rtn_store<D>(x, live, li, row_out<BIG>(a.k_cache, a.kc_bytes, (uint64_t)row * D),
+                    row_out<BIG>(a.k_scale, a.ks_bytes, (uint64_t)row * 4u));
 
   // ---- V: RTN, or 3-bit Lloyd-Max ----
   if constexpr (!K8V3) {
-    rows_rtn_store<D>(y, live, li, vc, row * (uint32_t)D + (uint32_t)li * 16u, vs, row * 4u);
+    rows_rtn_store<D>(y, live, li, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * D),
+                      row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * 4u));
   } else {
     static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
     float cb[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
-    rows_lloydmax3_store<D>(y, live, li, cb, vc, row * (uint32_t)(D / 32 * 3 * 4), vs, row * (uint32_t)(D / 128 * 4));
+    rows_lloydmax3_store<D>(y, live, li, cb, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * (D / 32 * 3 * 4)),
+                            row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * (D / 128 * 4)));
   }
 }
 
-template <bool K8V3>
-static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) {
+template <bool K8V3, bool BIG>
+static int launch_append_impl(const AppendArgs& a, int head_dim, hipStream_t stream) {
   const int64_t rows = a.num_tokens * a.num_kv_heads;
   if (rows == 0) return S8KV_OK;
   const bool rows16 = ((uintptr_t)a.k % 16 == 0) && ((uintptr_t)a.v % 16 == 0) && a.k_stride_t % 8 == 0 &&
@@ -315,13 +337,13 @@ static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) 
     dim3 g((unsigned)grid), b(64 * kAppendWaves);
     switch (head_dim) {
       case 32:
-        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<32, false>), g, b, 0, stream, a); break; }
+        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<32, false, BIG>), g, b, 0, stream, a); break; }
         return S8KV_ERR_UNSUPPORTED;
       case 64:
-        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<64, false>), g, b, 0, stream, a); break; }
+        if constexpr (!K8V3) { hipLaunchKernelGGL((append_rows_kernel<64, false, BIG>), g, b, 0, stream, a); break; }
         return S8KV_ERR_UNSUPPORTED;
-      case 128: hipLaunchKernelGGL((append_rows_kernel<128, K8V3>), g, b, 0, stream, a); break;
-      case 256: hipLaunchKernelGGL((append_rows_kernel<256, K8V3>), g, b, 0, stream, a); break;
+      case 128: hipLaunchKernelGGL((append_rows_kernel<128, K8V3, BIG>), g, b, 0, stream, a); break;
+      case 256: hipLaunchKernelGGL((append_rows_kernel<256, K8V3, BIG>), g, b, 0, stream, a); break;
       default: return S8KV_ERR_UNSUPPORTED;
     }
     return check_launch(K8V3 ? "s8kv_append_k8v3" : "s8kv_append_int8");
@@ -331,16 +353,21 @@ static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) 
   dim3 g((unsigned)grid), b(64 * kAppendWaves);
   switch (head_dim) {
     case 32:
-      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<32, false>), g, b, 0, stream, a); break; }
+      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<32, false, BIG>), g, b, 0, stream, a); break; }
       return S8KV_ERR_UNSUPPORTED;
     case 64:
-      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<64, false>), g, b, 0, stream, a); break; }
+      if constexpr (!K8V3) { hipLaunchKernelGGL((append_kernel<64, false, BIG>), g, b, 0, stream, a); break; }
       return S8KV_ERR_UNSUPPORTED;
-    case 128: hipLaunchKernelGGL((append_kernel<128, K8V3>), g, b, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((append_kernel<256, K8V3>), g, b, 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((append_kernel<128, K8V3, BIG>), g, b, 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((append_kernel<256, K8V3, BIG>), g, b, 0, stream, a); break;
     default: return S8KV_ERR_UNSUPPORTED;
   }
   return check_launch(K8V3 ? "s8kv_append_k8v3" : "s8kv_append_int8");
+}
+
+template <bool K8V3>
+static int launch_append(const AppendArgs& a, int head_dim, hipStream_t stream) {
+  return a.big ? launch_append_impl<K8V3, true>(a, head_dim, stream) : launch_append_impl<K8V3, false>(a, head_dim, stream);
 }
 
 static int common_append_checks(const void* k, const void* v, int64_t num_tokens, int num_kv_heads, int head_dim,
@@ -366,7 +393,7 @@ extern "C" int s8kv_append_int8(const void* k, const void* v, int64_t num_tokens
   int rc = common_append_checks(k, v, num_tokens, num_kv_heads, head_dim, slot_mapping, num_blocks, block_size);
   if (rc) return rc;
   const int64_t rows = num_blocks * num_kv_heads * block_size;
-  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "append: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE(fits_u32(rows), S8KV_ERR_UNSUPPORTED, "append: more than 2^32 cache rows per layer");
   S8KV_REQUIRE(k_cache && k_scale && v_cache && v_scale, S8KV_ERR_INVALID, "append: null cache pointer");
   AppendArgs a{};
   a.k = (const _Float16*)k;
@@ -377,10 +404,11 @@ extern "C" int s8kv_append_int8(const void* k, const void* v, int64_t num_tokens
   a.v_stride_t = v_stride_t; a.v_stride_h = v_stride_h;
   a.slot_mapping = slot_mapping;
   a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_cache; a.v_scale = v_scale;
-  a.kc_bytes = (uint32_t)(rows * head_dim);
-  a.vc_bytes = (uint32_t)(rows * head_dim);
-  a.ks_bytes = (uint32_t)(rows * 4);
-  a.vs_bytes = (uint32_t)(rows * 4);
+  a.big = !fits_u32(rows * head_dim);
+  a.kc_bytes = cap_u32((uint64_t)(rows * head_dim));
+  a.vc_bytes = cap_u32((uint64_t)(rows * head_dim));
+  a.ks_bytes = cap_u32((uint64_t)(rows * 4));
+  a.vs_bytes = cap_u32((uint64_t)(rows * 4));
   a.num_blocks = num_blocks;
   a.block_size_log2 = log2i(block_size);
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
@@ -400,7 +428,7 @@ extern "C" int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens
   S8KV_REQUIRE(k_cache && k_scale && v_packed && v_norm && v_codebook, S8KV_ERR_INVALID,
                "append_k8v3: null cache pointer");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
-  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "append_k8v3: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE(fits_u32(rows), S8KV_ERR_UNSUPPORTED, "append_k8v3: more than 2^32 cache rows per layer");
   AppendArgs a{};
   a.k = (const _Float16*)k;
   a.v = (const _Float16*)v;
@@ -411,10 +439,11 @@ extern "C" int s8kv_append_k8v3(const void* k, const void* v, int64_t num_tokens
   a.slot_mapping = slot_mapping;
   a.k_cache = k_cache; a.k_scale = k_scale; a.v_cache = v_packed; a.v_scale = v_norm;
   a.v_codebook = v_codebook;
-  a.kc_bytes = (uint32_t)(rows * head_dim);
-  a.ks_bytes = (uint32_t)(rows * 4);
-  a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
-  a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
+  a.big = !fits_u32(rows * head_dim);
+  a.kc_bytes = cap_u32((uint64_t)(rows * head_dim));
+  a.ks_bytes = cap_u32((uint64_t)(rows * 4));
+  a.vc_bytes = cap_u32((uint64_t)(rows * (head_dim / 32 * 3) * 4));
+  a.vs_bytes = cap_u32((uint64_t)(rows * (head_dim / 128) * 4));
   a.num_blocks = num_blocks;
   a.block_size_log2 = log2i(block_size);
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));

@@ -154,6 +154,10 @@ struct DecodeArgs {
   const void* v_scale;   // fp32 V scale or fp32 V norms
   const float* v_codebook;
   uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
+  // the tensors' full sizes; decode_kernel<.., BIG> (a tensor past 4 GiB,
+  // block_size >= 32) addresses each tile through a descriptor rebased to it
+  uint64_t kc_total, ks_total, vc_total, vs_total;
+  int big;
   const int32_t* block_table;
   int64_t bt_stride;
   const int32_t* context_lens;
@@ -336,7 +340,7 @@ struct TileIO {
   float4_t vs[2][C::NB];
 };
 
-template <int D, bool K8V3, bool FUSE, bool WIN = false>
+template <int D, bool K8V3, bool FUSE, bool WIN = false, bool BIG = false>
 __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kernel(DecodeArgs a) {
   static_assert(!(FUSE && WIN), "the sliding-window form has no fused append");
   using C = DecCfg<D, K8V3>;
@@ -657,6 +661,28 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
       TileIO<D, K8V3> io;
       auto issue_kv = [&](int tb, uint32_t r0) {
+        if constexpr (BIG) {  // the tile through descriptors rebased to its first row (block_size >= 32)
+          const rsrc_t kt = window_rsrc(a.k_cache, a.kc_total, (uint64_t)r0 * D);
+#pragma unroll
+          for (int s = 0; s < 2; ++s) load_kchunk<C::KCH>(kt, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s]);
+          if constexpr (!K8V3) {
+            const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * D);
+#pragma unroll
+            for (int jj = 0; jj < C::VLOADS; ++jj)
+              io.v[jj] = bload128(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
+          } else {
+            const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (C::WORDS * 4));
+#pragma unroll
+            for (int jj = 0; jj < C::VLOADS; ++jj) {
+              const int job = jj * 64 + lane;
+              const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
+              io.v[jj].x = bload32(vt, off);
+              io.v[jj].y = bload32(vt, off + 4);
+              io.v[jj].z = bload32(vt, off + 8);
+            }
+          }
+          return;
+        }
         if (tile_in_block) {
 #pragma unroll
           for (int s = 0; s < 2; ++s)
@@ -702,6 +728,23 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         }
       };
       auto issue_scales = [&](int tb, uint32_t r0) {
+        if constexpr (BIG) {
+          const rsrc_t kst = window_rsrc(a.k_scale, a.ks_total, (uint64_t)r0 * 4u);
+          const rsrc_t vst = window_rsrc(a.v_scale, a.vs_total, (uint64_t)r0 * (C::NB * 4u));
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const uint32_t row = (uint32_t)(16 * s + 4 * g);
+            io.ks[s] = bloadf4(kst, row * 4u);
+            if constexpr (C::NB == 1) {
+              io.vs[s][0] = bloadf4(vst, row * 4u);
+            } else {
+              const float4_t n0 = bloadf4(vst, row * 8u), n1 = bloadf4(vst, row * 8u + 16u);
+              io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
+              io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
+            }
+          }
+          return;
+        }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           uint32_t row, so;
@@ -984,17 +1027,26 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             for (int e = 0; e < E; ++e) x[e] = (float)(_Float16)materialize(x[e] * a.rot_norm);
             int qk[E];
             const float sk = rtn_row<D>(x, qk);
-            const uint32_t nrow = tile_in_block ? tile_row0(tb) + (uint32_t)(last - tb) : row_of(last);
+            uint32_t nrow = tile_in_block ? tile_row0(tb) + (uint32_t)(last - tb) : row_of(last);
+            // (BIG: descriptors rebased to the new token's row, which then is row 0)
+            rsrc_t kc_n = kc, ks_n = ks, vc_n = vc, vs_n = vs;
+            if constexpr (BIG) {
+              kc_n = window_rsrc(a.k_cache, a.kc_total, (uint64_t)nrow * D);
+              ks_n = window_rsrc(a.k_scale, a.ks_total, (uint64_t)nrow * 4u);
+              vc_n = window_rsrc(a.v_cache, a.vc_total, (uint64_t)nrow * (K8V3 ? C::WORDS * 4 : D));
+              vs_n = window_rsrc(a.v_scale, a.vs_total, (uint64_t)nrow * (C::NB * 4u));
+              nrow = 0;
+            }
             char* nn = smem + a.smem_new;
             if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
               for (int e = 0; e < E; ++e) {
-                bstore8((uint8_t)(int8_t)qk[e], kc, nrow * (uint32_t)D + lane + 64 * e);
+                bstore8((uint8_t)(int8_t)qk[e], kc_n, nrow * (uint32_t)D + lane + 64 * e);
                 nn[C::NEW_I8K + lane + 64 * e] = (char)qk[e];
               }
             }
             if (lane == 0) {
-              bstore32(__builtin_bit_cast(uint32_t, sk), ks, nrow * 4u);
+              bstore32(__builtin_bit_cast(uint32_t, sk), ks_n, nrow * 4u);
               *reinterpret_cast<float*>(nn + C::NEW_KS) = sk;
             }
             if constexpr (!K8V3) {
@@ -1003,12 +1055,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
               if (lane < RowLayout<D>::ACTIVE) {
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
-                  bstore8((uint8_t)(int8_t)qv[e], vc, nrow * (uint32_t)D + lane + 64 * e);
+                  bstore8((uint8_t)(int8_t)qv[e], vc_n, nrow * (uint32_t)D + lane + 64 * e);
                   nn[C::NEW_V + lane + 64 * e] = (char)qv[e];
                 }
               }
               if (lane == 0) {
-                bstore32(__builtin_bit_cast(uint32_t, sv), vs, nrow * 4u);
+                bstore32(__builtin_bit_cast(uint32_t, sv), vs_n, nrow * 4u);
                 *reinterpret_cast<float*>(nn + C::NEW_VS) = sv;
               }
             } else {  // 3-bit Lloyd-Max V: packed words and per-128 block norms
@@ -1019,11 +1071,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
               float nv;
               lloydmax3_encode_row<D>(y, cb, lane, w, nv);
               if (lane < C::WORDS) {
-                bstore32(w, vc, nrow * (uint32_t)(C::WORDS * 4) + lane * 4u);
+                bstore32(w, vc_n, nrow * (uint32_t)(C::WORDS * 4) + lane * 4u);
                 reinterpret_cast<uint32_t*>(nn + C::NEW_V)[lane] = w;
               }
               if (lane < C::NB) {
-                bstore32(__builtin_bit_cast(uint32_t, nv), vs, nrow * (uint32_t)(C::NB * 4) + lane * 4u);
+                bstore32(__builtin_bit_cast(uint32_t, nv), vs_n, nrow * (uint32_t)(C::NB * 4) + lane * 4u);
                 reinterpret_cast<float*>(nn + C::NEW_VS)[lane] = nv;
               }
             }
@@ -1233,8 +1285,8 @@ static int plan_wg_per_head(int num_kv_heads, int resident_per_cu) {
   return w < 1 ? 1 : (w > cap ? cap : w);
 }
 
-template <int D, bool K8V3, bool FUSE, bool WIN = false>
-static int launch_decode(DecodeArgs& a, hipStream_t stream) {
+template <int D, bool K8V3, bool FUSE, bool WIN, bool BIG>
+static int launch_decode_impl(DecodeArgs& a, hipStream_t stream) {
   using C = DecCfg<D, K8V3>;
   constexpr int kNewBytes = FUSE ? C::NEW_BYTES : 0;  // fused append: the new token's rows
   const auto smem_main_for = [](int group) {  // V staging + rotated q, or the cross-wave merge
@@ -1250,7 +1302,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   static int resident_by_group[17] = {};
   static bool lds_raised = false;
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3, FUSE, WIN>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, K8V3, FUSE, WIN, BIG>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             smem_main_for(16) + (kMaxSubBlocks + kLensLds) * 4 + kNewBytes) != hipSuccess) {
       set_error("s8kv_decode: cannot raise the dynamic LDS limit");
@@ -1261,7 +1313,7 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
   int& resident = resident_by_group[a.group];
   if (resident == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3, FUSE, WIN>, 64 * kDecWaves, smem) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<D, K8V3, FUSE, WIN, BIG>, 64 * kDecWaves, smem) != hipSuccess ||
         n <= 0)
       n = 2;
     resident = n < kMaxResidentPerCU ? n : kMaxResidentPerCU;
@@ -1292,11 +1344,16 @@ static int launch_decode(DecodeArgs& a, hipStream_t stream) {
 #endif
   hipEvent_t* ev = a.untimed ? nullptr : timing_slot(stream);
   if (ev) {  // events stamped with the kernel's own start and end times
-    hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
+    hipExtLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN, BIG>), grid, dim3(64 * kDecWaves), smem, stream, ev[0], ev[1], 0, a);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN>), grid, dim3(64 * kDecWaves), smem, stream, a);
+    hipLaunchKernelGGL((decode_kernel<D, K8V3, FUSE, WIN, BIG>), grid, dim3(64 * kDecWaves), smem, stream, a);
   }
   return check_launch("s8kv_decode");
+}
+template <int D, bool K8V3, bool FUSE, bool WIN = false>
+static int launch_decode(DecodeArgs& a, hipStream_t stream) {
+  return a.big ? launch_decode_impl<D, K8V3, FUSE, WIN, true>(a, stream)
+               : launch_decode_impl<D, K8V3, FUSE, WIN, false>(a, stream);
 }
 
 // Workspace: (max, sum) and unnormalised output partials of every (q head,
@@ -1335,20 +1392,24 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
                S8KV_ERR_INVALID, "decode: null pointer argument");
   S8KV_REQUIRE(!fuse || (a.k_new && a.v_new), S8KV_ERR_INVALID, "decode_append: null k_new / v_new");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
-  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "decode: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE(fits_u32(rows), S8KV_ERR_UNSUPPORTED, "decode: more than 2^32 cache rows per layer");
+  // a tensor past 4 GiB: tiles through descriptors rebased per tile, which
+  // needs tiles inside one block
+  a.big = !fits_u32(rows * head_dim);
+  S8KV_REQUIRE(!a.big || block_size >= 32, S8KV_ERR_UNSUPPORTED,
+               "decode: a per-layer cache past 4 GiB needs block_size >= 32 (got %d)", block_size);
   a.batch = batch;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
-  a.kc_bytes = (uint32_t)(rows * head_dim);
-  a.ks_bytes = (uint32_t)(rows * 4);
-  if (k8v3) {
-    a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
-    a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
-  } else {
-    a.vc_bytes = (uint32_t)(rows * head_dim);
-    a.vs_bytes = (uint32_t)(rows * 4);
-  }
+  a.kc_total = (uint64_t)(rows * head_dim);
+  a.ks_total = (uint64_t)(rows * 4);
+  a.vc_total = (uint64_t)(k8v3 ? rows * (head_dim / 32 * 3) * 4 : rows * head_dim);
+  a.vs_total = (uint64_t)(k8v3 ? rows * (head_dim / 128) * 4 : rows * 4);
+  a.kc_bytes = cap_u32(a.kc_total);  // (BIG: unused by the tiles)
+  a.ks_bytes = cap_u32(a.ks_total);
+  a.vc_bytes = cap_u32(a.vc_total);
+  a.vs_bytes = cap_u32(a.vs_total);
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));

@@ -34,6 +34,13 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// Pools past 4 GiB: a descriptor over a tensor's bytes from the wave-uniform
+// 64-bit offset `off` on (at most 4 GiB - 1 of them, none past the end), so a
+// tile's or a row's accesses keep 32-bit offsets from a base rebased per tile.
+__device__ __forceinline__ rsrc_t window_rsrc(const void* base, uint64_t total, uint64_t off) {
+  const uint64_t rem = off < total ? total - off : 0;
+  return make_rsrc(static_cast<const char*>(base) + off, (uint32_t)(rem < 0xFFFFFFFFull ? rem : 0xFFFFFFFFull));
+}
 // `off` is the per-lane (VGPR) byte offset, `soff` a wave-uniform (SGPR) one.
 __device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off, uint32_t soff = 0) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));

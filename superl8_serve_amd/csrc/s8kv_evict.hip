@@ -31,7 +31,7 @@ struct ScoreArgs {
   // paged int8 K (one sequence): its block ids in order
   const void* k_cache;
   const void* k_scale;
-  uint32_t kc_bytes, ks_bytes;
+  int64_t num_blocks;
   const int32_t* block_row;
   int bs_log2;
   // dense K [Hkv][n][D]
@@ -78,14 +78,18 @@ __global__ __launch_bounds__(64 * kWaves) void snapkv_logits_kernel(ScoreArgs a)
   const int t = blockIdx.x * kTok + lane;
   if (t >= a.n) return;
   float kscale = 1.0f;
-  uint32_t row = 0;
-  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);  // dense: unused (size 0)
-  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const char* krow = nullptr;  // paged: the token's int8 K row (64-bit addressing: pools past 4 GiB)
   if constexpr (PAGED) {
     const uint32_t bsm = (1u << a.bs_log2) - 1u;
     const uint32_t blk = (uint32_t)a.block_row[t >> a.bs_log2];
-    row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.bs_log2) + ((uint32_t)t & bsm);
-    kscale = __builtin_bit_cast(float, bload32(ks, row * 4u));
+    if ((int64_t)blk < a.num_blocks) {  // a block id outside the pool scores as a zero key
+      const uint64_t row = ((uint64_t)blk * (uint32_t)a.num_kv_heads + (uint32_t)h) * (1u << a.bs_log2) +
+                           ((uint32_t)t & bsm);
+      kscale = reinterpret_cast<const float*>(a.k_scale)[row];
+      krow = static_cast<const char*>(a.k_cache) + row * D;
+    } else {
+      kscale = 0.0f;
+    }
   }
   constexpr int kMaxHeads = 16;  // q heads per wave: G <= 64
   float acc[kMaxHeads];
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(64 * kWaves) void snapkv_logits_kernel(ScoreArgs a)
     if constexpr (PAGED) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const u32x4_t w = bload128(kc, row * (uint32_t)D + (uint32_t)(c + 16 * p));
+        const u32x4_t w = krow ? *reinterpret_cast<const u32x4_t*>(krow + c + 16 * p) : u32x4_t{0u, 0u, 0u, 0u};
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 16; ++i) kv[16 * p + i] = (float)(int8_t)(ws[i / 4] >> (8 * (i % 4)));
@@ -275,8 +279,7 @@ extern "C" int s8kv_snapkv_scores_paged(const void* q, int q_is_f32, int64_t q_s
   S8KV_REQUIRE(is_pow2(block_size) && block_size >= 4, S8KV_ERR_UNSUPPORTED,
                "snapkv_scores_paged: block_size %d must be a power of two >= 4", block_size);
   S8KV_REQUIRE(q_stride >= head_dim && num_blocks > 0, S8KV_ERR_INVALID, "snapkv_scores_paged: bad q stride or pool");
-  const int64_t rows = num_blocks * num_kv_heads * block_size;
-  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "snapkv_scores_paged: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE((uintptr_t)k_cache % 16 == 0, S8KV_ERR_INVALID, "snapkv_scores_paged: k_cache not 16-byte aligned");
   a.q = q;
   a.q_f32 = q_is_f32 ? 1 : 0;
   a.q_stride = q_stride;
@@ -284,8 +287,7 @@ extern "C" int s8kv_snapkv_scores_paged(const void* q, int q_is_f32, int64_t q_s
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
   a.k_cache = k_cache;
   a.k_scale = k_scale;
-  a.kc_bytes = (uint32_t)(rows * head_dim);
-  a.ks_bytes = (uint32_t)(rows * 4);
+  a.num_blocks = num_blocks;
   a.block_row = block_row;
   a.bs_log2 = log2i(block_size);
   return evict::dispatch_scores<true>(a, head_dim, (hipStream_t)stream);

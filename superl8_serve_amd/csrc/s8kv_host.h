@@ -30,6 +30,8 @@ inline bool head_dim_ok(int d) { return d == 32 || d == 64 || d == 128 || d == 2
 
 // Bytes of a per-layer cache tensor must fit the 32-bit buffer-descriptor range.
 inline bool fits_u32(int64_t bytes) { return bytes >= 0 && bytes < (int64_t(1) << 32); }
+// A byte count as a buffer descriptor's 32-bit size (4 GiB - 1 at most).
+inline uint32_t cap_u32(uint64_t n) { return (uint32_t)(n < 0xFFFFFFFFull ? n : 0xFFFFFFFFull); }
 
 inline int check_launch(const char* what) {
   hipError_t e = hipGetLastError();

@@ -87,6 +87,10 @@ struct VerifyArgs {
   const float* v_scale;       // int8 V scales, or K8V3 block norms
   const float* v_codebook;    // K8V3: fp32 [8]
   uint32_t kc_bytes, ks_bytes, vc_bytes, vs_bytes;
+  // the tensors' full sizes; verify_kernel<.., BIG> (a tensor past 4 GiB,
+  // block_size >= 32) loads each tile through descriptors rebased to it
+  uint64_t kc_total, ks_total, vc_total, vs_total;
+  int big;
   const int32_t* block_table;
   int64_t bt_stride;
   const int32_t* prefix_lens;
@@ -124,9 +128,10 @@ struct VerifyArgs {
 // transpose-read rows (keys 4g..4g+3 and 16+4g..16+4g+3) are rows 8g..8g+7.
 __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
+template <int D, bool K8V3, bool WIN = false, bool DENSE = false, bool BIG = false>
 __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   static_assert(!DENSE || !K8V3, "dense inputs: fp16 K / V");
+  static_assert(!DENSE || !BIG, "dense inputs are not paged");
   using C = Cfg<D, K8V3>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
@@ -316,6 +321,40 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
           }
         }
         R.s = 1.0f;
+        return;
+      }
+      if constexpr (BIG) {  // one block holds the tile (block_size >= 32): descriptors rebased to its first row
+        const uint32_t r0 = __builtin_amdgcn_readfirstlane(row_of(base));
+        auto local = [&](int tt) -> uint32_t { return (uint32_t)(min(base + tt, u1 - 1) - base); };
+        const rsrc_t kt = window_rsrc(a.k_cache, a.kc_total, (uint64_t)r0 * D);
+        const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (K8V3 ? C::WORDS * 4 : D));
+        const rsrc_t kst = window_rsrc(a.k_scale, a.ks_total, (uint64_t)r0 * 4u);
+        const rsrc_t vst = window_rsrc(a.v_scale, a.vs_total, (uint64_t)r0 * (C::NB * 4u));
+#pragma unroll
+        for (int i = 0; i < C::LOADS; ++i) {
+          const int ch = tid + i * kThreads;
+          if (ch < C::CHUNKS) {
+            const int tt = ch / (D / 16), part = ch % (D / 16);
+            const uint32_t off = local(tt) * (uint32_t)D + (uint32_t)part * 16u;
+            R.k[i] = bload128(kt, off);
+            if constexpr (!K8V3) R.v[i] = bload128(vt, off);
+          }
+        }
+        if constexpr (K8V3) {
+          if (tid < C::VJOBS) {
+            const int grp = tid / C::SPLIT;
+            const int tt = grp / C::NG, gi = grp % C::NG;
+            const uint32_t off = local(tt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
+            R.v[0].x = bload32(vt, off);
+            R.v[0].y = bload32(vt, off + 4);
+            R.v[0].z = bload32(vt, off + 8);
+          }
+        }
+        if (tid < (1 + C::NB) * kTile) {
+          const uint32_t lr = local(tid & (kTile - 1));
+          const int nb = tid / kTile - 1;
+          R.s = __builtin_bit_cast(float, bload32(nb < 0 ? kst : vst, nb < 0 ? lr * 4u : (lr * C::NB + nb) * 4u));
+        }
         return;
       }
 #pragma unroll
@@ -804,13 +843,13 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
   *reinterpret_cast<half4_t*>(a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D + 4 * c4) = o;
 }
 
-template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
-static int launch(VerifyArgs& a, hipStream_t stream) {
+template <int D, bool K8V3, bool WIN, bool DENSE, bool BIG>
+static int launch_impl(VerifyArgs& a, hipStream_t stream) {
   static_assert(Cfg<D, K8V3>::ROWS == 16 * kWaves * (D <= 64 ? 2 : 1), "rows_per_wg");
   using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN, DENSE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_kernel<D, K8V3, WIN, DENSE, BIG>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, WIN ? C::SMEM_WIN : C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -823,7 +862,7 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE>), dim3((unsigned)grid), dim3(kThreads),
+  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE, BIG>), dim3((unsigned)grid), dim3(kThreads),
                      WIN ? C::SMEM_WIN : C::SMEM, stream, a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
@@ -834,6 +873,14 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
     return check_launch("s8kv_verify_combine");
   }
   return check_launch("s8kv_verify");
+}
+template <int D, bool K8V3, bool WIN = false, bool DENSE = false>
+static int launch(VerifyArgs& a, hipStream_t stream) {
+  if constexpr (DENSE)
+    return launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
+  else
+    return a.big ? launch_impl<D, K8V3, WIN, DENSE, true>(a, stream)
+                 : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
 }  // namespace verify
@@ -921,7 +968,12 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   S8KV_REQUIRE(q && k_cache && k_scale && block_table && prefix_lens && out, S8KV_ERR_INVALID,
                "verify: null pointer argument");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
-  S8KV_REQUIRE(fits_u32(rows * head_dim), S8KV_ERR_UNSUPPORTED, "verify: per-layer cache exceeds 4 GiB");
+  S8KV_REQUIRE(fits_u32(rows), S8KV_ERR_UNSUPPORTED, "verify: more than 2^32 cache rows per layer");
+  // a tensor past 4 GiB: tiles through descriptors rebased per tile, which
+  // needs tiles inside one block
+  a.big = !fits_u32(rows * head_dim);
+  S8KV_REQUIRE(!a.big || block_size >= 32, S8KV_ERR_UNSUPPORTED,
+               "verify: a per-layer cache past 4 GiB needs block_size >= 32 (got %d)", block_size);
   a.q = (const _Float16*)q;
   a.q_stride_b = q_stride_b;
   a.q_stride_h = q_stride_h;
@@ -933,8 +985,10 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.max_queries = max_queries;
   a.k_cache = k_cache;
   a.k_scale = k_scale;
-  a.kc_bytes = (uint32_t)(rows * head_dim);
-  a.ks_bytes = (uint32_t)(rows * 4);
+  a.kc_total = (uint64_t)(rows * head_dim);
+  a.ks_total = (uint64_t)(rows * 4);
+  a.kc_bytes = cap_u32(a.kc_total);  // (BIG: unused by the tiles)
+  a.ks_bytes = cap_u32(a.ks_total);
   a.block_table = block_table;
   a.bt_stride = block_table_stride;
   a.prefix_lens = prefix_lens;
@@ -985,6 +1039,8 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   S8KV_REQUIRE(v_cache && v_scale, S8KV_ERR_INVALID, "verify: null pointer argument");
   a.v_cache = v_cache;
   a.v_scale = v_scale;
+  a.vc_total = a.kc_total;
+  a.vs_total = a.ks_total;
   a.vc_bytes = a.kc_bytes;
   a.vs_bytes = a.ks_bytes;
   hipStream_t s = (hipStream_t)stream;
@@ -1077,8 +1133,10 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.v_cache = v_packed;
   a.v_scale = v_norm;
   a.v_codebook = v_codebook;
-  a.vc_bytes = (uint32_t)(rows * (head_dim / 32 * 3) * 4);
-  a.vs_bytes = (uint32_t)(rows * (head_dim / 128) * 4);
+  a.vc_total = (uint64_t)(rows * (head_dim / 32 * 3) * 4);
+  a.vs_total = (uint64_t)(rows * (head_dim / 128) * 4);
+  a.vc_bytes = cap_u32(a.vc_total);
+  a.vs_bytes = cap_u32(a.vs_total);
   hipStream_t s = (hipStream_t)stream;
   if (a.window > 0)
     return head_dim == 128 ? verify::launch<128, true, true>(a, s) : verify::launch<256, true, true>(a, s);

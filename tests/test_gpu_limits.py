@@ -7,11 +7,12 @@
 * One sequence of 2^18 tokens beside short rows, split across every
   workgroup and recombined: decode, the fused decode-append and a chunk
   verify against the oracle.
-* Pools just under the 4 GiB a buffer descriptor addresses: rows whose blocks
-  sit at the top of the pool, on both sides of the 2 GiB byte offset and at
-  the bottom, against the oracle on a compact copy of those blocks; and one
-  sequence through every block of such a pool (33,554,176 tokens) whose
-  output has a closed form.
+* Pools just under the 4 GiB one buffer descriptor addresses, and 6 GiB pools
+  (addressed through descriptors rebased per tile, and 64-bit pointers for
+  appends): rows whose blocks sit at the top of the pool, on both sides of
+  byte offset 2^31 or 2^32 and at the bottom, against the oracle on a compact
+  copy of those blocks; and one sequence through every block of such a pool
+  (33,554,176 or 50,331,648 tokens) whose output has a closed form.
 
 The caches are filled by the GPU append (bit-exact against the oracle in
 test_gpu_kernels.py and again here) and read back for the oracle."""
@@ -28,11 +29,6 @@ from tests.kvcase import empty_int8_cache, empty_k8v3_cache, make_case, make_nee
 from tests.kvgpu import CODEBOOK, DEV, KINDS, alloc, append, assert_close, decode, decode_append, layer, t, to_np, verify
 
 pytestmark = pytest.mark.gpu
-
-
-def _pool_blocks(hkv, bs, d):
-    """The largest block count whose int8 K pool stays under 4 GiB."""
-    return ((1 << 32) - 1) // (hkv * bs * d)
 
 
 def _oracle_fill(kind, case, keep=None):
@@ -162,26 +158,43 @@ def test_one_long_sequence(kind):
 # 4 GiB pools
 # ---------------------------------------------------------------------------
 
+def _edge_ids(case, nblk, specials, rng):
+    """Compact block -> pool block: the longest row's last block (its new
+    token) is the pool's last, the next used blocks take `specials`, the rest
+    random free blocks."""
+    bs = case.block_size
+    need = (case.lens + bs - 1) // bs
+    ids = np.full(case.num_blocks, -1, np.int64)
+    ids[case.block_table[0, need[0] - 1]] = nblk - 1
+    used = [int(case.block_table[b, i]) for b in range(case.batch) for i in range(need[b])]
+    rest = [c for c in used if ids[c] < 0]
+    for c, blk in zip(rest, specials):
+        ids[c] = blk
+    ids[ids < 0] = rng.choice(np.setdiff1d(np.arange(nblk), ids[ids >= 0]), int((ids < 0).sum()), replace=False)
+    return ids
+
+
+# (pool blocks, pool blocks of interest) at Hkv 2, block 256, D 128 (64 KiB of K per block)
+POOLS = {
+    "under_4gib": (65535, (32768, 32767, 0, 65533, 1)),            # 4,294,901,760 K bytes; blocks at 2 GiB
+    "6gib": (98304, (65536, 65535, 32768, 0, 98302)),              # 6 GiB: blocks on either side of 4 GiB
+}
+
+
+@pytest.mark.parametrize("pool", sorted(POOLS))
 @pytest.mark.parametrize("kind", KINDS)
-def test_rows_at_the_top_of_a_4gib_pool(kind):
-    """Rows of a 65535-block pool (Hkv 2, block 256, D 128: 4,294,901,760 K
-    bytes) whose blocks are the pool's last (holding the longest row's new
-    token), the two on either side of byte offset 2^31, the first, and random
-    others; checked against the oracle on a compact copy of those blocks."""
+def test_rows_at_the_edges_of_a_large_pool(kind, pool):
+    """Rows of a pool just under 4 GiB (one buffer descriptor spans it) and of
+    a 6 GiB pool (tiles through descriptors rebased per tile, appends through
+    64-bit pointers) whose blocks are the pool's last (holding the longest
+    row's new token), the blocks on either side of byte offset 2^31 or 2^32,
+    the first, and random others; append, fused decode-append, decode and
+    chunk verify against the oracle on a compact copy of those blocks."""
     hq, hkv, d, bs, nq = 8, 2, 128, 256, 8
-    nblk = _pool_blocks(hkv, bs, d)
-    half = (1 << 31) // (hkv * bs * d)  # the first block at or past 2 GiB
+    nblk, specials = POOLS[pool]
     lens = np.array([2000, 300, 257, 9])
     case = make_case(730, len(lens), hq, hkv, d, bs, lens, outlier_channels=2)
-    need = (lens + bs - 1) // bs
-    ids = np.full(case.num_blocks, -1, np.int64)  # compact block -> pool block
-    ids[case.block_table[0, need[0] - 1]] = nblk - 1
-    used = [int(case.block_table[b, i]) for b in range(len(lens)) for i in range(need[b])]
-    rest = [c for c in used if ids[c] < 0]
-    for c, blk in zip(rest, (half, half - 1, 0, nblk - 2, 1)):
-        ids[c] = blk
-    rng = np.random.default_rng(731)
-    ids[ids < 0] = rng.choice(np.setdiff1d(np.arange(nblk), ids[ids >= 0]), int((ids < 0).sum()), replace=False)
+    ids = _edge_ids(case, nblk, specials, np.random.default_rng(731))
     bt = ids[case.block_table].astype(np.int32)
     slots = (ids[case.slots // bs] * bs + case.slots % bs).astype(np.int32)
 
@@ -192,39 +205,69 @@ def test_rows_at_the_top_of_a_4gib_pool(kind):
         q, btt, cl = t(case.q), t(bt), t(lens.astype(np.int32))
         max_ctx = int(lens.max())
         fused = to_np(decode_append(kind, q, t(k_new), t(v_new), cache, btt, cl, bs, max_ctx, case.scale).float())
-        gather = t(ids)
-        compact = tuple(to_np(x.index_select(0, gather)) for x in cache)
-        _assert_same_bytes(compact, _oracle_fill(kind, case), f"{kind} 4 GiB pool")
+        compact = tuple(to_np(x.index_select(0, t(ids))) for x in cache)
+        _assert_same_bytes(compact, _oracle_fill(kind, case), f"{kind} {pool} pool")
         out = to_np(decode(kind, q, cache, btt, cl, bs, max_ctx, case.scale).float())
         assert np.array_equal(fused, out), "fused decode-append differs from append + decode"
         lc = layer(kind, compact)
-        assert_close(out, O.paged_decode(case.q, lc, case.block_table, lens, case.scale), f"{kind} 4 GiB pool decode")
+        assert_close(out, O.paged_decode(case.q, lc, case.block_table, lens, case.scale), f"{kind} {pool} decode")
         prefix = lens - nq
         qv = np.random.default_rng(732).standard_normal((len(lens), hq, nq, d)).astype(np.float16)
         got = verify(kind, t(qv), cache, btt, t(prefix.astype(np.int32)), None, bs, max_ctx, case.scale)
         ref = O.paged_verify(qv, lc, case.block_table, prefix, case.scale)
-        assert_close(to_np(got.float()), ref, f"{kind} 4 GiB pool verify")
+        assert_close(to_np(got.float()), ref, f"{kind} {pool} verify")
+        if pool == "6gib":  # SnapKV scores of the longest row, whose blocks include the pool's last
+            need = (int(lens[0]) + bs - 1) // bs
+            qs = torch.randn(hq, d, generator=torch.Generator(device=DEV).manual_seed(733), device=DEV)
+            got = to_np(ops.snapkv_scores_paged(qs, cache[0], cache[1], bt[0, :need].tolist(), int(lens[0]), hq))
+            want = O.snapkv_scores_paged(to_np(qs), O.LayerCache(compact[0], compact[1]),
+                                         case.block_table[0, :need], int(lens[0]), hq)
+            assert np.max(np.abs(got - want) / np.maximum(want, 1e-30)) < 2e-4
     finally:
         del cache
         torch.cuda.empty_cache()
 
 
-def _whole_pool():
-    """One sequence over every block of the largest int8 pool under 4 GiB at
-    Hkv 1, block 256, D 128 (131071 blocks, 33,554,176 tokens), in a shuffled
-    block order whose last position is the pool's final row.  Background keys
-    are zero (score 0) with one constant V row; eight needle keys, one per q
-    head, sit at the pool's first and last rows, on either side of byte offset
-    2^31, at the sequence's first position and elsewhere.  Head h scores its
+def test_large_pool_needs_blocks_of_32():
+    """Past 4 GiB per tensor the decode and verify rebase a descriptor per
+    tile, which needs tiles inside one block: block_size 16 is refused."""
+    hkv, d, bs = 2, 128, 16
+    nblk = (1 << 32) // (hkv * bs * d) + 1
+    cache = alloc("int8", nblk, hkv, bs, d)
+    try:
+        q = torch.zeros((1, 8, 1, d), dtype=torch.float16, device=DEV)
+        bt = torch.zeros((1, 1), dtype=torch.int32, device=DEV)
+        cl = torch.ones(1, dtype=torch.int32, device=DEV)
+        with pytest.raises(RuntimeError, match="block_size >= 32"):
+            ops.attn_paged_decode_cached(q, *cache, bt, cl, bs, max_context_len=1, scale=0.1)
+        with pytest.raises(RuntimeError, match="block_size >= 32"):
+            ops.attn_paged_verify(q, *cache, bt, torch.zeros(1, dtype=torch.int32, device=DEV), bs,
+                                  max_context_len=1, scale=0.1)
+    finally:
+        del cache
+        torch.cuda.empty_cache()
+
+
+WHOLE_POOLS = {"under_4gib": ((1 << 32) - 1) // (256 * 128), "6gib": 3 * (1 << 31) // (256 * 128)}
+
+
+def _whole_pool(nblk):
+    """One sequence over every block of an int8 pool of `nblk` blocks at Hkv 1,
+    block 256, D 128 (131071 blocks: the largest under 4 GiB; 196608: 6 GiB),
+    in a shuffled block order whose last position is the pool's final row.
+    Background keys are zero (score 0) with one constant V row; eight needle
+    keys, one per q head, sit at the pool's first and last rows, on either side
+    of byte offset 2^31 and of 2^32 (or near the end of a smaller pool), at the
+    sequence's first position and elsewhere.  Head h scores its
     needle near ln(n) and the others near 0, so needle and background carry
     comparable weight and the output has a closed form (pinned against the
     oracle on a small pool in test_limit_cases.py).
     Returns the case and its cache tensors (k, k_scale, v, v_scale)."""
     hq, d, bs = 8, 128, 256
-    nblk = _pool_blocks(1, bs, d)
     half = (1 << 31) // (bs * d)  # the first block at or past 2 GiB
-    nc = make_needle_case(740, nblk, bs, d, hq, [(0, 0), (half, 0), (half - 1, bs - 1), (3 * half // 2, 128),
-                                                 (half // 2, 17)])
+    top = min(2 * half, nblk - 1)  # the first block at or past 4 GiB, when the pool reaches it
+    nc = make_needle_case(740, nblk, bs, d, hq, [(0, 0), (half, 0), (half - 1, bs - 1), (top, 128),
+                                                 (top - 1, 17)])
     assert nc.rows[0] == nblk * bs - 1
     kc = torch.zeros((nblk, 1, bs, d), dtype=torch.int8, device=DEV)
     ks = torch.full((nblk, 1, bs), 1 / 128, dtype=torch.float32, device=DEV)
@@ -238,10 +281,11 @@ def _whole_pool():
     return nc, [kc, ks, vc, vs]
 
 
-def test_decode_through_a_whole_4gib_pool():
+@pytest.mark.parametrize("pool", sorted(WHOLE_POOLS))
+def test_decode_through_a_whole_pool(pool):
     """Decode over the whole-pool sequence, then the fused decode-append
     rewriting its last position (the pool's final row)."""
-    nc, cache = _whole_pool()
+    nc, cache = _whole_pool(WHOLE_POOLS[pool])
     try:
         kc, ks, vc, vs = cache
         n, d, bs = nc.n, nc.head_dim, nc.block_size
@@ -269,12 +313,13 @@ def test_decode_through_a_whole_4gib_pool():
         torch.cuda.empty_cache()
 
 
-def test_chain_verify_through_a_whole_4gib_pool():
+@pytest.mark.parametrize("pool", sorted(WHOLE_POOLS))
+def test_chain_verify_through_a_whole_pool(pool):
     """A 4-query chain verify of the whole-pool sequence's last positions:
     query s sees positions [0, n - 4 + s].  The single query block's 33.5M
     keys are split across workgroups (no workgroup accumulates more than 2^20
     in fp32, whose rounding would otherwise drift past the tolerance)."""
-    nc, cache = _whole_pool()
+    nc, cache = _whole_pool(WHOLE_POOLS[pool])
     try:
         kc, ks, vc, vs = cache
         n, d, bs, hq, nq = nc.n, nc.head_dim, nc.block_size, len(nc.pos), 4
