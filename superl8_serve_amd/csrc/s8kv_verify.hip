@@ -804,6 +804,14 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
   const int pos = r / G;
   if (pos >= a.max_queries) return;
   const int head = h * G + (r - pos * G);
+  half4_t* const op = reinterpret_cast<half4_t*>(a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D +
+                                                 4 * c4);
+  // rows past the sequence's query count are zeros, as the unsplit kernel writes them
+  const int nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
+  if (pos >= nq) {
+    *op = half4_t{0, 0, 0, 0};
+    return;
+  }
   const int S = a.splits;
   const int64_t stride = (int64_t)ROWS * (D + 4);  // between splits of one row
   const float* row = a.part + ((int64_t)pq * S * ROWS + rl) * (D + 4);
@@ -840,7 +848,7 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
   half4_t o;
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(num[rr] * inv);
-  *reinterpret_cast<half4_t*>(a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D + 4 * c4) = o;
+  *op = o;
 }
 
 template <int D, bool K8V3, bool WIN, bool DENSE, bool BIG>

@@ -37,10 +37,11 @@ def _case(seed, kind, hq, hkv, d, bs, prefix, nq):
     return case, cache, tuple(to_np(x) for x in cache), qv, prefix
 
 
-def _run(kind, case, cache, qv, prefix, tree_mask=None, window=None):
+def _run(kind, case, cache, qv, prefix, tree_mask=None, window=None, query_lens=None):
     fn = ops.attn_paged_verify if kind == "int8" else ops.attn_paged_verify_k8v3
     extra = () if kind == "int8" else (t(CODEBOOK),)
     out = fn(t(qv), *cache, *extra, t(case.block_table), t(prefix.astype(np.int32)), case.block_size,
+             query_lens=None if query_lens is None else t(np.asarray(query_lens, np.int32)),
              tree_mask=None if tree_mask is None else t(tree_mask), max_context_len=int(case.lens.max()),
              scale=case.scale, window=window)
     torch.cuda.synchronize()
@@ -74,6 +75,22 @@ def test_split_tree_and_empty_splits(splits, monkeypatch):
     got = _run("int8", case, cache, qv, prefix, tree_mask=tm)
     ref = O.paged_verify(qv, layer("int8", host), case.block_table, prefix, case.scale, tree_mask=tm)
     assert_close(got, ref, f"tree verify, {splits} splits")
+
+
+@pytest.mark.parametrize("kind,splits", [("int8", 4), ("int8", 1), ("k8v3", 7)])
+def test_split_query_lens(kind, splits, monkeypatch):
+    """Rows past a sequence's query count are zeros also when they share a
+    query block with live rows (G 4: positions 0-15 per 64-row block) and
+    the block's keys are split; the live rows match the oracle."""
+    nq = 24
+    ql = np.array([5, 24, 0, 17])
+    case, cache, host, qv, prefix = _case(990 + splits, kind, 16, 4, 128, 32, [3000, 2100, 1500, 2600], nq)
+    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    got = _run(kind, case, cache, qv, prefix, query_lens=ql)
+    ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, query_lens=ql)
+    for b, n in enumerate(ql):
+        assert not got[b, :, n:].any(), f"row {b}: outputs past its {n} queries"
+    assert_close(got, ref, f"{kind} verify with query_lens, {splits} splits")
 
 
 @pytest.mark.parametrize("kind", ["int8", "k8v3"])
