@@ -81,6 +81,7 @@ enum TraceSlot {
   kTrExit = 7,       // workgroup end
   kTrWork = 8,       // tokens processed | segments << 32
   kTrFlags = 9,      // 1 | last segment whole row << 8 | last segment combined its row << 9
+  kTrHwId = 10,      // the workgroup's XCC, shader engine and CU (__smid)
 };
 constexpr int kTraceWords = 16;
 #define S8KV_TRACE_STAMP(slot)                                                 \
@@ -320,12 +321,12 @@ __device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) 
 template <int KCH>
 __device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4], uint32_t soff = 0) {
   if constexpr (KCH == 8) {
-    u32x2_t v = bload64(r, off, soff);
+    u32x2_t v = bload64<kNT>(r, off, soff);
     dst[0] = v.x; dst[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < KCH / 16; ++i) {
-      u32x4_t v = bload128(r, off + 16 * i, soff);
+      u32x4_t v = bload128<kNT>(r, off + 16 * i, soff);
       dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
     }
   }
@@ -669,16 +670,16 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * D);
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
+              io.v[jj] = bload128<kNT>(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
           } else {
             const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (C::WORDS * 4));
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj) {
               const int job = jj * 64 + lane;
               const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-              io.v[jj].x = bload32(vt, off);
-              io.v[jj].y = bload32(vt, off + 4);
-              io.v[jj].z = bload32(vt, off + 8);
+              io.v[jj].x = bload32<kNT>(vt, off);
+              io.v[jj].y = bload32<kNT>(vt, off + 4);
+              io.v[jj].z = bload32<kNT>(vt, off + 8);
             }
           }
           return;
@@ -690,16 +691,16 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
           if constexpr (!K8V3) {
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
+              io.v[jj] = bload128<kNT>(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
           } else {
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj) {
               const int job = jj * 64 + lane;
               const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
               const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
-              io.v[jj].x = bload32(vc, off, so);
-              io.v[jj].y = bload32(vc, off + 4, so);
-              io.v[jj].z = bload32(vc, off + 8, so);
+              io.v[jj].x = bload32<kNT>(vc, off, so);
+              io.v[jj].y = bload32<kNT>(vc, off + 4, so);
+              io.v[jj].z = bload32<kNT>(vc, off + 8, so);
             }
           }
           return;
@@ -713,7 +714,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
           for (int jj = 0; jj < C::VLOADS; ++jj) {
             const uint32_t row = row_of(min(tb + jj * RPI + lane / LPR, last));
-            io.v[jj] = bload128(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
+            io.v[jj] = bload128<kNT>(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
           }
         } else {
 #pragma unroll
@@ -721,9 +722,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             const int job = jj * 64 + lane;
             const uint32_t row = row_of(min(tb + job / C::NG, last));
             const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
-            io.v[jj].x = bload32(vc, base);
-            io.v[jj].y = bload32(vc, base + 4);
-            io.v[jj].z = bload32(vc, base + 8);
+            io.v[jj].x = bload32<kNT>(vc, base);
+            io.v[jj].y = bload32<kNT>(vc, base + 4);
+            io.v[jj].z = bload32<kNT>(vc, base + 8);
           }
         }
       };
@@ -734,11 +735,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
             const uint32_t row = (uint32_t)(16 * s + 4 * g);
-            io.ks[s] = bloadf4(kst, row * 4u);
+            io.ks[s] = bloadf4<kNT>(kst, row * 4u);
             if constexpr (C::NB == 1) {
-              io.vs[s][0] = bloadf4(vst, row * 4u);
+              io.vs[s][0] = bloadf4<kNT>(vst, row * 4u);
             } else {
-              const float4_t n0 = bloadf4(vst, row * 8u), n1 = bloadf4(vst, row * 8u + 16u);
+              const float4_t n0 = bloadf4<kNT>(vst, row * 8u), n1 = bloadf4<kNT>(vst, row * 8u + 16u);
               io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
               io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
             }
@@ -755,11 +756,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
             so = 0;
           }
-          io.ks[s] = bloadf4(ks, row * 4u, so * 4u);
+          io.ks[s] = bloadf4<kNT>(ks, row * 4u, so * 4u);
           if constexpr (C::NB == 1) {
-            io.vs[s][0] = bloadf4(vs, row * 4u, so * 4u);
+            io.vs[s][0] = bloadf4<kNT>(vs, row * 4u, so * 4u);
           } else {
-            const float4_t n0 = bloadf4(vs, row * 8u, so * 8u), n1 = bloadf4(vs, row * 8u + 16u, so * 8u);
+            const float4_t n0 = bloadf4<kNT>(vs, row * 8u, so * 8u), n1 = bloadf4<kNT>(vs, row * 8u + 16u, so * 8u);
             io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
             io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
           }
@@ -1219,6 +1220,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #ifdef S8KV_DECODE_TRACE
   S8KV_TRACE_STAMP(kTrExit);
   S8KV_TRACE_SET(kTrWork, tr_tok | (tr_seg << 32));
+  S8KV_TRACE_SET(kTrHwId, (unsigned long long)__smid());
   __syncthreads();
   if (a.trace != nullptr && threadIdx.x < kTraceWords)
     a.trace[(int64_t)blockIdx.x * kTraceWords + threadIdx.x] = trace_lds[threadIdx.x];

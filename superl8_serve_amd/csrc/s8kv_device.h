@@ -42,17 +42,25 @@ __device__ __forceinline__ rsrc_t window_rsrc(const void* base, uint64_t total, 
   return make_rsrc(static_cast<const char*>(base) + off, (uint32_t)(rem < 0xFFFFFFFFull ? rem : 0xFFFFFFFFull));
 }
 // `off` is the per-lane (VGPR) byte offset, `soff` a wave-uniform (SGPR) one.
+// AUX is the cache-policy operand: 0, or kNT for data streamed once (the
+// loads are marked non-temporal, so they do not displace reused lines in the
+// caches; a read-only sweep over the decode's tiles reads ~12 % faster so).
+constexpr int kNT = 2;
+template <int AUX = 0>
 __device__ __forceinline__ u32x4_t bload128(rsrc_t r, uint32_t off, uint32_t soff = 0) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, AUX));
 }
+template <int AUX = 0>
 __device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off, uint32_t soff = 0) {
-  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, 0));
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, AUX));
 }
+template <int AUX = 0>
 __device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off, uint32_t soff = 0) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, AUX);
 }
+template <int AUX = 0>
 __device__ __forceinline__ float4_t bloadf4(rsrc_t r, uint32_t off, uint32_t soff = 0) {
-  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, AUX));
 }
 __device__ __forceinline__ void bstore128(u32x4_t v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, 0);

@@ -6,7 +6,8 @@
 // and V rows and their scales -- with the decode kernel's shape: about as
 // many 4-wave workgroups as stay resident, each taking an equal contiguous
 // share of the tile list, waves taking tiles in turn with the next tile's
-// loads in flight while the current one is folded into a checksum.
+// loads in flight while the current one is folded into a checksum; the loads
+// are non-temporal, as the decode kernel's.
 // s8kv_probe_read_linear reads one contiguous buffer the same way (16-byte
 // loads, four in flight per lane).  Each workgroup writes one checksum word,
 // so no load can be dropped.
@@ -43,11 +44,11 @@ __device__ __forceinline__ void load_tile(const TileProbeArgs& a, rsrc_t kc, rsr
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t off = row0 * 128u + (uint32_t)(i * 1024 + lane * 16);
-    r.k[i] = bload128(kc, off);
-    r.v[i] = bload128(vc, off);
+    r.k[i] = bload128<kNT>(kc, off);
+    r.v[i] = bload128<kNT>(vc, off);
   }
-  r.ks = bload32(ks, row0 * 4u + (uint32_t)(lane & 31) * 4u);
-  r.vs = bload32(vs, row0 * 4u + (uint32_t)(lane & 31) * 4u);
+  r.ks = bload32<kNT>(ks, row0 * 4u + (uint32_t)(lane & 31) * 4u);
+  r.vs = bload32<kNT>(vs, row0 * 4u + (uint32_t)(lane & 31) * 4u);
 }
 
 __device__ __forceinline__ uint32_t fold(const TileRegs& r) {
