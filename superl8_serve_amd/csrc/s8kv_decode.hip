@@ -109,6 +109,13 @@ constexpr int kTraceWords = 16;
 #endif
 
 constexpr int kDecWaves = 4;
+// Cache policy of the tile loads (K, V, scales): non-temporal for the int8
+// layout, whose loads read whole lines once (a read-only sweep over the
+// decode's tiles: 5.6 -> 6.3 TB/s); the default for K8V3, whose V words a
+// tile reads as three dword loads over the same lines (non-temporal there
+// measured 4-13 % slower).
+template <bool K8V3>
+constexpr int kTilePolicy = K8V3 ? 0 : kNT;
 constexpr int kTile = 32;
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kMaxSlack = 8.0f;                        // lazy softmax max: rescale only past this (log2 units)
@@ -318,15 +325,15 @@ __device__ __forceinline__ int row_stream_len(const DecodeArgs& a, const int* le
 // consecutive rows 8g..8g+7.
 __device__ __forceinline__ int lds_row_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
-template <int KCH>
+template <int KCH, int AUX>
 __device__ __forceinline__ void load_kchunk(rsrc_t r, uint32_t off, uint32_t (&dst)[KCH / 4], uint32_t soff = 0) {
   if constexpr (KCH == 8) {
-    u32x2_t v = bload64<kNT>(r, off, soff);
+    u32x2_t v = bload64<AUX>(r, off, soff);
     dst[0] = v.x; dst[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < KCH / 16; ++i) {
-      u32x4_t v = bload128<kNT>(r, off + 16 * i, soff);
+      u32x4_t v = bload128<AUX>(r, off + 16 * i, soff);
       dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
     }
   }
@@ -661,25 +668,26 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       };
 
       TileIO<D, K8V3> io;
+      constexpr int kPol = kTilePolicy<K8V3>;
       auto issue_kv = [&](int tb, uint32_t r0) {
         if constexpr (BIG) {  // the tile through descriptors rebased to its first row (block_size >= 32)
           const rsrc_t kt = window_rsrc(a.k_cache, a.kc_total, (uint64_t)r0 * D);
 #pragma unroll
-          for (int s = 0; s < 2; ++s) load_kchunk<C::KCH>(kt, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s]);
+          for (int s = 0; s < 2; ++s) load_kchunk<C::KCH, kPol>(kt, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s]);
           if constexpr (!K8V3) {
             const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * D);
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128<kNT>(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
+              io.v[jj] = bload128<kPol>(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
           } else {
             const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (C::WORDS * 4));
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj) {
               const int job = jj * 64 + lane;
               const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-              io.v[jj].x = bload32<kNT>(vt, off);
-              io.v[jj].y = bload32<kNT>(vt, off + 4);
-              io.v[jj].z = bload32<kNT>(vt, off + 8);
+              io.v[jj].x = bload32<kPol>(vt, off);
+              io.v[jj].y = bload32<kPol>(vt, off + 4);
+              io.v[jj].z = bload32<kPol>(vt, off + 8);
             }
           }
           return;
@@ -687,20 +695,20 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         if (tile_in_block) {
 #pragma unroll
           for (int s = 0; s < 2; ++s)
-            load_kchunk<C::KCH>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
+            load_kchunk<C::KCH, kPol>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
           if constexpr (!K8V3) {
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128<kNT>(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
+              io.v[jj] = bload128<kPol>(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
           } else {
 #pragma unroll
             for (int jj = 0; jj < C::VLOADS; ++jj) {
               const int job = jj * 64 + lane;
               const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
               const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
-              io.v[jj].x = bload32<kNT>(vc, off, so);
-              io.v[jj].y = bload32<kNT>(vc, off + 4, so);
-              io.v[jj].z = bload32<kNT>(vc, off + 8, so);
+              io.v[jj].x = bload32<kPol>(vc, off, so);
+              io.v[jj].y = bload32<kPol>(vc, off + 4, so);
+              io.v[jj].z = bload32<kPol>(vc, off + 8, so);
             }
           }
           return;
@@ -708,13 +716,13 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           const uint32_t row = row_of(min(tb + 16 * s + c, last));
-          load_kchunk<C::KCH>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
+          load_kchunk<C::KCH, kPol>(kc, row * (uint32_t)D + (uint32_t)(g * C::KCH), io.k[s]);
         }
         if constexpr (!K8V3) {
 #pragma unroll
           for (int jj = 0; jj < C::VLOADS; ++jj) {
             const uint32_t row = row_of(min(tb + jj * RPI + lane / LPR, last));
-            io.v[jj] = bload128<kNT>(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
+            io.v[jj] = bload128<kPol>(vc, row * (uint32_t)D + (uint32_t)((lane % LPR) * 16));
           }
         } else {
 #pragma unroll
@@ -722,9 +730,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             const int job = jj * 64 + lane;
             const uint32_t row = row_of(min(tb + job / C::NG, last));
             const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
-            io.v[jj].x = bload32<kNT>(vc, base);
-            io.v[jj].y = bload32<kNT>(vc, base + 4);
-            io.v[jj].z = bload32<kNT>(vc, base + 8);
+            io.v[jj].x = bload32<kPol>(vc, base);
+            io.v[jj].y = bload32<kPol>(vc, base + 4);
+            io.v[jj].z = bload32<kPol>(vc, base + 8);
           }
         }
       };
@@ -735,11 +743,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
             const uint32_t row = (uint32_t)(16 * s + 4 * g);
-            io.ks[s] = bloadf4<kNT>(kst, row * 4u);
+            io.ks[s] = bloadf4<kPol>(kst, row * 4u);
             if constexpr (C::NB == 1) {
-              io.vs[s][0] = bloadf4<kNT>(vst, row * 4u);
+              io.vs[s][0] = bloadf4<kPol>(vst, row * 4u);
             } else {
-              const float4_t n0 = bloadf4<kNT>(vst, row * 8u), n1 = bloadf4<kNT>(vst, row * 8u + 16u);
+              const float4_t n0 = bloadf4<kPol>(vst, row * 8u), n1 = bloadf4<kPol>(vst, row * 8u + 16u);
               io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
               io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
             }
@@ -756,11 +764,11 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
             so = 0;
           }
-          io.ks[s] = bloadf4<kNT>(ks, row * 4u, so * 4u);
+          io.ks[s] = bloadf4<kPol>(ks, row * 4u, so * 4u);
           if constexpr (C::NB == 1) {
-            io.vs[s][0] = bloadf4<kNT>(vs, row * 4u, so * 4u);
+            io.vs[s][0] = bloadf4<kPol>(vs, row * 4u, so * 4u);
           } else {
-            const float4_t n0 = bloadf4<kNT>(vs, row * 8u, so * 8u), n1 = bloadf4<kNT>(vs, row * 8u + 16u, so * 8u);
+            const float4_t n0 = bloadf4<kPol>(vs, row * 8u, so * 8u), n1 = bloadf4<kPol>(vs, row * 8u + 16u, so * 8u);
             io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
             io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
           }

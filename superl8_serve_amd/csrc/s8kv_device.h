@@ -62,14 +62,17 @@ template <int AUX = 0>
 __device__ __forceinline__ float4_t bloadf4(rsrc_t r, uint32_t off, uint32_t soff = 0) {
   return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, AUX));
 }
+template <int AUX = 0>
 __device__ __forceinline__ void bstore128(u32x4_t v, rsrc_t r, uint32_t off) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, AUX);
 }
+template <int AUX = 0>
 __device__ __forceinline__ void bstore32(uint32_t v, rsrc_t r, uint32_t off) {
-  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, AUX);
 }
+template <int AUX = 0>
 __device__ __forceinline__ void bstore8(uint8_t v, rsrc_t r, uint32_t off) {
-  __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, AUX);
 }
 
 // ---------------------------------------------------------------------------
