@@ -133,35 +133,47 @@ def build(device, layers: int = NUM_LAYERS, keep_prefix: bool = False):
     }
 
 
-def decode_layer(w, layer: int, fused: bool):
+def decode_layer(w, layer: int, fused: bool, plan=None):
     """One layer of the decode step: append the new token of every row, then
-    attend.  fused: one launch (attn_paged_decode_append); otherwise the
-    reference's two calls (quantize_kv_write_paged, attn_paged_decode_cached)."""
+    attend.  fused: one launch (attn_paged_decode_append, reading the step's
+    slice plan when one is given); otherwise the reference's two calls
+    (quantize_kv_write_paged, attn_paged_decode_cached)."""
     from superl8_serve_amd import ops
 
     scale = 1.0 / math.sqrt(D)
     if fused:
         return ops.attn_paged_decode_append(
             w["q"][layer], w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
-            w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
+            w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale, plan=plan)
     ops.quantize_kv_write_paged(w["k_new"][layer], w["v_new"][layer], w["kc"][layer], w["ks"][layer],
                                 w["vc"][layer], w["vs"][layer], w["new_sm"])
     return ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer],
                                         w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
 
 
-def make_step(w, fused: bool):
+def step_plan(w):
+    """The step's slice plan: one launch, shared by the 36 layers' launches
+    (every layer decodes the same rows)."""
+    from superl8_serve_amd import ops
+
+    return ops.attn_paged_decode_plan(w["kc"][0], w["bt"], w["cl"], BS, num_q_heads=HQ, max_context_len=MAX_LEN)
+
+
+def make_step(w, fused: bool, planned: bool = True):
+    """The 36-layer step; the fused form starts with the step's plan launch
+    when `planned`."""
     outs = [None] * NUM_LAYERS
 
     def step():
+        plan = step_plan(w) if fused and planned else None
         for layer in range(NUM_LAYERS):
-            outs[layer] = decode_layer(w, layer, fused)
+            outs[layer] = decode_layer(w, layer, fused, plan)
         return outs
 
     return step
 
 
-def time_decode_kernel(w, reps: int, fused: bool) -> dict:
+def time_decode_kernel(w, reps: int, fused: bool, planned: bool = True) -> dict:
     """Average duration of the decode attention kernel (which also combines
     the partials of rows split across workgroups), from HIP events the library
     records on the launch stream around each launch (s8kv_timing_begin/end),
@@ -177,13 +189,14 @@ def time_decode_kernel(w, reps: int, fused: bool) -> dict:
 
     lib = _lib.load()
     scale = 1.0 / math.sqrt(D)
+    plan = step_plan(w) if fused and planned else None
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2e8))  # ~0.1 s of GPU spin while the host enqueues
     _lib.check(lib.s8kv_timing_begin(), "s8kv_timing_begin")
     for _ in range(reps):
         for layer in range(NUM_LAYERS):
             if fused:
-                decode_layer(w, layer, True)
+                decode_layer(w, layer, True, plan)
             else:
                 ops.attn_paged_decode_cached(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer],
                                              w["vs"][layer], w["bt"], w["cl"], BS, max_context_len=MAX_LEN,
@@ -693,11 +706,12 @@ def k8v3_workload(dev, layers: int = NUM_LAYERS, keep_rows=()):
             "prefix_kv": kept}
 
 
-def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
+def run_k8v3(steps: int, warmup: int, fused: bool, planned: bool = True) -> None:
     """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
     36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
     needed, distinct storage per layer; one launch per layer
-    (attn_paged_decode_append_k8v3) unless `fused` is False."""
+    (attn_paged_decode_append_k8v3, after the step's one plan launch when
+    `planned`) unless `fused` is False."""
     import torch
 
     from superl8_serve_amd import ops
@@ -710,11 +724,13 @@ def run_k8v3(steps: int, warmup: int, fused: bool) -> None:
     scale = 1.0 / math.sqrt(D)
 
     def step():
+        plan = (ops.attn_paged_decode_plan(kc[0], btd, cl, BS, num_q_heads=HQ, max_context_len=max_ctx,
+                                           layout="k8v3") if fused and planned else None)
         for layer in range(NUM_LAYERS):
             if fused:
                 ops.attn_paged_decode_append_k8v3(q[layer], k_new[layer], v_new[layer], kc[layer], ks[layer],
                                                   vp[layer], vn[layer], cb, btd, cl, BS, max_context_len=max_ctx,
-                                                  scale=scale)
+                                                  scale=scale, plan=plan)
                 continue
             ops.quantize_kv_write_paged_k8v3(k_new[layer], v_new[layer], kc[layer], ks[layer], vp[layer], vn[layer],
                                              cb, new_sm)
@@ -996,6 +1012,8 @@ def main():
                     help="eager event-timed decode passes over the 36 layers (0 = skip, one-launch step only)")
     ap.add_argument("--ceiling-steps", type=int, default=5,
                     help="graph replays per read-ceiling probe (0 = skip the read-ceiling leg)")
+    ap.add_argument("--no-plan", action="store_true",
+                    help="fused step without the per-step slice plan (every launch locates its own work)")
     ap.add_argument("--separate-append", action="store_true",
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
@@ -1040,7 +1058,7 @@ def main():
         run_verify(args.workload.removesuffix("_k8v3"), args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
         return
     if args.workload == "k8v3":
-        run_k8v3(args.steps, args.warmup, not args.separate_append)
+        run_k8v3(args.steps, args.warmup, not args.separate_append, not args.no_plan)
         return
     if args.workload == "copy":
         run_copy(args.steps)
@@ -1058,7 +1076,8 @@ def main():
     device = "cuda"
     w = build(device)
     fused = not args.separate_append
-    step = make_step(w, fused)
+    planned = fused and not args.no_plan
+    step = make_step(w, fused, planned)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -1086,14 +1105,15 @@ def main():
     b = step_bytes(w["lens"])
     value = b["step"] / (ms * 1e-3) / 1e9
     # eager per-launch timing: required for the two-call step, a cross-check otherwise
-    kt = (time_decode_kernel(w, args.kernel_reps, fused) if args.kernel_reps > 0 or not fused
+    kt = (time_decode_kernel(w, args.kernel_reps, fused, planned) if args.kernel_reps > 0 or not fused
           else {"decode_s": None, "launches": 0})
     kernel = "decode_kernel<128, int8, fused append>" if fused else "decode_kernel<128, int8>"
     kernel_bytes = b["fused_layer"] if fused else b["decode_layer"]
-    # The one-launch step graph holds exactly NUM_LAYERS decode_kernel launches
-    # and nothing else, so the events around the timed replays give the
-    # kernel's average launch duration over the timed region (gaps between the
-    # back-to-back launches included).  The two-call step also runs the append
+    # The one-launch step graph holds NUM_LAYERS decode_kernel launches and
+    # (planned) the step's one plan launch, so the events around the timed
+    # replays give the kernel's average launch duration over the timed region
+    # (gaps between the back-to-back launches and the plan launch's share
+    # included).  The two-call step also runs the append
     # kernel, so there the library's per-launch events over eager passes time
     # the decode kernel alone.
     dec_s = ev_launch_s if fused else kt["decode_s"]
@@ -1125,6 +1145,8 @@ def main():
             "bytes_per_step": b["step"],
             "append": "in the decode launch (attn_paged_decode_append)" if fused
                       else "separate kernel (quantize_kv_write_paged)",
+            "slice_plan": "one attn_paged_decode_plan launch per step, read by the 36 launches" if planned
+                          else "none (every launch locates its own work)",
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "roofline": {

@@ -177,6 +177,53 @@ int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_k
                             void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Per-step slice plan of the decode launches.  No counterpart in the
+ * reference (its decode op locates its work per call); it serves the step
+ * the reference runs as one decode call per layer with the same block_table
+ * and context_lens (ModelRunner's decode step, gqa_attention.py:174-190).
+ * s8kv_decode_plan computes, from block_table and context_lens only, the
+ * split of the token stream over the decode workgroups and the storage rows
+ * of each workgroup's first tiles -- what every decode launch of the step
+ * would otherwise compute in its prologue -- into `plan` (device memory,
+ * 4-byte aligned, at least s8kv_decode_plan_size(num_kv_heads) bytes).
+ * layout: 0 int8, 1 K8V3; fused: 1 for the s8kv_decode_append_* launches.
+ * The other arguments are those of the decode launches the plan is for.
+ * Stream-ordered, no host synchronization, capturable.
+ */
+int64_t s8kv_decode_plan_size(int num_kv_heads);
+int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
+                     int64_t num_blocks, int block_size, const int32_t* block_table, int64_t block_table_stride,
+                     const int32_t* context_lens, int max_context_len, void* plan, int64_t plan_bytes, void* stream);
+
+/*
+ * s8kv_decode_append_int8 / s8kv_decode_append_k8v3 reading a plan made by
+ * s8kv_decode_plan for the same geometry and the same block_table and
+ * context_lens buffers, whose contents must not have changed since: the
+ * launch then issues its first K/V loads at once.  Same cache bytes and
+ * outputs as the unplanned calls (the plan holds exactly what their prologue
+ * computes).  A plan whose header names another geometry or other buffers is
+ * ignored (the launch locates its work itself).  Replace the same reference
+ * calls as the unplanned forms.
+ */
+int s8kv_decode_append_int8_planned(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                    int64_t k_new_stride_b, int64_t k_new_stride_h, const void* v_new,
+                                    int64_t v_new_stride_b, int64_t v_new_stride_h, int8_t* k_cache, float* k_scale,
+                                    int8_t* v_cache, float* v_scale, int64_t num_blocks, int block_size,
+                                    const int32_t* block_table, int64_t block_table_stride,
+                                    const int32_t* context_lens, int max_context_len, float scale, void* out,
+                                    void* workspace, int64_t workspace_bytes, void* stream, const void* plan);
+int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                    int64_t k_new_stride_b, int64_t k_new_stride_h, const void* v_new,
+                                    int64_t v_new_stride_b, int64_t v_new_stride_h, int8_t* k_cache, float* k_scale,
+                                    int32_t* v_packed, float* v_norm, const float* v_codebook, int lloyd_block,
+                                    int64_t num_blocks, int block_size, const int32_t* block_table,
+                                    int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                    float scale, void* out, void* workspace, int64_t workspace_bytes, void* stream,
+                                    const void* plan);
+
+/*
  * Decode attention over the K8V3 cache (int8 K, 3-bit Lloyd-Max V dequantized
  * in-kernel).  Replaces superl8.attn_paged_decode_k8v3(q, k_cache, k_scale,
  * v_packed, v_norm, v_codebook, block_table, context_lens, block_size, *,

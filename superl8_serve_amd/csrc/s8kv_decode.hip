@@ -194,6 +194,9 @@ struct DecodeArgs {
   // sliding window (decode_kernel<D, K8V3, false, true>): row b attends only
   // its last `window` tokens (window >= 1)
   int window;
+  // per-step slice plan (decode_plan_kernel; null: the prologue computes it)
+  const int32_t* plan;
+  int32_t* plan_out;  // host only: s8kv_decode_plan writes the plan here instead of decoding
   int untimed;  // host only: never stamp this launch with timing events
 #ifdef S8KV_DECODE_TRACE
   unsigned long long* trace;  // [grid][kTraceWords] per-workgroup records, or null
@@ -320,6 +323,140 @@ __device__ __forceinline__ int row_stream_len(const DecodeArgs& a, const int* le
   return r < a.batch ? stream_len(a, view_len<WIN>(a, lens_lds, r)) : 0;
 }
 
+// ---- where a workgroup's work lies ----
+// The slice of workgroup column j in its head's token stream and the segment
+// it processes first.  Every decode launch can compute it from the context
+// lengths in its prologue; the launches of one step (one per layer, the same
+// lengths and block table) can instead share one plan computed once by
+// decode_plan_kernel (s8kv_decode_plan), whose entry for column j also holds
+// the storage row (KV head 0) of each wave's first tile, so that a planned
+// launch issues its first K/V loads before anything else.
+struct SliceLoc {
+  int total;                       // the head's stream length
+  int lo, hi;                      // the slice [lo, hi)
+  int b, pb, L;                    // the segment processed first: row, its stream start, its length (0: none)
+  int b_first, pb_first, L_first;  // the slice's first segment
+  int b_stop;                      // rows from here on are left to the reordered segment
+  int reordered;                   // the slice's last segment runs first
+};
+// Plan layout (int32 words): a header naming the launch geometry the plan was
+// made for, then one entry per workgroup column j.
+constexpr int kPlanHeader = 16;
+constexpr int kPlanEntry = 16;
+constexpr int kPlanMagic = 0x50384B53;
+constexpr uint32_t kNoTile = 0xFFFFFFFFu;
+enum PlanWord {  // entry words
+  kPwTotal = 0, kPwLo, kPwHi, kPwB, kPwPb, kPwL, kPwBFirst, kPwPbFirst, kPwLFirst, kPwBStop, kPwReordered,
+  kPwTile0 = 12,  // kPwTile0 + w: wave w's first tile row at KV head 0, or kNoTile
+};
+// Header word i of the plan a launch with arguments `a` needs.
+__host__ __device__ inline int32_t plan_header_word(const DecodeArgs& a, int i) {
+  switch (i) {
+    case 0: return kPlanMagic;
+    case 1: return a.batch;
+    case 2: return a.max_context_len;
+    case 3: return a.wg_per_head;
+    case 4: return a.slot_classes;
+    case 5: return a.slot_skew;
+    case 6: return a.ghost;
+    case 7: return a.bs_log2;
+    case 8: return a.num_kv_heads;
+    case 9: return a.window;
+    case 10: return (int32_t)(uint32_t)(uintptr_t)a.block_table;
+    case 11: return (int32_t)(uint32_t)((uint64_t)(uintptr_t)a.block_table >> 32);
+    case 12: return (int32_t)(uint32_t)(uintptr_t)a.context_lens;
+    case 13: return (int32_t)(uint32_t)((uint64_t)(uintptr_t)a.context_lens >> 32);
+    case 14: return (int32_t)a.bt_stride;
+    default: return 0;
+  }
+}
+
+// Advance (rb, rpb) to the first row from rb on whose real tokens
+// [rpb + ghost, rpb + ghost + padded32(L)) overlap [lo, hi); returns its
+// length, or 0 when the slice holds no further segment.
+template <bool WIN>
+__device__ __forceinline__ int find_segment(const DecodeArgs& a, const int* lens_lds, int lo, int hi, int& rb,
+                                            int& rpb) {
+  for (; rb < a.batch && rpb + a.ghost < hi; ++rb) {
+    const int L = __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, rb));
+    if (L == 0) continue;
+    if (rpb + a.ghost + padded32(L) > lo) return L;
+    rpb += stream_len(a, L);
+  }
+  return 0;
+}
+
+// Column j's slice and the segment it processes first, from the context
+// lengths in LDS (all lanes of a wave; the results are wave-uniform).
+// Returns false when the slice holds no segment.
+template <bool WIN>
+__device__ __forceinline__ bool locate_slice(const DecodeArgs& a, const int* lens_lds, int j, int lane, SliceLoc& s) {
+  // stream positions: prefix of the rows' stream lengths
+  const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
+  const int incl0 = wave_incl_scan(v0);  // rows 0..63
+  int total = __builtin_amdgcn_readlane(incl0, 63);
+  for (int c0 = 64; c0 < a.batch; c0 += 64)
+    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len<WIN>(a, lens_lds, c0, lane)), 63);
+  s.total = __builtin_amdgcn_readfirstlane(total);
+  s.L = 0;
+  const SliceLayout sl = slice_layout(s.total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
+  s.lo = slice_start(sl, j);
+  if (s.lo >= s.total) return false;
+  s.hi = j + 1 >= a.wg_per_head ? s.total : min(s.total, slice_start(sl, j + 1));
+
+  // the row whose stream range holds position pos (< total), and the start of that range
+  auto find_row = [&](int pos, int& rb, int& rpb) {
+    rb = 0;
+    rpb = 0;
+    int carry = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int v = c0 == 0 ? v0 : row_stream_len<WIN>(a, lens_lds, c0, lane);
+      const int incl = (c0 == 0 ? incl0 : wave_incl_scan(v)) + carry;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(incl > pos);
+      if (m != 0) {
+        const int f = (int)__builtin_ctzll(m);
+        rb = c0 + f;
+        rpb = __builtin_amdgcn_readlane(incl - v, f);
+        break;
+      }
+      carry = __builtin_amdgcn_readlane(incl, 63);
+    }
+    rb = __builtin_amdgcn_readfirstlane(rb);
+    rpb = __builtin_amdgcn_readfirstlane(rpb);
+  };
+  int b, pb;
+  find_row(s.lo, b, pb);
+  int L = find_segment<WIN>(a, lens_lds, s.lo, s.hi, b, pb);
+  if (L == 0) return false;
+  // Segment order: when the slice's last segment is split by the slice end
+  // (its row continues in the next slice) and is not its first segment, it
+  // is processed first, then the segments from the first one on, stopping
+  // before its row.  Both parts of a row shared by two slices are then
+  // processed early in their slices, so the row's combine happens while
+  // other workgroups stream, not in the kernel's tail.
+  s.b_first = b;
+  s.pb_first = pb;
+  s.L_first = L;
+  s.b_stop = a.batch;
+  s.reordered = 0;
+  {
+    int bl, pbl;
+    find_row(s.hi - 1, bl, pbl);
+    const int Ll = bl > b ? __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, bl)) : 0;
+    if (Ll > 0 && pbl + a.ghost < s.hi && pbl + a.ghost + padded32(Ll) > s.hi) {
+      b = bl;
+      pb = pbl;
+      L = Ll;
+      s.b_stop = bl;
+      s.reordered = 1;
+    }
+  }
+  s.b = b;
+  s.pb = pb;
+  s.L = L;
+  return true;
+}
+
 // Position of tile token tt (0..31) in the LDS-staged V tile: lane group g's
 // eight transpose-read rows (tokens 4g..4g+3 and 16+4g..16+4g+3) are
 // consecutive rows 8g..8g+7.
@@ -374,60 +511,6 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   unsigned long long tr_tok = 0, tr_seg = 0;
 #endif
 
-  // ---- context lengths -> LDS (one global round trip for the whole prologue) ----
-  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
-  __syncthreads();
-  S8KV_TRACE_STAMP(kTrLens);
-
-  // ---- stream positions: prefix of the rows' stream lengths (every wave) ----
-  const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
-  const int incl0 = wave_incl_scan(v0);  // rows 0..63
-  int total = __builtin_amdgcn_readlane(incl0, 63);
-  for (int c0 = 64; c0 < a.batch; c0 += 64)
-    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len<WIN>(a, lens_lds, c0, lane)), 63);
-  total = __builtin_amdgcn_readfirstlane(total);
-
-  // ---- this workgroup's slice [lo, hi) of the token stream ----
-  if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
-    for (int c0 = 0; c0 < a.batch; c0 += 64) {
-      uint64_t m = __builtin_amdgcn_ballot_w64(c0 + lane < a.batch && lens_at(a, lens_lds, c0 + lane) == 0);
-      while (m != 0) {
-        const int b = c0 + (int)__builtin_ctzll(m);
-        m &= m - 1;
-        for (int i = tid; i < G * D; i += 64 * kDecWaves)
-          a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
-      }
-    }
-  }
-  const SliceLayout sl = slice_layout(total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
-  const int lo = slice_start(sl, j);
-  if (lo >= total) return;
-  const int hi = j + 1 >= a.wg_per_head ? total : min(total, slice_start(sl, j + 1));
-
-  // The row whose stream range holds position pos (< total), and the start of
-  // that range.
-  auto find_row = [&](int pos, int& rb, int& rpb) {
-    rb = 0;
-    rpb = 0;
-    int carry = 0;
-    for (int c0 = 0; c0 < a.batch; c0 += 64) {
-      const int v = c0 == 0 ? v0 : row_stream_len<WIN>(a, lens_lds, c0, lane);
-      const int incl = (c0 == 0 ? incl0 : wave_incl_scan(v)) + carry;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(incl > pos);
-      if (m != 0) {
-        const int f = (int)__builtin_ctzll(m);
-        rb = c0 + f;
-        rpb = __builtin_amdgcn_readlane(incl - v, f);
-        break;
-      }
-      carry = __builtin_amdgcn_readlane(incl, 63);
-    }
-    rb = __builtin_amdgcn_readfirstlane(rb);
-    rpb = __builtin_amdgcn_readfirstlane(rpb);
-  };
-  int b, pb;  // row, and the start of its stream range
-  find_row(lo, b, pb);
-
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
@@ -446,6 +529,130 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   const int bt_width = (a.max_context_len + (1 << bs_log2) - 1) >> bs_log2;  // readable entries per row
   const int bt_first = (kSubTokens >> bs_log2) + 1;
   constexpr int kBtRegs = (kMaxSubBlocks + 64 * kDecWaves - 1) / (64 * kDecWaves);
+  constexpr int kPol = kTilePolicy<K8V3>;
+
+  // The tile's loads in flight (a planned launch issues its first tile in the
+  // prologue), and the loads of a tile inside one block (block_size >= 32)
+  // from its first storage row r0: K and V, then the scales.
+  TileIO<D, K8V3> io;
+  auto tile_kv_at = [&](uint32_t r0, int ln) {
+    const int cc = ln & 15, gg = ln >> 4;
+    if constexpr (BIG) {  // descriptors rebased to the tile's first row
+      const rsrc_t kt = window_rsrc(a.k_cache, a.kc_total, (uint64_t)r0 * D);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) load_kchunk<C::KCH, kPol>(kt, (uint32_t)((16 * s + cc) * D + gg * C::KCH), io.k[s]);
+      if constexpr (!K8V3) {
+        const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * D);
+#pragma unroll
+        for (int jj = 0; jj < C::VLOADS; ++jj)
+          io.v[jj] = bload128<kPol>(vt, (uint32_t)((jj * RPI + ln / LPR) * D + (ln % LPR) * 16));
+      } else {
+        const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (C::WORDS * 4));
+#pragma unroll
+        for (int jj = 0; jj < C::VLOADS; ++jj) {
+          const int job = jj * 64 + ln;
+          const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
+          io.v[jj].x = bload32<kPol>(vt, off);
+          io.v[jj].y = bload32<kPol>(vt, off + 4);
+          io.v[jj].z = bload32<kPol>(vt, off + 8);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        load_kchunk<C::KCH, kPol>(kc, (uint32_t)((16 * s + cc) * D + gg * C::KCH), io.k[s], r0 * (uint32_t)D);
+      if constexpr (!K8V3) {
+#pragma unroll
+        for (int jj = 0; jj < C::VLOADS; ++jj)
+          io.v[jj] = bload128<kPol>(vc, (uint32_t)((jj * RPI + ln / LPR) * D + (ln % LPR) * 16), r0 * (uint32_t)D);
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < C::VLOADS; ++jj) {
+          const int job = jj * 64 + ln;
+          const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
+          const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
+          io.v[jj].x = bload32<kPol>(vc, off, so);
+          io.v[jj].y = bload32<kPol>(vc, off + 4, so);
+          io.v[jj].z = bload32<kPol>(vc, off + 8, so);
+        }
+      }
+    }
+  };
+  auto tile_scales_at = [&](uint32_t r0, int ln) {
+    const int gg = ln >> 4;
+    rsrc_t kst = ks, vst = vs;
+    uint32_t so = r0;
+    if constexpr (BIG) {
+      kst = window_rsrc(a.k_scale, a.ks_total, (uint64_t)r0 * 4u);
+      vst = window_rsrc(a.v_scale, a.vs_total, (uint64_t)r0 * (C::NB * 4u));
+      so = 0;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t row = (uint32_t)(16 * s + 4 * gg);
+      io.ks[s] = bloadf4<kPol>(kst, row * 4u, so * 4u);
+      if constexpr (C::NB == 1) {
+        io.vs[s][0] = bloadf4<kPol>(vst, row * 4u, so * 4u);
+      } else {
+        const float4_t n0 = bloadf4<kPol>(vst, row * 8u, so * 8u), n1 = bloadf4<kPol>(vst, row * 8u + 16u, so * 8u);
+        io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
+        io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
+      }
+    }
+  };
+
+  // ---- the slice and its first segment: from the step's plan, or located here ----
+  SliceLoc sl;
+  bool pre_issued = false;  // this wave's first tile of the first segment is in flight
+  bool planned = false;
+  if (a.plan != nullptr) {
+    const int32_t* hd = a.plan;
+    planned = true;
+#pragma unroll
+    for (int i = 0; i < kPlanHeader; ++i) planned = planned && hd[i] == plan_header_word(a, i);
+  }
+  if (planned) {
+    const int32_t* e = a.plan + kPlanHeader + (int64_t)j * kPlanEntry;
+    sl.total = e[kPwTotal];
+    sl.lo = e[kPwLo];
+    sl.hi = e[kPwHi];
+    sl.b = e[kPwB];
+    sl.pb = e[kPwPb];
+    sl.L = e[kPwL];
+    sl.b_first = e[kPwBFirst];
+    sl.pb_first = e[kPwPbFirst];
+    sl.L_first = e[kPwLFirst];
+    sl.b_stop = e[kPwBStop];
+    sl.reordered = e[kPwReordered];
+    const uint32_t r0 = (uint32_t)e[kPwTile0 + wave];
+    // (rows outside the batch would index outputs and partials out of range)
+    if (sl.L > 0 && !(sl.b >= 0 && sl.b < a.batch && sl.b_first >= 0 && sl.b_first < a.batch && sl.b_stop >= 0 &&
+                      sl.b_stop <= a.batch))
+      planned = false;
+    else if (sl.L > 0 && r0 != kNoTile && tile_in_block) {
+      tile_kv_at(r0 + ((uint32_t)h << bs_log2), lane);
+      tile_scales_at(r0 + ((uint32_t)h << bs_log2), lane);
+      pre_issued = true;
+    }
+  }
+  // context lengths -> LDS (one global round trip for the whole prologue)
+  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
+  __syncthreads();
+  S8KV_TRACE_STAMP(kTrLens);
+  bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
+  if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      uint64_t m = __builtin_amdgcn_ballot_w64(c0 + lane < a.batch && lens_at(a, lens_lds, c0 + lane) == 0);
+      while (m != 0) {
+        const int b = c0 + (int)__builtin_ctzll(m);
+        m &= m - 1;
+        for (int i = tid; i < G * D; i += 64 * kDecWaves)
+          a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
+      }
+    }
+  }
+  if (!has_seg) return;
+  const int total = sl.total, lo = sl.lo, hi = sl.hi;
 
   // K8V3 codebook byte tables (fp16 of the fp32 codebook).
   uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
@@ -458,19 +665,6 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
     }
   }
-
-  // Advance (b, pb) to the first row from b on whose real tokens
-  // [pb + ghost, pb + ghost + padded32(L)) overlap [lo, hi); returns its
-  // length, or 0 when the slice holds no further segment.
-  auto find_segment = [&](int& rb, int& rpb) -> int {
-    for (; rb < a.batch && rpb + a.ghost < hi; ++rb) {
-      const int L = __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, rb));
-      if (L == 0) continue;
-      if (rpb + a.ghost + padded32(L) > lo) return L;
-      rpb += stream_len(a, L);
-    }
-    return 0;
-  };
 
   // Set-up loads of a segment that starts at token 0 of row rb (or at s0 for
   // the slice's first row): the lane's raw q fragment and the first
@@ -520,29 +714,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     }
   };
 
-  int L = find_segment(b, pb);
-  if (L == 0) return;
-  // Segment order: when the slice's last segment is split by the slice end
-  // (its row continues in the next slice) and is not its first segment, it
-  // is processed first, then the segments from the first one on, stopping
-  // before its row.  Both parts of a row shared by two slices are then
-  // processed early in their slices, so the row's combine happens while
-  // other workgroups stream, not in the kernel's tail.
-  const int b_first = b, pb_first = pb, L_first = L;
-  int b_stop = a.batch;  // rows from here on are left to the reordered segment
-  bool reordered = false;
-  {
-    int bl, pbl;
-    find_row(hi - 1, bl, pbl);
-    const int Ll = bl > b ? __builtin_amdgcn_readfirstlane(view_len<WIN>(a, lens_lds, bl)) : 0;
-    if (Ll > 0 && pbl + a.ghost < hi && pbl + a.ghost + padded32(Ll) > hi) {
-      b = bl;
-      pb = pbl;
-      L = Ll;
-      b_stop = bl;
-      reordered = true;
-    }
-  }
+  int b = sl.b, pb = sl.pb, L = sl.L;
+  const int b_first = sl.b_first, pb_first = sl.pb_first, L_first = sl.L_first;
+  const int b_stop = sl.b_stop;  // rows from here on are left to the reordered segment
+  bool reordered = sl.reordered != 0;
   S8KV_TRACE_STAMP(kTrFound);
   prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
   store_prefetched_bt();
@@ -667,50 +842,9 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         return __builtin_amdgcn_readfirstlane(((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)tb & bsm));
       };
 
-      TileIO<D, K8V3> io;
-      constexpr int kPol = kTilePolicy<K8V3>;
       auto issue_kv = [&](int tb, uint32_t r0) {
-        if constexpr (BIG) {  // the tile through descriptors rebased to its first row (block_size >= 32)
-          const rsrc_t kt = window_rsrc(a.k_cache, a.kc_total, (uint64_t)r0 * D);
-#pragma unroll
-          for (int s = 0; s < 2; ++s) load_kchunk<C::KCH, kPol>(kt, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s]);
-          if constexpr (!K8V3) {
-            const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * D);
-#pragma unroll
-            for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128<kPol>(vt, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16));
-          } else {
-            const rsrc_t vt = window_rsrc(a.v_cache, a.vc_total, (uint64_t)r0 * (C::WORDS * 4));
-#pragma unroll
-            for (int jj = 0; jj < C::VLOADS; ++jj) {
-              const int job = jj * 64 + lane;
-              const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-              io.v[jj].x = bload32<kPol>(vt, off);
-              io.v[jj].y = bload32<kPol>(vt, off + 4);
-              io.v[jj].z = bload32<kPol>(vt, off + 8);
-            }
-          }
-          return;
-        }
-        if (tile_in_block) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s)
-            load_kchunk<C::KCH, kPol>(kc, (uint32_t)((16 * s + c) * D + g * C::KCH), io.k[s], r0 * (uint32_t)D);
-          if constexpr (!K8V3) {
-#pragma unroll
-            for (int jj = 0; jj < C::VLOADS; ++jj)
-              io.v[jj] = bload128<kPol>(vc, (uint32_t)((jj * RPI + lane / LPR) * D + (lane % LPR) * 16), r0 * (uint32_t)D);
-          } else {
-#pragma unroll
-            for (int jj = 0; jj < C::VLOADS; ++jj) {
-              const int job = jj * 64 + lane;
-              const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-              const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
-              io.v[jj].x = bload32<kPol>(vc, off, so);
-              io.v[jj].y = bload32<kPol>(vc, off + 4, so);
-              io.v[jj].z = bload32<kPol>(vc, off + 8, so);
-            }
-          }
+        if (BIG || tile_in_block) {  // (BIG needs block_size >= 32)
+          tile_kv_at(r0, lane);
           return;
         }
 #pragma unroll
@@ -737,38 +871,18 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         }
       };
       auto issue_scales = [&](int tb, uint32_t r0) {
-        if constexpr (BIG) {
-          const rsrc_t kst = window_rsrc(a.k_scale, a.ks_total, (uint64_t)r0 * 4u);
-          const rsrc_t vst = window_rsrc(a.v_scale, a.vs_total, (uint64_t)r0 * (C::NB * 4u));
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const uint32_t row = (uint32_t)(16 * s + 4 * g);
-            io.ks[s] = bloadf4<kPol>(kst, row * 4u);
-            if constexpr (C::NB == 1) {
-              io.vs[s][0] = bloadf4<kPol>(vst, row * 4u);
-            } else {
-              const float4_t n0 = bloadf4<kPol>(vst, row * 8u), n1 = bloadf4<kPol>(vst, row * 8u + 16u);
-              io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};
-              io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
-            }
-          }
+        if (BIG || tile_in_block) {
+          tile_scales_at(r0, lane);
           return;
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          uint32_t row, so;
-          if (tile_in_block) {
-            row = (uint32_t)(16 * s + 4 * g);
-            so = r0;
-          } else {
-            row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
-            so = 0;
-          }
-          io.ks[s] = bloadf4<kPol>(ks, row * 4u, so * 4u);
+          const uint32_t row = row_of(min(tb + 16 * s + 4 * g, last & ~3));
+          io.ks[s] = bloadf4<kPol>(ks, row * 4u);
           if constexpr (C::NB == 1) {
-            io.vs[s][0] = bloadf4<kPol>(vs, row * 4u, so * 4u);
+            io.vs[s][0] = bloadf4<kPol>(vs, row * 4u);
           } else {
-            const float4_t n0 = bloadf4<kPol>(vs, row * 8u, so * 8u), n1 = bloadf4<kPol>(vs, row * 8u + 16u, so * 8u);
+            const float4_t n0 = bloadf4<kPol>(vs, row * 8u), n1 = bloadf4<kPol>(vs, row * 8u + 16u);
             io.vs[s][0] = float4_t{n0.x, n0.z, n1.x, n1.z};  // [token][block] -> per block
             io.vs[s][1] = float4_t{n0.y, n0.w, n1.y, n1.w};
           }
@@ -1005,10 +1119,14 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       };
 
       int tb = u0 + kTile * wave;
+      const bool pre = pre_issued;  // (the first sub-split of the first segment only)
+      pre_issued = false;
       if (tb < t1) {
         const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
-        issue_kv(tb, r0);
-        issue_scales(tb, r0);
+        if (!pre) {
+          issue_kv(tb, r0);
+          issue_scales(tb, r0);
+        }
         if constexpr (WIN) {  // the row's first tile holds tokens below the window
           if (tb < lo_tok && tb + kTile * kDecWaves < t1) {
             process(tb, std::true_type{}, std::true_type{});
@@ -1110,7 +1228,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     } else {
       nb = b + 1;
       npb = pb + stream_len(a, L);
-      nL = find_segment(nb, npb);
+      nL = find_segment<WIN>(a, lens_lds, lo, hi, nb, npb);
       if (nb >= b_stop) nL = 0;
     }
     // (unconditional, from a valid row when there is no next segment: values
@@ -1235,6 +1353,69 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #endif
 }
 
+// The step's slice plan: one wave per workgroup column j, the decode
+// prologue's arithmetic on the same lengths (locate_slice), plus the storage
+// row (KV head 0) of each wave's first tile in the segment processed first --
+// tile s0 + 32 w of the segment's first sub-split, when it exists and the
+// block size keeps a tile inside one block.  Block 0 also writes the header.
+template <bool WIN>
+__global__ __launch_bounds__(64 * kDecWaves) void decode_plan_kernel(DecodeArgs a) {
+  __shared__ int lens_lds[kLensLds];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = blockIdx.x * kDecWaves + wave;
+  int32_t* plan = a.plan_out;
+  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
+  if (blockIdx.x == 0 && tid < kPlanHeader) plan[tid] = plan_header_word(a, tid);
+  __syncthreads();
+  if (j >= a.wg_per_head) return;
+  SliceLoc s;
+  if (!locate_slice<WIN>(a, lens_lds, j, lane, s)) {  // no segment: the launch's workgroup j returns at once
+    if (s.lo >= s.total) s.lo = s.hi = s.total;
+    s.L = 0;
+    s.b = s.pb = s.b_first = s.pb_first = s.L_first = s.reordered = 0;
+    s.b_stop = a.batch;
+  }
+  uint32_t r0 = kNoTile;
+  if (s.L > 0 && a.bs_log2 >= 5 && lane < kDecWaves) {
+    const int rs = s.pb + a.ghost;
+    const int s0 = max(s.lo, rs) - rs;
+    const int s1 = min(s.hi, rs + padded32(s.L)) - rs;
+    const int t1 = min(min(s1, s0 + kSubTokens), s.L);
+    const int al = WIN ? win_base(a, lens_at(a, lens_lds, s.b)) : 0;
+    const int tb = s0 + kTile * lane + al;
+    if (s0 + kTile * lane < t1) {
+      const uint32_t blk = (uint32_t)a.block_table[(int64_t)s.b * a.bt_stride + (tb >> a.bs_log2)];
+      r0 = ((blk * (uint32_t)a.num_kv_heads) << a.bs_log2) + ((uint32_t)tb & ((1u << a.bs_log2) - 1u));
+    }
+  }
+  const int w0 = __builtin_amdgcn_readlane((int)r0, 0), w1 = __builtin_amdgcn_readlane((int)r0, 1);
+  const int w2 = __builtin_amdgcn_readlane((int)r0, 2), w3 = __builtin_amdgcn_readlane((int)r0, 3);
+  if (lane < kPlanEntry) {
+    int v = 0;
+    switch (lane) {
+      case kPwTotal: v = s.total; break;
+      case kPwLo: v = s.lo; break;
+      case kPwHi: v = s.hi; break;
+      case kPwB: v = s.b; break;
+      case kPwPb: v = s.pb; break;
+      case kPwL: v = s.L; break;
+      case kPwBFirst: v = s.b_first; break;
+      case kPwPbFirst: v = s.pb_first; break;
+      case kPwLFirst: v = s.L_first; break;
+      case kPwBStop: v = s.b_stop; break;
+      case kPwReordered: v = s.reordered; break;
+      case kPwTile0: v = w0; break;
+      case kPwTile0 + 1: v = w1; break;
+      case kPwTile0 + 2: v = w2; break;
+      case kPwTile0 + 3: v = w3; break;
+      default: v = 0;
+    }
+    plan[kPlanHeader + (int64_t)j * kPlanEntry + lane] = v;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1348,6 +1529,11 @@ static int launch_decode_impl(DecodeArgs& a, hipStream_t stream) {
     return S8KV_ERR_UNSUPPORTED;
   }
   a.slots = a.batch + a.wg_per_head;
+  if (a.plan_out != nullptr) {  // s8kv_decode_plan: the slice plan of this launch geometry
+    const dim3 pgrid((a.wg_per_head + kDecWaves - 1) / kDecWaves);
+    hipLaunchKernelGGL((decode_plan_kernel<WIN>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
+    return check_launch("s8kv_decode_plan");
+  }
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
 #ifdef S8KV_DECODE_TRACE
   a.trace = trace_slot((int64_t)grid.x * kTraceWords);
@@ -1376,6 +1562,11 @@ static int64_t partial_count(int batch, int num_q_heads, int num_kv_heads) {
 static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim) {
   return partial_count(batch, num_q_heads, num_kv_heads) * (head_dim + 2) * 4 + (int64_t)num_kv_heads * batch * 8;
 }
+// Slice plan: header + one entry per workgroup column, for the largest grid
+// a launch of this geometry may use.
+static int64_t plan_bytes(int num_kv_heads) {
+  return (int64_t)(kPlanHeader + kPlanEntry * max_wg_per_head(num_kv_heads)) * 4;
+}
 
 
 static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1398,9 +1589,11 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
                max_context_len);
   S8KV_REQUIRE((int64_t)batch * (max_context_len + 31) < (int64_t(1) << 31), S8KV_ERR_UNSUPPORTED,
                "decode: batch * max_context_len too large");
-  S8KV_REQUIRE(a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.block_table && a.context_lens && a.out,
-               S8KV_ERR_INVALID, "decode: null pointer argument");
-  S8KV_REQUIRE(!fuse || (a.k_new && a.v_new), S8KV_ERR_INVALID, "decode_append: null k_new / v_new");
+  const bool plan_only = a.plan_out != nullptr;  // s8kv_decode_plan: reads lengths and block table only
+  S8KV_REQUIRE(a.block_table && a.context_lens, S8KV_ERR_INVALID, "decode: null block table or context lengths");
+  S8KV_REQUIRE(plan_only || (a.q && a.k_cache && a.k_scale && a.v_cache && a.v_scale && a.out), S8KV_ERR_INVALID,
+               "decode: null pointer argument");
+  S8KV_REQUIRE(plan_only || !fuse || (a.k_new && a.v_new), S8KV_ERR_INVALID, "decode_append: null k_new / v_new");
   const int64_t rows = num_blocks * num_kv_heads * block_size;
   S8KV_REQUIRE(fits_u32(rows), S8KV_ERR_UNSUPPORTED, "decode: more than 2^32 cache rows per layer");
   // a tensor past 4 GiB: tiles through descriptors rebased per tile, which
@@ -1424,15 +1617,22 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   a.max_context_len = max_context_len;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
-  const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
-  S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
-               "decode: workspace of %lld bytes needed, %lld given", (long long)need, (long long)workspace_bytes_given);
-  S8KV_REQUIRE((uintptr_t)workspace % 8 == 0, S8KV_ERR_WORKSPACE, "decode: workspace not 8-byte aligned");
-  const int64_t partials = partial_count(batch, num_q_heads, num_kv_heads);
-  a.ws_ml = reinterpret_cast<float*>(workspace);
-  a.ws_acc = a.ws_ml + partials * 2;
-  a.ws_cnt = reinterpret_cast<unsigned long long*>(a.ws_acc + partials * head_dim);
-  a.tag = next_launch_tag();
+  if (plan_only) {
+    S8KV_REQUIRE(workspace_bytes_given >= plan_bytes(num_kv_heads) && (uintptr_t)a.plan_out % 4 == 0,
+                 S8KV_ERR_INVALID, "decode_plan: a plan of %lld bytes (4-byte aligned) is needed, %lld given",
+                 (long long)plan_bytes(num_kv_heads), (long long)workspace_bytes_given);
+  } else {
+    const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+    S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
+                 "decode: workspace of %lld bytes needed, %lld given", (long long)need,
+                 (long long)workspace_bytes_given);
+    S8KV_REQUIRE((uintptr_t)workspace % 8 == 0, S8KV_ERR_WORKSPACE, "decode: workspace not 8-byte aligned");
+    const int64_t partials = partial_count(batch, num_q_heads, num_kv_heads);
+    a.ws_ml = reinterpret_cast<float*>(workspace);
+    a.ws_acc = a.ws_ml + partials * 2;
+    a.ws_cnt = reinterpret_cast<unsigned long long*>(a.ws_acc + partials * head_dim);
+    a.tag = next_launch_tag();
+  }
   hipStream_t s = (hipStream_t)stream;
   if (a.window > 0) {  // sliding window (no fused append)
     switch (head_dim) {
@@ -1572,15 +1772,16 @@ extern "C" int s8kv_decode_int8(const void* q, int batch, int num_q_heads, int n
                        max_context_len, scale, workspace, workspace_bytes, stream);
 }
 
-extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+static int decode_append_int8_impl(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                        int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
                                        int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
                                        int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int8_t* v_cache,
                                        float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
                                        int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
                                        float scale, void* out, void* workspace, int64_t workspace_bytes,
-                                       void* stream) {
+                                       void* stream, const int32_t* plan) {
   DecodeArgs a{};
+  a.plan = plan;
   a.q = (const _Float16*)q;
   a.q_stride_b = q_stride_b;
   a.q_stride_h = q_stride_h;
@@ -1597,6 +1798,39 @@ extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads
   a.vn_stride_h = v_new_stride_h;
   return decode_common(a, false, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_append_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                                       int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                                       int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int8_t* v_cache,
+                                       float* v_scale, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                       int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                       float scale, void* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  return decode_append_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
+                                 k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
+                                 k_scale, v_cache, v_scale, num_blocks, block_size, block_table, block_table_stride,
+                                 context_lens, max_context_len, scale, out, workspace, workspace_bytes, stream,
+                                 nullptr);
+}
+
+extern "C" int s8kv_decode_append_int8_planned(const void* q, int batch, int num_q_heads, int num_kv_heads,
+                                               int head_dim, int64_t q_stride_b, int64_t q_stride_h,
+                                               const void* k_new, int64_t k_new_stride_b, int64_t k_new_stride_h,
+                                               const void* v_new, int64_t v_new_stride_b, int64_t v_new_stride_h,
+                                               int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                                               int64_t num_blocks, int block_size, const int32_t* block_table,
+                                               int64_t block_table_stride, const int32_t* context_lens,
+                                               int max_context_len, float scale, void* out, void* workspace,
+                                               int64_t workspace_bytes, void* stream, const void* plan) {
+  S8KV_REQUIRE(plan != nullptr && (uintptr_t)plan % 4 == 0, S8KV_ERR_INVALID,
+               "decode_append_int8_planned: null or unaligned plan");
+  return decode_append_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
+                                 k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
+                                 k_scale, v_cache, v_scale, num_blocks, block_size, block_table, block_table_stride,
+                                 context_lens, max_context_len, scale, out, workspace, workspace_bytes, stream,
+                                 static_cast<const int32_t*>(plan));
 }
 
 extern "C" int s8kv_decode_append_int8_noalloc(const void* q, int batch, int num_q_heads, int num_kv_heads,
@@ -1639,17 +1873,18 @@ extern "C" int s8kv_decode_append_int8_noalloc(const void* q, int batch, int num
                        max_context_len, scale, ws, kScratchBytes, stream);
 }
 
-extern "C" int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+static int decode_append_k8v3_impl(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                        int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
                                        int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
                                        int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int32_t* v_packed,
                                        float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
                                        int block_size, const int32_t* block_table, int64_t block_table_stride,
                                        const int32_t* context_lens, int max_context_len, float scale, void* out,
-                                       void* workspace, int64_t workspace_bytes, void* stream) {
+                                       void* workspace, int64_t workspace_bytes, void* stream, const int32_t* plan) {
   S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "decode_append_k8v3: lloyd_block %d != 128", lloyd_block);
   S8KV_REQUIRE(v_codebook != nullptr, S8KV_ERR_INVALID, "decode_append_k8v3: null codebook");
   DecodeArgs a{};
+  a.plan = plan;
   a.q = (const _Float16*)q;
   a.q_stride_b = q_stride_b;
   a.q_stride_h = q_stride_h;
@@ -1667,6 +1902,61 @@ extern "C" int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads
   a.vn_stride_h = v_new_stride_h;
   return decode_common(a, true, true, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int s8kv_decode_append_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_new_stride_b,
+                                       int64_t k_new_stride_h, const void* v_new, int64_t v_new_stride_b,
+                                       int64_t v_new_stride_h, int8_t* k_cache, float* k_scale, int32_t* v_packed,
+                                       float* v_norm, const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                       int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                       const int32_t* context_lens, int max_context_len, float scale, void* out,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_append_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
+                                 k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
+                                 k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks, block_size,
+                                 block_table, block_table_stride, context_lens, max_context_len, scale, out,
+                                 workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num_q_heads, int num_kv_heads,
+                                               int head_dim, int64_t q_stride_b, int64_t q_stride_h,
+                                               const void* k_new, int64_t k_new_stride_b, int64_t k_new_stride_h,
+                                               const void* v_new, int64_t v_new_stride_b, int64_t v_new_stride_h,
+                                               int8_t* k_cache, float* k_scale, int32_t* v_packed, float* v_norm,
+                                               const float* v_codebook, int lloyd_block, int64_t num_blocks,
+                                               int block_size, const int32_t* block_table, int64_t block_table_stride,
+                                               const int32_t* context_lens, int max_context_len, float scale,
+                                               void* out, void* workspace, int64_t workspace_bytes, void* stream,
+                                               const void* plan) {
+  S8KV_REQUIRE(plan != nullptr && (uintptr_t)plan % 4 == 0, S8KV_ERR_INVALID,
+               "decode_append_k8v3_planned: null or unaligned plan");
+  return decode_append_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
+                                 k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
+                                 k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks, block_size,
+                                 block_table, block_table_stride, context_lens, max_context_len, scale, out,
+                                 workspace, workspace_bytes, stream, static_cast<const int32_t*>(plan));
+}
+
+extern "C" int64_t s8kv_decode_plan_size(int num_kv_heads) {
+  return num_kv_heads > 0 ? plan_bytes(num_kv_heads) : 0;
+}
+
+extern "C" int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
+                                int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                void* plan, int64_t plan_bytes_given, void* stream) {
+  S8KV_REQUIRE(layout == 0 || layout == 1, S8KV_ERR_INVALID, "decode_plan: layout %d is neither 0 (int8) nor 1 (k8v3)",
+               layout);
+  S8KV_REQUIRE(plan != nullptr, S8KV_ERR_INVALID, "decode_plan: null plan");
+  DecodeArgs a{};
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.plan_out = static_cast<int32_t*>(plan);
+  a.untimed = 1;
+  return decode_common(a, layout == 1, fused != 0, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                       max_context_len, 1.0f, plan, plan_bytes_given, stream);
 }
 
 extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,

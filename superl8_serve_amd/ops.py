@@ -255,8 +255,48 @@ def attn_paged_decode_window(q, k_cache, k_scale, v_cache, v_scale, block_table,
     return out
 
 
+def attn_paged_decode_plan(k_cache, block_table, context_lens, block_size, *, num_q_heads, max_context_len,
+                           layout: str = "int8", fused: bool = True):
+    """Slice plan of one decode step, shared by its per-layer launches.
+
+    Every layer of a step decodes the same rows: the same ``block_table`` and
+    ``context_lens``, so the same split of the token stream over the
+    workgroups.  This launch computes that split once (and the storage rows
+    of every workgroup's first tiles) into a small int32 device tensor;
+    ``attn_paged_decode_append(..., plan=)`` / ``attn_paged_decode_append_k8v3(
+    ..., plan=)`` read it instead of recomputing it.  ``k_cache`` is any
+    layer's cache (geometry only); ``layout`` "int8" or "k8v3"; ``fused``
+    the one-launch step ops.  Capturable (no host synchronization)."""
+    dev = k_cache.device
+    _on_gpu("k_cache", k_cache, torch.int8, dev)
+    _on_gpu("block_table", block_table, torch.int32, dev)
+    _on_gpu("context_lens", context_lens, torch.int32, dev)
+    _require(layout in ("int8", "k8v3"), f"layout must be 'int8' or 'k8v3', got {layout!r}")
+    n, hkv, bs, d = _cache_geometry(k_cache)
+    _require(int(block_size) == bs, f"block_size {block_size} does not match the cache ({bs})")
+    _require(block_table.dim() == 2 and block_table.stride(1) == 1, "block_table must be a [B, max_blocks] tensor "
+             "with unit stride on its last dim (the decode ops are then given the same tensor)")
+    b = block_table.shape[0]
+    _require(context_lens.dim() == 1 and context_lens.shape[0] == b and context_lens.is_contiguous(),
+             f"context_lens must be a contiguous [{b}] tensor")
+    lib = _lib.load()
+    nbytes = int(lib.s8kv_decode_plan_size(hkv))
+    plan = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    rc = lib.s8kv_decode_plan(b, int(num_q_heads), hkv, d, 1 if layout == "k8v3" else 0, 1 if fused else 0, n, bs,
+                              block_table.data_ptr(), block_table.stride(0), context_lens.data_ptr(),
+                              int(max_context_len), plan.data_ptr(), nbytes, _stream(k_cache))
+    _lib.check(rc, "attn_paged_decode_plan")
+    return plan
+
+
+def _plan_ptr(plan, dev):
+    _on_gpu("plan", plan, torch.int32, dev)
+    _require(plan.is_contiguous(), "plan must be contiguous")
+    return plan.data_ptr()
+
+
 def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale, block_table, context_lens,
-                             block_size, *, max_context_len, scale):
+                             block_size, *, max_context_len, scale, plan=None):
     """One decode step of a layer in one launch: append row b's new token at
     position ``context_lens[b] - 1`` of its block table, then attend over
     positions ``0 .. context_lens[b] - 1``.
@@ -267,7 +307,13 @@ def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale
     same output.  ``k_new``, ``v_new``: fp16 ``[B, Hkv, D]``.  Rows with
     ``context_lens[b] == 0`` or ``> max_context_len`` append nothing.  The
     block receiving a row's new token must not be read by another row of the
-    same call (a block being appended to is owned by its sequence)."""
+    same call (a block being appended to is owned by its sequence).
+
+    ``plan``: the step's slice plan from ``attn_paged_decode_plan`` (made from
+    these ``block_table`` and ``context_lens`` tensors, unchanged since); the
+    launch then skips locating its work and issues its first loads at once.
+    Same bytes and outputs as without it; a plan made for another geometry
+    or other tensors is ignored."""
     q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
         q, k_cache, block_table, context_lens, block_size, max_context_len)
     n, hkv, bs, d, b, hq = geo
@@ -286,25 +332,31 @@ def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale
     if b == 0:
         return out
     lib = _lib.load()
-    rc = lib.s8kv_decode_append_int8(
+    args = (
         q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
         k_new.data_ptr(), k_new.stride(0), k_new.stride(1), v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
         k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), n, bs,
         bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
+    if plan is None:
+        rc = lib.s8kv_decode_append_int8(*args)
+    else:
+        rc = lib.s8kv_decode_append_int8_planned(*args, _plan_ptr(plan, dev))
     _lib.check(rc, "attn_paged_decode_append")
     return out
 
 
 def attn_paged_decode_append_k8v3(q, k_new, v_new, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table,
-                                  context_lens, block_size, *, max_context_len, scale, lloyd_block: int = 128):
+                                  context_lens, block_size, *, max_context_len, scale, lloyd_block: int = 128,
+                                  plan=None):
     """``attn_paged_decode_append`` for the K8V3 layout: row b's new token is
     written at position ``context_lens[b] - 1`` exactly as
     ``quantize_kv_write_paged_k8v3`` writes it (int8 K; 3-bit Lloyd-Max V
     words and block norms), then the row attends as ``attn_paged_decode_k8v3``
     does -- one launch for the pair the reference runs as its K8V3 write
-    (kv_cache.py:587-626) and ``decode_attn_static`` (kv_cache.py:1167-1182)."""
+    (kv_cache.py:587-626) and ``decode_attn_static`` (kv_cache.py:1167-1182).
+    ``plan``: as for ``attn_paged_decode_append`` (made with layout "k8v3")."""
     q3, bt, cl, out, ws, ws_bytes, geo, max_context_len = _decode_prep(
         q, k_cache, block_table, context_lens, block_size, max_context_len)
     n, hkv, bs, d, b, hq = geo
@@ -327,13 +379,17 @@ def attn_paged_decode_append_k8v3(q, k_new, v_new, k_cache, k_scale, v_packed, v
     if b == 0:
         return out
     lib = _lib.load()
-    rc = lib.s8kv_decode_append_k8v3(
+    args = (
         q3.data_ptr(), b, hq, hkv, d, q3.stride(0), q3.stride(1),
         k_new.data_ptr(), k_new.stride(0), k_new.stride(1), v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
         k_cache.data_ptr(), k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
         lloyd_block, n, bs, bt.data_ptr(), bt.stride(0), cl.data_ptr(), max_context_len, float(scale),
         out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q3),
     )
+    if plan is None:
+        rc = lib.s8kv_decode_append_k8v3(*args)
+    else:
+        rc = lib.s8kv_decode_append_k8v3_planned(*args, _plan_ptr(plan, dev))
     _lib.check(rc, "attn_paged_decode_append_k8v3")
     return out
 

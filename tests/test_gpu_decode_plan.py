@@ -1,0 +1,222 @@
+"""GPU tests of the per-step slice plan (``attn_paged_decode_plan`` and the
+``plan=`` form of the one-launch decode step ops).
+
+A planned launch reads, from the plan, what the unplanned launch computes in
+its prologue (the slice of the token stream each workgroup takes, the
+segment it processes first, and the storage rows of its waves' first tiles),
+so its cache bytes and outputs must equal the unplanned launch's bit for bit,
+for every slicing.  A plan made for other buffers or another geometry must be
+ignored, and the plan's entries must tile the token stream."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from superl8_serve_amd import ops
+from tests.kvcase import empty_int8_cache, empty_k8v3_cache, make_case
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+CODEBOOK = O.gaussian_codebook(3, 128)
+HEADER, ENTRY = 16, 16  # plan words: header, then one entry per workgroup column
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _last_tokens(case):
+    """The cache without each row's last token (oracle append), the rows' last
+    tokens [B, Hkv, D] (zeros for empty rows)."""
+    ends = np.cumsum(case.lens)
+    last = ends - 1
+    has = case.lens > 0
+    keep = np.ones(int(ends[-1]) if len(ends) else 0, bool)
+    keep[last[has]] = False
+    k_new = np.zeros((case.batch, case.num_kv_heads, case.head_dim), np.float16)
+    v_new = np.zeros_like(k_new)
+    k_new[has] = case.k[last[has]]
+    v_new[has] = case.v[last[has]]
+    return keep, k_new, v_new
+
+
+class _Step:
+    """One layer's fused decode step over device copies of a case, run with
+    and without a plan on the same block-table and length tensors."""
+
+    def __init__(self, case, layout):
+        self.case, self.layout = case, layout
+        keep, k_new, v_new = _last_tokens(case)
+        if layout == "int8":
+            self.pre = empty_int8_cache(case)
+            O.quantize_kv_write_paged(case.k[keep], case.v[keep], *self.pre, case.slots[keep])
+        else:
+            self.pre = empty_k8v3_cache(case)
+            O.k8v3_write_paged(case.k[keep], case.v[keep], *self.pre, CODEBOOK, case.slots[keep])
+        self.kn, self.vn = _t(k_new), _t(v_new)
+        self.q = _t(case.q)[:, :, None, :]
+        self.bt = _t(case.block_table)
+        self.cl = _t(case.lens.astype(np.int32))
+        self.cb = _t(CODEBOOK)
+        self.max_ctx = int(case.lens.max())
+
+    def plan(self, **kw):
+        kw.setdefault("max_context_len", self.max_ctx)
+        return ops.attn_paged_decode_plan(_t(self.pre[0]), kw.pop("bt", self.bt), kw.pop("cl", self.cl),
+                                          self.case.block_size, num_q_heads=self.case.num_q_heads,
+                                          layout=self.layout, **kw)
+
+    def run(self, plan=None, cache=None):
+        c = self.case
+        cache = [_t(x) for x in self.pre] if cache is None else cache
+        if self.layout == "int8":
+            out = ops.attn_paged_decode_append(self.q, self.kn, self.vn, *cache, self.bt, self.cl, c.block_size,
+                                               max_context_len=self.max_ctx, scale=c.scale, plan=plan)
+        else:
+            kc, ks, vp, vnrm = cache
+            out = ops.attn_paged_decode_append_k8v3(self.q, self.kn, self.vn, kc, ks, vp, vnrm, self.cb, self.bt,
+                                                    self.cl, c.block_size, max_context_len=self.max_ctx,
+                                                    scale=c.scale, plan=plan)
+        torch.cuda.synchronize()
+        return _np(out.float()), [_np(x) for x in cache]
+
+
+def _same(a, b, what):
+    out_a, cache_a = a
+    out_b, cache_b = b
+    for x, y, name in zip(cache_a, cache_b, ("k_cache", "k_scale", "v", "v_scale")):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"{what}: {name} differs"
+    assert np.array_equal(out_a, out_b), f"{what}: outputs differ (max {np.abs(out_a - out_b).max():.3e})"
+
+
+@pytest.mark.parametrize("layout,hq,hkv,d,bs,lens", [
+    ("int8", 32, 8, 128, 256, "qwen"),                 # Qwen3-8B heads, ragged lengths
+    ("int8", 16, 8, 128, 16, [100, 17, 16, 15, 1, 0]),  # block_size < 32: no first tile in the plan
+    ("int8", 16, 8, 128, 256, [256, 257, 512, 255]),
+    ("int8", 8, 2, 256, 32, [50, 129, 4000]),
+    ("int8", 8, 4, 64, 64, [33, 2, 80, 0, 700]),
+    ("int8", 4, 2, 32, 32, "many"),                    # more than 64 rows (the scans' second pass)
+    ("k8v3", 32, 8, 128, 256, "long"),
+    ("k8v3", 8, 2, 256, 32, [50, 129, 300, 2100]),
+])
+def test_planned_step_equals_unplanned(layout, hq, hkv, d, bs, lens):
+    rng = np.random.default_rng(11)
+    if lens == "qwen":
+        lens = rng.integers(200, 3000, size=16).tolist()
+    elif lens == "long":
+        lens = rng.integers(1500, 6000, size=8).tolist()
+    elif lens == "many":
+        lens = rng.integers(0, 300, size=100).tolist()
+    case = make_case(4100 + hq + d + bs, len(lens), hq, hkv, d, bs, lens, outlier_channels=2 if d == 128 else 0)
+    step = _Step(case, layout)
+    plan = step.plan()
+    _same(step.run(plan), step.run(None), f"{layout} planned")
+
+
+@pytest.mark.parametrize("wg_per_head,ghost,batch,bs,lens", [
+    (1, 128, 4, 32, [1000, 129, 5000, 0]),          # one slice per head, rows past 2048 tokens
+    (2, 0, 4, 256, [5000, 100, 0, 37]),             # a split row's later block-id stage
+    (7, 0, 64, 32, "short"),                        # rows split across slices, reordered segments
+    (40, 512, 64, 32, "short"),                     # slices holding no tokens
+    (3, 64, 5, 8, [300, 1, 64, 2500, 31]),          # block_size < 32
+])
+def test_planned_step_slicings(wg_per_head, ghost, batch, bs, lens, monkeypatch):
+    monkeypatch.setenv("S8KV_DECODE_WG_PER_HEAD", str(wg_per_head))
+    monkeypatch.setenv("S8KV_DECODE_GHOST", str(ghost))
+    if lens == "short":
+        lens = np.random.default_rng(6).integers(0, 120, size=batch).tolist()
+    case = make_case(177 + wg_per_head, batch, 32, 8, 128, bs, lens)
+    step = _Step(case, "int8")
+    _same(step.run(step.plan()), step.run(None), f"planned wg/head={wg_per_head}")
+
+
+def test_plan_for_other_buffers_or_geometry_is_ignored():
+    """A plan names the block table, lengths and geometry it was made for; a
+    launch given a plan for anything else locates its work itself."""
+    case = make_case(4242, 12, 32, 8, 128, 256, np.random.default_rng(2).integers(300, 4000, size=12).tolist())
+    step = _Step(case, "int8")
+    ref = step.run(None)
+    other_cl = step.cl.clone()  # same lengths, another buffer
+    _same(step.run(step.plan(cl=other_cl)), ref, "plan of another lengths buffer")
+    other_bt = step.bt.clone()
+    _same(step.run(step.plan(bt=other_bt)), ref, "plan of another block table")
+    _same(step.run(step.plan(max_context_len=step.max_ctx + 1)), ref, "plan of another max_context_len")
+    _same(step.run(step.plan(fused=False)), ref, "plan of the unfused kernel")
+    junk = torch.full_like(step.plan(), -7)
+    _same(step.run(junk), ref, "garbage plan")
+
+
+def test_plan_entries_tile_the_stream():
+    """The entries cut the token stream into consecutive slices, and each
+    wave's first-tile row is the block-table row of its first tile."""
+    bs, hkv = 256, 8
+    lens = np.random.default_rng(8).integers(1, 6000, size=40)
+    case = make_case(4343, len(lens), 32, hkv, 128, bs, lens)
+    step = _Step(case, "int8")
+    plan = _np(step.plan()).astype(np.int64)
+    hdr = plan[:HEADER]
+    assert hdr[0] == 0x50384B53 and hdr[1] == len(lens) and hdr[2] == step.max_ctx and hdr[8] == hkv
+    w, ghost = int(hdr[3]), int(hdr[6])
+    ent = plan[HEADER: HEADER + ENTRY * w].reshape(w, ENTRY)
+    stream = np.where(lens > 0, (lens + 31) // 32 * 32 + ghost, 0)
+    total = int(stream.sum())
+    starts = np.concatenate([[0], np.cumsum(stream)])
+    assert (ent[:, 0] == total).all()
+    cut = ent[:, 1] < total  # slices inside the stream (the rest hold nothing)
+    lo, hi = ent[cut, 1], ent[cut, 2]
+    n_in = int(cut.sum())
+    assert cut[:n_in].all() and not cut[n_in:].any(), "the slices inside the stream come first"
+    assert lo[0] == 0 and hi[-1] == total and (lo[1:] == hi[:-1]).all() and (lo < hi).all()
+    for e in ent[ent[:, 5] > 0]:
+        b, pb, L = int(e[3]), int(e[4]), int(e[5])
+        assert pb == starts[b] and L == lens[b], "first segment: row start and length"
+        s0 = max(int(e[1]), pb + ghost) - (pb + ghost)
+        s1 = min(int(e[2]), pb + ghost + (L + 31) // 32 * 32) - (pb + ghost)
+        for wv in range(4):
+            tb = s0 + 32 * wv
+            if tb < min(s1, s0 + 2048, L):
+                blk = int(case.block_table[b, tb // bs])
+                assert e[12 + wv] == (blk * hkv) * bs + tb % bs, f"row {b}: wave {wv}'s first tile"
+            else:
+                assert e[12 + wv] == -1
+
+
+def test_planned_step_graph_replays():
+    """The plan launch and three layers' planned decode launches captured in
+    one graph: every replay returns the eager outputs and cache bytes."""
+    case = make_case(4444, 16, 32, 8, 128, 256, np.random.default_rng(9).integers(200, 5000, size=16).tolist(),
+                     outlier_channels=2)
+    step = _Step(case, "int8")
+    eager = step.run(None)
+    caches = [[_t(x) for x in step.pre] for _ in range(3)]
+    c = case
+
+    def body():
+        plan = ops.attn_paged_decode_plan(caches[0][0], step.bt, step.cl, c.block_size, num_q_heads=c.num_q_heads,
+                                          max_context_len=step.max_ctx)
+        return [ops.attn_paged_decode_append(step.q, step.kn, step.vn, *cache, step.bt, step.cl, c.block_size,
+                                             max_context_len=step.max_ctx, scale=c.scale, plan=plan)
+                for cache in caches]
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = body()
+    for _ in range(3):
+        torch.zeros(1 << 20, device=DEV).add_(1.0)  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for out, cache in zip(outs, caches):
+            _same((_np(out.float()), [_np(x) for x in cache]), eager, "graph replay")
