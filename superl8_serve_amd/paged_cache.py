@@ -488,23 +488,36 @@ class PagedKVCache:
                                        torch.tensor(ctx, dtype=torch.int32, device=self.device),
                                        max(ctx) if ctx else 0, scale=scale, window=window)
 
+    def decode_step_plan(self, block_table: torch.Tensor, context_lens: torch.Tensor, max_context_len: int, *,
+                         num_q_heads: int) -> torch.Tensor:
+        """The slice plan one decode step's ``decode_step_static`` calls can
+        share: every layer of a step reads the same ``block_table`` and
+        ``context_lens`` (these tensors, with unchanged contents), so the split
+        of the rows' tokens over the decode workgroups is computed once, on the
+        device, instead of in every layer's launch."""
+        return ops.attn_paged_decode_plan(self.k_cache[0], block_table, context_lens, self.block_size,
+                                          num_q_heads=num_q_heads, max_context_len=max_context_len,
+                                          layout="k8v3" if self.v_quant == "lloydmax3" else "int8")
+
     def decode_step_static(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                            block_table: torch.Tensor, context_lens: torch.Tensor, max_context_len: int, *,
-                           scale: float) -> torch.Tensor:
+                           scale: float, plan: torch.Tensor | None = None) -> torch.Tensor:
         """``write_decode_static`` + ``decode_attn_static`` in one launch (int8
         and K8V3 layouts): row b's new token goes to position ``context_lens[b] - 1``
         of its block table (where the reference's decode step writes it,
         kv_cache.py:1083-1093 with 1129-1146), then the row attends.  Same
-        cache bytes and output as the two calls."""
+        cache bytes and output as the two calls.  ``plan``: the step's
+        ``decode_step_plan`` (same results, the launch skips locating its work)."""
         row = self._layer_row(layer)
         if self.v_quant == "lloydmax3":
             return ops.attn_paged_decode_append_k8v3(
                 q, k_new, v_new, self.k_cache[row], self.k_scale[row], self.v_packed[row], self.v_norm[row],
                 self.v_codebook[row], block_table, context_lens, self.block_size, max_context_len=max_context_len,
-                scale=scale)
+                scale=scale, plan=plan)
         return ops.attn_paged_decode_append(q, k_new, v_new, self.k_cache[row], self.k_scale[row],
                                             self.v_cache[row], self.v_scale[row], block_table, context_lens,
-                                            self.block_size, max_context_len=max_context_len, scale=scale)
+                                            self.block_size, max_context_len=max_context_len, scale=scale,
+                                            plan=plan)
 
     def decode_step(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                     slots: list[int], lengths: list[int], *, scale: float) -> torch.Tensor:

@@ -220,3 +220,45 @@ def test_planned_step_graph_replays():
         torch.cuda.synchronize()
         for out, cache in zip(outs, caches):
             _same((_np(out.float()), [_np(x) for x in cache]), eager, "graph replay")
+
+
+@pytest.mark.parametrize("v_quant", ["int8", "lloydmax3"])
+def test_host_cache_decode_step_with_plan(v_quant):
+    """PagedKVCache: one plan per step shared by every layer's
+    decode_step_static equals the unplanned calls, cache bytes and outputs."""
+    import math
+
+    from superl8_serve_amd.paged_cache import PagedKVCache
+
+    hq, hkv, d, bs, layers = 32, 8, 128, 256, 3
+    lens = [700, 1, 2500, 256, 90]
+    g = torch.Generator(device=DEV).manual_seed(12)
+    caches = [PagedKVCache(layers, len(lens), hkv, 4096, d, device=DEV, block_size=bs, v_quant=v_quant)
+              for _ in range(2)]
+    for c in caches:
+        slots = [c.alloc() for _ in lens]
+        c.ensure_capacity(slots, [n + 1 for n in lens])
+    for layer in range(layers):
+        for s, n in zip(slots, lens):
+            k = torch.randn(1, hkv, n, d, generator=g, device=DEV).half()
+            v = torch.randn(1, hkv, n, d, generator=g, device=DEV).half()
+            for c in caches:
+                c.write_prefill(layer, k, v, slot=s)
+    kn = [torch.randn(len(lens), hkv, d, generator=g, device=DEV).half() for _ in range(layers)]
+    vn = [torch.randn(len(lens), hkv, d, generator=g, device=DEV).half() for _ in range(layers)]
+    q = [torch.randn(len(lens), hq, 1, d, generator=g, device=DEV).half() for _ in range(layers)]
+    bt = caches[0].block_table(slots)
+    ctx = [n + 1 for n in lens]
+    cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(d)
+    plan = caches[1].decode_step_plan(bt, cl, max(ctx), num_q_heads=hq)
+    for layer in range(layers):
+        ref = caches[0].decode_step_static(layer, q[layer], kn[layer], vn[layer], bt, cl, max(ctx), scale=scale)
+        out = caches[1].decode_step_static(layer, q[layer], kn[layer], vn[layer], bt, cl, max(ctx), scale=scale,
+                                           plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"layer {layer}"
+    names = (("k_cache", "k_scale", "v_cache", "v_scale") if v_quant == "int8"
+             else ("k_cache", "k_scale", "v_packed", "v_norm"))
+    for name in names:
+        assert torch.equal(getattr(caches[0], name), getattr(caches[1], name)), name
