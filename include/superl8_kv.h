@@ -202,8 +202,10 @@ int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim,
  * launch then issues its first K/V loads at once.  Same cache bytes and
  * outputs as the unplanned calls (the plan holds exactly what their prologue
  * computes).  A plan whose header names another geometry or other buffers is
- * ignored (the launch locates its work itself).  Replace the same reference
- * calls as the unplanned forms.
+ * ignored (the launch locates its work itself).  plan_bytes: the plan
+ * buffer's size, at least s8kv_decode_plan_size(num_kv_heads) (smaller:
+ * S8KV_ERR_INVALID).  Replace the same reference calls as the unplanned
+ * forms.
  */
 int s8kv_decode_append_int8_planned(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                     int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
@@ -212,7 +214,8 @@ int s8kv_decode_append_int8_planned(const void* q, int batch, int num_q_heads, i
                                     int8_t* v_cache, float* v_scale, int64_t num_blocks, int block_size,
                                     const int32_t* block_table, int64_t block_table_stride,
                                     const int32_t* context_lens, int max_context_len, float scale, void* out,
-                                    void* workspace, int64_t workspace_bytes, void* stream, const void* plan);
+                                    void* workspace, int64_t workspace_bytes, void* stream, const void* plan,
+                                    int64_t plan_bytes);
 int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                     int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
                                     int64_t k_new_stride_b, int64_t k_new_stride_h, const void* v_new,
@@ -221,7 +224,7 @@ int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num_q_heads, i
                                     int64_t num_blocks, int block_size, const int32_t* block_table,
                                     int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
                                     float scale, void* out, void* workspace, int64_t workspace_bytes, void* stream,
-                                    const void* plan);
+                                    const void* plan, int64_t plan_bytes);
 
 /*
  * Decode attention over the K8V3 cache (int8 K, 3-bit Lloyd-Max V dequantized

@@ -72,7 +72,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
         _c_void_p, _i64, _c_void_p,
-        _i32, _f32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+        _i32, _f32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
     ]),
     "s8kv_decode_append_k8v3_planned": (_i32, [
         _c_void_p, _i32, _i32, _i32, _i32,
@@ -80,7 +80,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i32,
         _c_void_p, _i64, _c_void_p,
-        _i32, _f32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+        _i32, _f32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
     ]),
     "s8kv_decode_plan_size": (_i64, [_i32]),
     "s8kv_decode_plan": (_i32, [

@@ -1564,7 +1564,7 @@ static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int
 }
 // Slice plan: header + one entry per workgroup column, for the largest grid
 // a launch of this geometry may use.
-static int64_t plan_bytes(int num_kv_heads) {
+static int64_t plan_bytes_for(int num_kv_heads) {
   return (int64_t)(kPlanHeader + kPlanEntry * max_wg_per_head(num_kv_heads)) * 4;
 }
 
@@ -1618,9 +1618,9 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
   if (plan_only) {
-    S8KV_REQUIRE(workspace_bytes_given >= plan_bytes(num_kv_heads) && (uintptr_t)a.plan_out % 4 == 0,
+    S8KV_REQUIRE(workspace_bytes_given >= plan_bytes_for(num_kv_heads) && (uintptr_t)a.plan_out % 4 == 0,
                  S8KV_ERR_INVALID, "decode_plan: a plan of %lld bytes (4-byte aligned) is needed, %lld given",
-                 (long long)plan_bytes(num_kv_heads), (long long)workspace_bytes_given);
+                 (long long)plan_bytes_for(num_kv_heads), (long long)workspace_bytes_given);
   } else {
     const int64_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
     S8KV_REQUIRE(workspace != nullptr && workspace_bytes_given >= need, S8KV_ERR_WORKSPACE,
@@ -1823,9 +1823,13 @@ extern "C" int s8kv_decode_append_int8_planned(const void* q, int batch, int num
                                                int64_t num_blocks, int block_size, const int32_t* block_table,
                                                int64_t block_table_stride, const int32_t* context_lens,
                                                int max_context_len, float scale, void* out, void* workspace,
-                                               int64_t workspace_bytes, void* stream, const void* plan) {
+                                               int64_t workspace_bytes, void* stream, const void* plan,
+                                               int64_t plan_bytes) {
   S8KV_REQUIRE(plan != nullptr && (uintptr_t)plan % 4 == 0, S8KV_ERR_INVALID,
                "decode_append_int8_planned: null or unaligned plan");
+  S8KV_REQUIRE(plan_bytes >= plan_bytes_for(num_kv_heads), S8KV_ERR_INVALID,
+               "decode_append_int8_planned: a plan of %lld bytes is needed, %lld given",
+               (long long)plan_bytes_for(num_kv_heads), (long long)plan_bytes);
   return decode_append_int8_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
                                  k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
                                  k_scale, v_cache, v_scale, num_blocks, block_size, block_table, block_table_stride,
@@ -1928,9 +1932,13 @@ extern "C" int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num
                                                int block_size, const int32_t* block_table, int64_t block_table_stride,
                                                const int32_t* context_lens, int max_context_len, float scale,
                                                void* out, void* workspace, int64_t workspace_bytes, void* stream,
-                                               const void* plan) {
+                                               const void* plan,
+                                               int64_t plan_bytes) {
   S8KV_REQUIRE(plan != nullptr && (uintptr_t)plan % 4 == 0, S8KV_ERR_INVALID,
                "decode_append_k8v3_planned: null or unaligned plan");
+  S8KV_REQUIRE(plan_bytes >= plan_bytes_for(num_kv_heads), S8KV_ERR_INVALID,
+               "decode_append_k8v3_planned: a plan of %lld bytes is needed, %lld given",
+               (long long)plan_bytes_for(num_kv_heads), (long long)plan_bytes);
   return decode_append_k8v3_impl(q, batch, num_q_heads, num_kv_heads, head_dim, q_stride_b, q_stride_h, k_new,
                                  k_new_stride_b, k_new_stride_h, v_new, v_new_stride_b, v_new_stride_h, k_cache,
                                  k_scale, v_packed, v_norm, v_codebook, lloyd_block, num_blocks, block_size,
@@ -1939,7 +1947,7 @@ extern "C" int s8kv_decode_append_k8v3_planned(const void* q, int batch, int num
 }
 
 extern "C" int64_t s8kv_decode_plan_size(int num_kv_heads) {
-  return num_kv_heads > 0 ? plan_bytes(num_kv_heads) : 0;
+  return num_kv_heads > 0 ? plan_bytes_for(num_kv_heads) : 0;
 }
 
 extern "C" int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,

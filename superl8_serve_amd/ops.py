@@ -289,10 +289,12 @@ def attn_paged_decode_plan(k_cache, block_table, context_lens, block_size, *, nu
     return plan
 
 
-def _plan_ptr(plan, dev):
+def _plan_args(plan, dev):
+    """(pointer, bytes) of a plan tensor, for the planned C entry points
+    (which reject a plan smaller than the geometry needs)."""
     _on_gpu("plan", plan, torch.int32, dev)
     _require(plan.is_contiguous(), "plan must be contiguous")
-    return plan.data_ptr()
+    return plan.data_ptr(), plan.numel() * 4
 
 
 def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale, block_table, context_lens,
@@ -342,7 +344,7 @@ def attn_paged_decode_append(q, k_new, v_new, k_cache, k_scale, v_cache, v_scale
     if plan is None:
         rc = lib.s8kv_decode_append_int8(*args)
     else:
-        rc = lib.s8kv_decode_append_int8_planned(*args, _plan_ptr(plan, dev))
+        rc = lib.s8kv_decode_append_int8_planned(*args, *_plan_args(plan, dev))
     _lib.check(rc, "attn_paged_decode_append")
     return out
 
@@ -389,7 +391,7 @@ def attn_paged_decode_append_k8v3(q, k_new, v_new, k_cache, k_scale, v_packed, v
     if plan is None:
         rc = lib.s8kv_decode_append_k8v3(*args)
     else:
-        rc = lib.s8kv_decode_append_k8v3_planned(*args, _plan_ptr(plan, dev))
+        rc = lib.s8kv_decode_append_k8v3_planned(*args, *_plan_args(plan, dev))
     _lib.check(rc, "attn_paged_decode_append_k8v3")
     return out
 

@@ -262,3 +262,14 @@ def test_host_cache_decode_step_with_plan(v_quant):
              else ("k_cache", "k_scale", "v_packed", "v_norm"))
     for name in names:
         assert torch.equal(getattr(caches[0], name), getattr(caches[1], name)), name
+
+
+def test_plan_smaller_than_the_geometry_needs_is_rejected():
+    """A plan buffer shorter than s8kv_decode_plan_size(num_kv_heads) is an
+    invalid argument (checked on the host before any launch)."""
+    case = make_case(4545, 4, 32, 8, 128, 256, [300, 40, 1000, 7])
+    step = _Step(case, "int8")
+    plan = step.plan()
+    with pytest.raises(ValueError, match="plan"):
+        step.run(plan[:HEADER + ENTRY])
+    _same(step.run(plan), step.run(None), "full-size plan")
