@@ -123,7 +123,7 @@ constexpr int kSubTokens = 2048;                         // block ids are staged
 constexpr int kMaxSubBlocks = kSubTokens / 4 + 2;        // block_size >= 4
 constexpr int kMaxResidentPerCU = 8;                     // bound used to size the workspace
 constexpr int kLensLds = 1024;                           // context lengths kept in LDS (rows beyond: global reads)
-constexpr int kGhostTokens = 256;                        // stream tokens charged per row start
+constexpr int kGhostTokens = 192;                        // stream tokens charged per row start
 constexpr int kSlotSkewPermille = 200;                   // slice weight skew across residency slots
 constexpr int kQHeadsPerWave = 4;                        // q heads a wave rotates (group <= 16, 4 waves)
 
