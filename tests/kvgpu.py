@@ -51,9 +51,15 @@ def decode(kind, q, cache, bt, lens, bs, max_ctx, scale):
     return fn(q, *cache, *_codebook(kind), bt, lens, bs, max_context_len=max_ctx, scale=scale)
 
 
-def decode_append(kind, q, k_new, v_new, cache, bt, lens, bs, max_ctx, scale):
+def decode_append(kind, q, k_new, v_new, cache, bt, lens, bs, max_ctx, scale, plan=None):
     fn = ops.attn_paged_decode_append if kind == "int8" else ops.attn_paged_decode_append_k8v3
-    return fn(q, k_new, v_new, *cache, *_codebook(kind), bt, lens, bs, max_context_len=max_ctx, scale=scale)
+    return fn(q, k_new, v_new, *cache, *_codebook(kind), bt, lens, bs, max_context_len=max_ctx, scale=scale,
+              plan=plan)
+
+
+def decode_plan(kind, cache, bt, lens, bs, hq, max_ctx):
+    return ops.attn_paged_decode_plan(cache[0], bt, lens, bs, num_q_heads=hq, max_context_len=max_ctx,
+                                      layout="int8" if kind == "int8" else "k8v3")
 
 
 def verify(kind, q, cache, bt, prefix, query_lens, bs, max_ctx, scale):

@@ -26,7 +26,8 @@ import torch
 from oracle import kv_oracle as O
 from superl8_serve_amd import ops
 from tests.kvcase import empty_int8_cache, empty_k8v3_cache, make_case, make_needle_case, needle_reference
-from tests.kvgpu import CODEBOOK, DEV, KINDS, alloc, append, assert_close, decode, decode_append, layer, t, to_np, verify
+from tests.kvgpu import (CODEBOOK, DEV, KINDS, alloc, append, assert_close, decode, decode_append, decode_plan, layer, t,
+                         to_np, verify)
 
 pytestmark = pytest.mark.gpu
 
@@ -205,6 +206,12 @@ def test_rows_at_the_edges_of_a_large_pool(kind, pool):
         q, btt, cl = t(case.q), t(bt), t(lens.astype(np.int32))
         max_ctx = int(lens.max())
         fused = to_np(decode_append(kind, q, t(k_new), t(v_new), cache, btt, cl, bs, max_ctx, case.scale).float())
+        # the planned launch (its first tiles through the plan's rows; the
+        # append rewrites the same bytes): the same output
+        plan = decode_plan(kind, cache, btt, cl, bs, hq, max_ctx)
+        planned = to_np(decode_append(kind, q, t(k_new), t(v_new), cache, btt, cl, bs, max_ctx, case.scale,
+                                      plan=plan).float())
+        assert np.array_equal(planned, fused), f"{kind} {pool}: the planned step differs"
         compact = tuple(to_np(x.index_select(0, t(ids))) for x in cache)
         _assert_same_bytes(compact, _oracle_fill(kind, case), f"{kind} {pool} pool")
         out = to_np(decode(kind, q, cache, btt, cl, bs, max_ctx, case.scale).float())
@@ -308,6 +315,11 @@ def test_decode_through_a_whole_pool(pool):
         _assert_same_bytes(got, want, "whole-pool fused append")
         nc.k_i8[0], nc.k_scale[0], nc.v_i8[0], nc.v_scale[0] = want[0][0], want[1][0], want[2][0], want[3][0]
         assert_close(to_np(out.float())[0], needle_reference(nc, n), "whole-pool fused decode-append")
+        # planned (the append rewrites the same bytes): the same output
+        plan = ops.attn_paged_decode_plan(kc, btt, cl, bs, num_q_heads=q.shape[1], max_context_len=n)
+        again = ops.attn_paged_decode_append(q, t(k_new), t(v_new), kc, ks, vc, vs, btt, cl, bs, max_context_len=n,
+                                             scale=nc.scale, plan=plan)
+        assert torch.equal(again, out), "whole-pool planned decode-append differs"
     finally:
         cache.clear()
         torch.cuda.empty_cache()
