@@ -2,11 +2,11 @@
 // draft query sees the prefix plus its ancestors in the draft tree) and
 // chunked prefill / chain verify (query s sees the prefix plus drafts 0..s).
 //
-// Layout of the work: a workgroup of 4 waves owns 64 * RG query rows of one
-// (sequence, KV head) pair -- row r is query position r / G of q head
+// Layout of the work: a workgroup of W waves (4; 8 for K8V3) owns 16 * W * RG
+// query rows of one (sequence, KV head) pair -- row r is query position r / G of q head
 // h*G + r % G -- and streams the pair's keys in 32-key tiles.  Each tile's K
 // and V rows are loaded once per workgroup, converted int8 -> fp16 (exact) on
-// the way into LDS (double-buffered), and shared by the 4 waves (K8V3: V's
+// the way into LDS (double-buffered), and shared by its waves (K8V3: V's
 // 3-bit codes become the fp16 codebook entries, as in the decode kernel); a
 // wave owns RG groups of 16 query rows (RG = 2 for head_dim 64, else 1),
 // each group the 16 columns of its own MFMA tiles, and every K and V operand a
@@ -33,8 +33,9 @@
 namespace s8kv {
 namespace verify {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+// Waves per workgroup: 4, or 8 for the K8V3 layout, whose V-code expansion
+// into LDS (VALU work per tile) is then shared by twice the query rows.
+template <bool K8V3> constexpr int kWavesOf = K8V3 ? 8 : 4;
 constexpr int kTile = 32;
 constexpr int kSubKeys = 2048;                 // block ids staged in LDS per 2048 keys
 constexpr int kMaxSubBlocks = kSubKeys / 4 + 2;  // block_size >= 4
@@ -48,7 +49,9 @@ constexpr float kMaxInit = -1.0e30f;
 template <int D, bool K8V3>
 struct Cfg {
   static constexpr int RG = D <= 64 ? 2 : 1;         // 16-row groups per wave (as registers allow)
-  static constexpr int ROWS = 16 * RG * kWaves;      // query rows per workgroup
+  static constexpr int WAVES = kWavesOf<K8V3>;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int ROWS = 16 * RG * WAVES;       // query rows per workgroup
   static constexpr int KCH = D / 4;      // dims per lane per key row (MFMA A / B chunk of the lane group)
   static constexpr int NQK = D / 32;     // QK MFMAs per 16-key subtile
   static constexpr int NPV = D / 16;     // PV MFMAs per tile
@@ -62,14 +65,14 @@ struct Cfg {
   static constexpr int SBYTES = (1 + NB) * kTile * 4;  // k_scale, then the V scales of each block
   static constexpr int BUF = KBYTES + VBYTES + SBYTES;
   static constexpr int CHUNKS = kTile * D / 16;                 // 16-byte int8 chunks per K (or V) tile
-  static constexpr int LOADS = (CHUNKS + kThreads - 1) / kThreads;
+  static constexpr int LOADS = (CHUNKS + THREADS - 1) / THREADS;
   static constexpr int CHUNKS_F16 = kTile * D / 8;              // dense fp16 inputs: 16-byte chunks per tile
-  static constexpr int LOADS_F16 = (CHUNKS_F16 + kThreads - 1) / kThreads;
+  static constexpr int LOADS_F16 = (CHUNKS_F16 + THREADS - 1) / THREADS;
   // K8V3: a code group's 32 values are expanded by SPLIT threads (16 values
   // each when the tile has fewer groups than the workgroup has threads)
-  static constexpr int SPLIT = kTile * NG < kThreads ? kThreads / (kTile * NG) : 1;
+  static constexpr int SPLIT = kTile * NG < THREADS ? (THREADS >= 2 * kTile * NG ? 2 : 1) : 1;
   static constexpr int VJOBS = kTile * NG * SPLIT;              // K8V3: expansion jobs per tile
-  static_assert(!K8V3 || (VJOBS <= kThreads && (SPLIT == 1 || SPLIT == 2)), "one K8V3 job per thread");
+  static_assert(!K8V3 || (VJOBS <= THREADS && (SPLIT == 1 || SPLIT == 2)), "one K8V3 job per thread");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
   // window verify with fresh drafts: the low fp16 part of the draft keys'
   // fp32 K, one K-sized tile per buffer after the block ids
@@ -129,7 +132,7 @@ struct VerifyArgs {
 __device__ __forceinline__ int vrow_of(int tt) { return 8 * ((tt & 15) >> 2) + 4 * (tt >> 4) + (tt & 3); }
 
 template <int D, bool K8V3, bool WIN = false, bool DENSE = false, bool BIG = false>
-__global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
+__global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kernel(VerifyArgs a) {
   static_assert(!DENSE || !K8V3, "dense inputs: fp16 K / V");
   static_assert(!DENSE || !BIG, "dense inputs are not paged");
   using C = Cfg<D, K8V3>;
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   uint64_t tmask[RG];
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
-    const int r = row0 + (rg * kWaves + wave) * 16 + c;
+    const int r = row0 + (rg * C::WAVES + wave) * 16 + c;
     pos[rg] = r / G;
     head[rg] = h * G + (r - pos[rg] * G);
     row_live[rg] = pos[rg] < nq;
@@ -291,7 +294,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
     const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
     __syncthreads();  // previous users of bt_lds and the tile buffers are done
     if constexpr (!DENSE)
-      for (int i = tid; i < nblk; i += kThreads) bt_lds[i] = bt_row[fb + i];
+      for (int i = tid; i < nblk; i += C::THREADS) bt_lds[i] = bt_row[fb + i];
     __syncthreads();
 
     // storage row of key kk (clamped to the last key, so every address is a real row)
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       if constexpr (DENSE) {  // fp16 K / V rows of keys base .. base+31 (clamped to the last key)
 #pragma unroll
         for (int i = 0; i < C::LOADS_F16; ++i) {
-          const int ch = tid + i * kThreads;
+          const int ch = tid + i * C::THREADS;
           if (ch < C::CHUNKS_F16) {
             const int tt = ch / (D / 8), part = ch % (D / 8);
             const int64_t tok = k0 + min(base + tt, nk - 1);
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
         const rsrc_t vst = window_rsrc(a.v_scale, a.vs_total, (uint64_t)r0 * (C::NB * 4u));
 #pragma unroll
         for (int i = 0; i < C::LOADS; ++i) {
-          const int ch = tid + i * kThreads;
+          const int ch = tid + i * C::THREADS;
           if (ch < C::CHUNKS) {
             const int tt = ch / (D / 16), part = ch % (D / 16);
             const uint32_t off = local(tt) * (uint32_t)D + (uint32_t)part * 16u;
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < C::LOADS; ++i) {
-        const int ch = tid + i * kThreads;
+        const int ch = tid + i * C::THREADS;
         if (ch < C::CHUNKS) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
           const uint32_t row = row_of(base + tt);
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       if constexpr (DENSE) {
 #pragma unroll
         for (int i = 0; i < C::LOADS_F16; ++i) {
-          const int ch = tid + i * kThreads;
+          const int ch = tid + i * C::THREADS;
           if (ch < C::CHUNKS_F16) {
             const int tt = ch / (D / 8), part = ch % (D / 8);
             *reinterpret_cast<u32x4_t*>(kb + tt * C::KROW + part * 16) = R.k[i];
@@ -423,7 +426,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < C::LOADS; ++i) {
-        const int ch = tid + i * kThreads;
+        const int ch = tid + i * C::THREADS;
         if (ch < C::CHUNKS) {
           const int tt = ch / (D / 16), part = ch % (D / 16);
           const int di = fresh_draft(tt);
@@ -744,7 +747,7 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
       const float l_tot = sum_x32(sum_x16(l_run[rg]));
-      const int rl = (rg * kWaves + wave) * 16 + c;  // row within the block
+      const int rl = (rg * C::WAVES + wave) * 16 + c;  // row within the block
       float* pr = a.part + ((((int64_t)p * a.n_qblocks + qb) * a.splits + sp) * C::ROWS + rl) * (D + 4);
 #pragma unroll
       for (int n = 0; n < C::NPV; ++n) *reinterpret_cast<float4_t*>(pr + 16 * n + 4 * g) = acc[rg][n];
@@ -776,8 +779,10 @@ __global__ __launch_bounds__(kThreads, 2) void verify_kernel(VerifyArgs a) {
   }
 }
 
-// Query rows per workgroup at this head_dim (Cfg<D, *>::ROWS).
-static int rows_per_wg(int head_dim) { return 16 * kWaves * (head_dim <= 64 ? 2 : 1); }
+// Query rows per workgroup at this head_dim and layout (Cfg<D, K8V3>::ROWS),
+// and the workgroups a CU keeps resident (the kernel's launch bounds).
+static int rows_per_wg(int head_dim, bool k8v3) { return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1); }
+static int wg_per_cu(bool k8v3) { return k8v3 ? 1 : 2; }
 
 // Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
 // KV head, query block) merges the row's `splits` partials -- each relative to
@@ -785,9 +790,8 @@ static int rows_per_wg(int head_dim) { return 16 * kWaves * (head_dim <= 64 ? 2 
 // normalized fp16 dims.  Workgroup x covers items kCombineThreads * (x %
 // blocks_per_unit) .. of unit x / blocks_per_unit.
 constexpr int kCombineThreads = 256;
-template <int D>
+template <int D, int ROWS>
 __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyArgs a) {
-  constexpr int ROWS = 16 * kWaves * (D <= 64 ? 2 : 1);
   constexpr int V4 = D / 4;
   constexpr int BLOCKS = ROWS * V4 / kCombineThreads;  // workgroups per unit
   static_assert(ROWS * V4 % kCombineThreads == 0, "whole workgroups per unit");
@@ -853,7 +857,7 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
 
 template <int D, bool K8V3, bool WIN, bool DENSE, bool BIG>
 static int launch_impl(VerifyArgs& a, hipStream_t stream) {
-  static_assert(Cfg<D, K8V3>::ROWS == 16 * kWaves * (D <= 64 ? 2 : 1), "rows_per_wg");
+  static_assert(Cfg<D, K8V3>::ROWS == 16 * kWavesOf<K8V3> * (D <= 64 ? 2 : 1), "rows_per_wg");
   using C = Cfg<D, K8V3>;
   static bool attr = false;
   if (!attr) {
@@ -870,13 +874,13 @@ static int launch_impl(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE, BIG>), dim3((unsigned)grid), dim3(kThreads),
+  hipLaunchKernelGGL((verify_kernel<D, K8V3, WIN, DENSE, BIG>), dim3((unsigned)grid), dim3(C::THREADS),
                      WIN ? C::SMEM_WIN : C::SMEM, stream, a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
     const int64_t units = (int64_t)P * a.n_qblocks;
-    hipLaunchKernelGGL((verify_combine_kernel<D>), dim3((unsigned)(units * (C::ROWS * (D / 4) / kCombineThreads))),
+    hipLaunchKernelGGL((verify_combine_kernel<D, C::ROWS>), dim3((unsigned)(units * (C::ROWS * (D / 4) / kCombineThreads))),
                        dim3(kCombineThreads), 0, stream, a);
     return check_launch("s8kv_verify_combine");
   }
@@ -915,9 +919,9 @@ struct FreshDrafts {
 constexpr int kMinSplitKeys = 1024;
 constexpr int kMaxSplitKeys = 1 << 20;
 constexpr int kMaxSplits = 1024;
-static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys) {
+static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3) {
   const int64_t natural = (int64_t)batch * num_kv_heads * n_qblocks;
-  const int64_t resident = (int64_t)2 * device_cus();
+  const int64_t resident = (int64_t)verify::wg_per_cu(k8v3) * device_cus();
   int64_t s = natural < resident ? (resident + natural - 1) / natural : 1;
   s = std::min<int64_t>(s, std::max(1, keys / kMinSplitKeys));
   s = std::max<int64_t>(s, ((int64_t)keys + kMaxSplitKeys - 1) / kMaxSplitKeys);
@@ -927,9 +931,9 @@ static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int ke
   }
   return (int)std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
 }
-static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits) {
+static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits, bool k8v3) {
   if (splits <= 1) return 0;
-  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim) * (head_dim + 4) * 4;
+  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim, k8v3) * (head_dim + 4) * 4;
 }
 
 extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -937,21 +941,28 @@ extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int nu
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_queries <= 0 ||
       max_context_len < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
-  const int rows_wg = verify::rows_per_wg(head_dim);
-  const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
-  return verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
-                           verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len));
+  // either layout (its workgroups differ in query rows): the larger need
+  int64_t need = 0;
+  for (const bool k8v3 : {false, true}) {
+    const int rows_wg = verify::rows_per_wg(head_dim, k8v3);
+    const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
+    need = std::max(need, verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
+                                            verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len, k8v3),
+                                            k8v3));
+  }
+  return need;
 }
 
 // The split for this call (keys: the most any block reads -- a window layer's
 // window and drafts), used when the caller's workspace holds its partials;
 // never more than s8kv_verify_workspace_size plans for, which counts
 // max_context_len keys.
-static void verify_use_workspace(verify::VerifyArgs& a, int head_dim, void* workspace, int64_t workspace_bytes) {
+static void verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, void* workspace,
+                                 int64_t workspace_bytes) {
   const int keys = a.window > 0 ? (int)std::min<int64_t>(a.max_context_len, (int64_t)a.window + a.max_queries)
                                 : a.max_context_len;
-  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys);
-  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s);
+  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3);
+  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3);
   if (s > 1 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0) {
     a.splits = s;
     a.part = (float*)workspace;
@@ -964,7 +975,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
                         const int8_t* k_cache, const float* k_scale, int64_t num_blocks, int block_size,
                         const int32_t* block_table, int64_t block_table_stride, const int32_t* prefix_lens,
                         const int32_t* query_lens, const int64_t* tree_mask, int max_context_len, float scale,
-                        void* out) {
+                        void* out, bool k8v3) {
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
@@ -1004,7 +1015,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  const int rows_wg = verify::rows_per_wg(head_dim);
+  const int rows_wg = verify::rows_per_wg(head_dim, k8v3);
   a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
@@ -1025,10 +1036,10 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  verify_use_workspace(a, head_dim, workspace, workspace_bytes);
+  verify_use_workspace(a, head_dim, false, workspace, workspace_bytes);
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -1117,10 +1128,10 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  verify_use_workspace(a, head_dim, workspace, workspace_bytes);
+  verify_use_workspace(a, head_dim, true, workspace, workspace_bytes);
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -1218,7 +1229,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.max_queries = max_seqlen_q;
   a.max_context_len = max_seqlen_k;
   a.bs_log2 = 5;
-  const int rows_wg = verify::rows_per_wg(head_dim);
+  const int rows_wg = verify::rows_per_wg(head_dim, false);
   a.n_qblocks = (a.group * max_seqlen_q + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634);  // K is not rotated: no 1/sqrt(D)
   a.cu_q = cu_seqlens_q;
