@@ -289,6 +289,8 @@ int s8kv_decode_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * units than the GPU keeps resident, or with more than 2^20 keys per unit,
  * split each unit's keys across workgroups and combine their partials in a
  * second kernel on the same stream.  Calls that overlap on one workspace race.
+ * The size covers both layouts (s8kv_verify_int8 and s8kv_verify_k8v3 group
+ * query rows differently).
  */
 int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
                                    int max_context_len);
