@@ -877,7 +877,7 @@ def run_prefill(steps: int, warmup: int) -> None:
         "metric": "dense causal prefill attention TFLOP/s (fresh fp16 K/V), 16 x 4096 tokens, Qwen3-8B heads",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_layer": round(sec * 1e3, 4), "higher_is_better": True,
-        "dtype": "fp16 inputs, fp16 MFMA (hi+lo split q and P), fp32 accumulate",
+        "dtype": "fp16 inputs, fp16 MFMA (exact fp16 q, hi+lo split P), fp32 accumulate",
         "data": "synthetic (fp16 N(0,1), 2 of 128 channels x20, seed 6)",
         "config": {"workload": "dense varlen prefill attention", "sequences": PREFILL_SEQS, "tokens": PREFILL_LEN,
                    "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "flops_layer": flops},

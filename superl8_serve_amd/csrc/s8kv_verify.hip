@@ -12,7 +12,8 @@
 // each group the 16 columns of its own MFMA tiles, and every K and V operand a
 // wave reads from LDS feeds the MFMAs of all its groups:
 //   QK  : S^T[key][row] on MFMA 16x16x32 f16, A = K rows from LDS, B = the
-//         rotated, pre-scaled q split into fp16 hi + lo (two MFMAs).
+//         rotated, pre-scaled q split into fp16 hi + lo (two MFMAs); dense
+//         inputs: the fp16 q itself (one MFMA), the scale applied to the score.
 //   mask: keys below the prefix are visible to every row; draft key i is
 //         visible to row position s if i <= s (chain) or bit i of the row's
 //         tree mask is set (tree).
@@ -241,6 +242,11 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
       for (int e = 0; e < 8; ++e) {
         // (materialized: hi and lo must both come from this one fp32 value; a
         // fused fp16(x*s) for the lo term can differ from fp16(val) by one ulp)
+        if constexpr (DENSE) {  // q is the fp16 input: exact; the scale multiplies the fp32 score
+          qhi[rg][m][e] = (_Float16)x[8 * m + e];
+          qlo[rg][m][e] = (_Float16)0.0f;
+          continue;
+        }
         const float val = materialize(x[8 * m + e] * a.qscale);
         const _Float16 qh = (_Float16)val;
         qhi[rg][m][e] = qh;
@@ -421,7 +427,8 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
             *reinterpret_cast<u32x4_t*>(vb + vrow_of(tt) * C::VROW + part * 16) = R.v[i];
           }
         }
-        if (tid < 2 * kTile) sb[tid] = R.s;
+        // the K scale slots carry the softmax scale (q is unscaled), the V slots 1
+        if (tid < 2 * kTile) sb[tid] = tid < kTile ? a.qscale : R.s;
         return;
       }
 #pragma unroll
@@ -517,7 +524,7 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
 #pragma unroll
           for (int rg = 0; rg < RG; ++rg) {
             cacc[rg] = mfma16x16x32(ka, qhi[rg][m], cacc[rg]);
-            cacc[rg] = mfma16x16x32(ka, qlo[rg][m], cacc[rg]);
+            if constexpr (!DENSE) cacc[rg] = mfma16x16x32(ka, qlo[rg][m], cacc[rg]);
           }
         }
         if constexpr (WIN && !DENSE) {  // fresh draft keys: K = hi + lo (masked or not)
