@@ -541,6 +541,11 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) sc[rg][s] = cacc[rg];
       }
+      // dense inputs: the softmax runs at raised wave priority, so the other
+      // wave of the SIMD issues its MFMAs around it (+1.6 %; the paged
+      // instantiations gain nothing or lose up to 3 % with it)
+      constexpr bool prio = DENSE;
+      if constexpr (prio) __builtin_amdgcn_s_setprio(1);
       float4_t ksc[2], vsc[2], vsc1[2];  // vsc1: K8V3 head_dim 256, the second block's norms
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -692,6 +697,7 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
             }
           }
         }
+        if constexpr (prio) __builtin_amdgcn_s_setprio(0);
         // PV: each V^T operand read from LDS feeds the MFMAs of every row group
 #pragma unroll
         for (int n = 0; n < C::NPV; ++n) {
