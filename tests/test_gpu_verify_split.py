@@ -102,17 +102,20 @@ def test_split_window_verify(kind, monkeypatch):
     assert_close(got, ref, f"{kind} window verify, 6 splits")
 
 
-def test_batch_one_long_context_plans_a_split():
+@pytest.mark.parametrize("kind", ["int8", "k8v3"])
+def test_batch_one_long_context_plans_a_split(kind):
     """Batch 1 with a 32K prefix and a 32-node tree at Qwen3-8B heads has 16
-    units: the default plan splits them and the result matches the oracle."""
+    units (8 for K8V3, whose workgroups hold 128 query rows): the default
+    plan splits them within the workspace the size query gives for either
+    layout, and the result matches the oracle."""
     nq = 32
     ws = _lib.load().s8kv_verify_workspace_size(1, 32, 8, 128, nq, 32768 + nq)
     assert ws > 0
-    case, cache, host, qv, prefix = _case(970, "int8", 32, 8, 128, 256, [32768], nq)
+    case, cache, host, qv, prefix = _case(970, kind, 32, 8, 128, 256, [32768], nq)
     tm = _random_tree(np.random.default_rng(971), nq)[None]
-    got = _run("int8", case, cache, qv, prefix, tree_mask=tm)
-    ref = O.paged_verify(qv, layer("int8", host), case.block_table, prefix, case.scale, tree_mask=tm)
-    assert_close(got, ref, "batch-1 tree verify (planned split)")
+    got = _run(kind, case, cache, qv, prefix, tree_mask=tm)
+    ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, tree_mask=tm)
+    assert_close(got, ref, f"{kind} batch-1 tree verify (planned split)")
 
 
 def test_split_graph_replays(monkeypatch):
