@@ -615,9 +615,15 @@ class PagedKVCache:
         holes, so the live set occupies blocks ``[0, used_blocks)``.  One GPU
         block copy for all layers and tensors, then every reference (slot
         tables, prefix entries, refcounts, pins) is rewritten.  Returns the
-        ``(src, dst)`` moves."""
+        ``(src, dst)`` moves.
+
+        The live set is every block outside the free list: a block a slot
+        holds need not have a refcount entry (``KVEviction.compact`` takes
+        its new blocks from the pool without one, as the reference does), so
+        the refcount map alone would miss it."""
         used = self.used_blocks
-        live_high = sorted(b for b in self._block_refcount if b >= used)
+        free = set(self._free_blocks)
+        live_high = [b for b in range(used, self.num_blocks) if b not in free]
         holes = sorted(b for b in self._free_blocks if b < used)
         moves = list(zip(live_high, holes))
         if not moves:

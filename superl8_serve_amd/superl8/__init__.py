@@ -14,6 +14,17 @@ the bytes the fused append stores; the dense attention ops
 (``attn_int8_decode`` / ``attn_int8_fwd`` / ``attn_int8_varlen``) run the
 fp16-input prefill kernel.  Every function takes device tensors and raises on
 host tensors: there is no CPU implementation.
+
+Beyond the reference's names, the module also carries the ops a caller adopts
+at the same seam to replace several reference launches by one: the
+one-launch decode step (``attn_paged_decode_append[_k8v3]``, with the step's
+shared slice plan ``attn_paged_decode_plan``) for the write-then-attend pair
+of gqa_attention.py:174-190, the multi-query verify
+(``attn_paged_verify[_k8v3]``) for the S decode launches of
+gqa_attention.py:217-314, the sliding-window decode
+(``attn_paged_decode_window[_k8v3]``) for gqa_attention.py:191-196, the fused
+K8V3 append (``quantize_kv_write_paged_k8v3``) for kv_cache.py:587-626 and the
+block copy (``copy_blocks``) behind copy-on-write and compaction.
 """
 
 from __future__ import annotations
@@ -23,7 +34,20 @@ import math
 import torch
 
 from .. import ops
-from ..ops import attn_paged_decode_cached, attn_paged_decode_k8v3, quantize_kv_write_paged
+from ..ops import (
+    attn_paged_decode_append,
+    attn_paged_decode_append_k8v3,
+    attn_paged_decode_cached,
+    attn_paged_decode_k8v3,
+    attn_paged_decode_plan,
+    attn_paged_decode_window,
+    attn_paged_decode_window_k8v3,
+    attn_paged_verify,
+    attn_paged_verify_k8v3,
+    copy_blocks,
+    quantize_kv_write_paged,
+    quantize_kv_write_paged_k8v3,
+)
 from . import quant
 
 __all__ = [
@@ -36,6 +60,16 @@ __all__ = [
     "attn_int8_fwd",
     "attn_int8_varlen",
     "quant",
+    # one-launch replacements at the same seam (no reference counterpart)
+    "attn_paged_decode_append",
+    "attn_paged_decode_append_k8v3",
+    "attn_paged_decode_plan",
+    "attn_paged_decode_window",
+    "attn_paged_decode_window_k8v3",
+    "attn_paged_verify",
+    "attn_paged_verify_k8v3",
+    "quantize_kv_write_paged_k8v3",
+    "copy_blocks",
 ]
 
 

@@ -104,3 +104,46 @@ def test_oracle_gather_slots_moves_rows_only():
     for d in dst:
         keep[d // 4, d % 4] = False
     assert np.array_equal(u.transpose(1, 3, 0, 2, 4)[keep], t.transpose(1, 3, 0, 2, 4)[keep])
+
+
+def test_defragment_after_compaction_packs_every_live_block(monkeypatch):
+    """Compaction takes its new blocks from the pool without refcount entries
+    (as the reference's does); a later ``defragment`` must still move them
+    below the used watermark.  The byte moves run on host stand-ins built
+    from the oracle's copy and gather, so every token can be followed."""
+    import numpy as np
+
+    from oracle import kv_oracle as O
+    from superl8_serve_amd import ops
+
+    monkeypatch.setattr(ops, "copy_blocks",
+                        lambda ts, src, dst: O.copy_blocks([t.numpy() for t in ts], list(src), list(dst)))
+    monkeypatch.setattr(ops, "gather_slots",
+                        lambda ts, src, dst, bs: O.gather_slots([t.numpy() for t in ts], list(src), list(dst)))
+    bs = 4
+    c = PagedKVCache(num_layers=2, num_slots=4, num_kv_heads=2, max_len=32, head_dim=32, device="cpu",
+                     block_size=bs)
+    rng = np.random.default_rng(5)
+    c.k_cache.copy_(torch.from_numpy(rng.integers(-127, 128, size=tuple(c.k_cache.shape), dtype=np.int8)))
+    c.v_cache.copy_(torch.from_numpy(rng.integers(-127, 128, size=tuple(c.v_cache.shape), dtype=np.int8)))
+    a, b, d = c.alloc(), c.alloc(), c.alloc()
+    c.ensure_capacity([a, b, d], [20, 12, 16])
+    keep = [0, 3, 5, 9, 10, 17]
+    token = lambda s, p: (c.k_cache[:, c._slot_blocks[s][p // bs], :, p % bs].clone(),  # noqa: E731
+                          c.v_cache[:, c._slot_blocks[s][p // bs], :, p % bs].clone())
+    want_a = [token(a, p) for p in keep]
+    want_d = [token(d, p) for p in range(16)]
+    KVEviction.compact(c, a, keep)                       # a's new blocks carry no refcount entry
+    assert any(blk not in c._block_refcount for blk in c._slot_blocks[a])
+    c.free(b)
+    moves = c.defragment()
+    assert moves
+    live = {blk for s in (a, d) for blk in c._slot_blocks[s]}
+    assert len(live) == c.used_blocks and max(live) < c.used_blocks
+    assert set(c._free_blocks) == set(range(c.used_blocks, c.num_blocks))
+    for j, (k0, v0) in enumerate(want_a):
+        k1, v1 = token(a, j)
+        assert torch.equal(k0, k1) and torch.equal(v0, v1)
+    for p, (k0, v0) in enumerate(want_d):
+        k1, v1 = token(d, p)
+        assert torch.equal(k0, k1) and torch.equal(v0, v1)

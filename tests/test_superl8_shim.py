@@ -154,3 +154,44 @@ def test_unsupported_codec_parameters_are_rejected():
         lloydmax.quantize_lloydmax(torch.zeros(1, 128), block_size=64)
     with pytest.raises(ValueError):
         lloydmax.quantize_lloydmax(torch.zeros(1, 128), dim=0)
+
+
+def _integration_calls():
+    """Every ``superl8.X`` / ``ops.X`` attribute named in INTEGRATION.md's
+    code blocks (comments included: they show calls too)."""
+    import re
+
+    text = (Path(__file__).resolve().parent.parent / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    names = set()
+    for blk in blocks:
+        names.update(re.findall(r"\b((?:superl8|ops)(?:\.[A-Za-z_][A-Za-z_0-9]*)+)", blk))
+    return sorted(names)
+
+
+def test_integration_examples_name_only_real_functions():
+    import superl8
+
+    from superl8_serve_amd import ops
+
+    names = _integration_calls()
+    assert any(n.startswith("superl8.attn_paged_verify") for n in names)
+    for name in names:
+        root, *attrs = name.split(".")
+        obj = superl8 if root == "superl8" else ops
+        for attr in attrs:
+            assert hasattr(obj, attr), f"INTEGRATION.md calls {name}, which does not resolve"
+            obj = getattr(obj, attr)
+        assert callable(obj) or inspect.ismodule(obj), name
+
+
+@pytest.mark.parametrize("name", ["attn_paged_decode_append", "attn_paged_decode_append_k8v3",
+                                  "attn_paged_decode_plan", "attn_paged_verify", "attn_paged_verify_k8v3",
+                                  "attn_paged_decode_window", "attn_paged_decode_window_k8v3",
+                                  "quantize_kv_write_paged_k8v3", "copy_blocks"])
+def test_one_launch_ops_are_on_the_superl8_module(name):
+    import superl8
+
+    from superl8_serve_amd import ops
+
+    assert getattr(superl8, name) is getattr(ops, name)
