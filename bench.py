@@ -636,14 +636,16 @@ def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
             "tree_b1": "tree verify (1 x (32768 prefix + 32 draft tree))"}[kind]
     split = {}
     if kind == "tree_b1":  # the same call with the key-range split switched off
-        os.environ["S8KV_VERIFY_SPLITS"] = "1"
+        from superl8_serve_amd import _lib
+
+        _lib.check(_lib.load().s8kv_verify_set_splits(1), "s8kv_verify_set_splits")
         _spin_ahead()
         st.record()
         for i in range(steps * VERIFY_LAYERS):
             layer_ops(i % VERIFY_LAYERS, append=False)
         en.record()
         torch.cuda.synchronize()
-        del os.environ["S8KV_VERIFY_SPLITS"]
+        _lib.check(_lib.load().s8kv_verify_set_splits(0), "s8kv_verify_set_splits")
         t_one = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
         split = {"ms_per_layer_attention_unsplit": round(t_one * 1e3, 4), "split_speedup": round(t_one / t_attn, 2)}
     print(json.dumps({

@@ -284,16 +284,25 @@ int s8kv_decode_window_k8v3(const void* q, int batch, int num_q_heads, int num_k
  * out: fp16 [batch, num_q_heads, max_queries, head_dim] contiguous; queries
  * s >= query_lens[b] produce zeros.  head_dim 64, 128 or 256.
  *
- * workspace (16-byte aligned, s8kv_verify_workspace_size bytes; NULL or
- * smaller: no split) lets a call with fewer (sequence, KV head, query block)
- * units than the GPU keeps resident, or with more than 2^20 keys per unit,
- * split each unit's keys across workgroups and combine their partials in a
- * second kernel on the same stream.  Calls that overlap on one workspace race.
- * The size covers both layouts (s8kv_verify_int8 and s8kv_verify_k8v3 group
- * query rows differently).
+ * workspace (16-byte aligned, s8kv_verify_workspace_size bytes) lets a call
+ * with fewer (sequence, KV head, query block) units than the GPU keeps
+ * resident split each unit's keys across workgroups and combine their
+ * partials in a second kernel on the same stream (NULL or smaller: no split,
+ * a slower call); a call whose units read more than 2^20 keys must split
+ * (that bounds the rounding of one workgroup's fp32 sums), and without the
+ * workspace it fails with S8KV_ERR_WORKSPACE.  Calls that overlap on one
+ * workspace race.  The size covers both layouts (s8kv_verify_int8 and
+ * s8kv_verify_k8v3 group query rows differently).
  */
 int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
                                    int max_context_len);
+
+/*
+ * Diagnostics (no counterpart in the reference): force the verify's key
+ * split to `splits` workgroups per unit (0 restores the per-call plan).
+ * Results are the same up to the fp32 rounding of the combined partials.
+ */
+int s8kv_verify_set_splits(int splits);
 int s8kv_verify_int8(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim, int max_queries,
                      int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s, const int8_t* k_cache,
                      const float* k_scale, const int8_t* v_cache, const float* v_scale, int64_t num_blocks,

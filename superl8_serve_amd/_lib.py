@@ -110,6 +110,7 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _f32, _c_void_p, _c_void_p, _i64, _c_void_p,
     ]),
     "s8kv_verify_workspace_size": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "s8kv_verify_set_splits": (_i32, [_i32]),
     "s8kv_verify_int8": (_i32, [
         _c_void_p, _i32, _i32, _i32, _i32, _i32,
         _i64, _i64, _i64,

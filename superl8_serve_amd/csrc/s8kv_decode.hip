@@ -303,6 +303,21 @@ __device__ __forceinline__ int raw_len_at(const DecodeArgs& a, const int* lens_l
   return b < kLensLds ? lens_lds[b] : a.context_lens[b];
 }
 
+// Checksum of the raw context lengths (a plan records the one of the lengths
+// it was made from; a planned launch recomputes it and ignores a plan whose
+// lengths were changed in place since).  Every lane returns the same value.
+__device__ __forceinline__ uint32_t lens_checksum(const DecodeArgs& a, const int* lens_lds, int lane) {
+  uint32_t s = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int b = c0 + lane;
+    const uint32_t v =
+        b < a.batch ? ((uint32_t)raw_len_at(a, lens_lds, b) + 1u) * (2u * (uint32_t)b + 1u) * 0x9E3779B1u : 0u;
+    s += (uint32_t)__builtin_amdgcn_readlane(wave_incl_scan((int)v), 63);
+  }
+  return s;
+}
+constexpr int kPlanLensWord = 15;  // header word holding lens_checksum
+
 // Sliding window: a row of L tokens attends positions [L - window, L); the
 // kernel views it from win_base, that start rounded down to a multiple of 32
 // (so its tiles stay 32-aligned in the block table), and masks the tokens of
@@ -604,12 +619,13 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // ---- the slice and its first segment: from the step's plan, or located here ----
   SliceLoc sl;
   bool pre_issued = false;  // this wave's first tile of the first segment is in flight
+  uint32_t pre_r0 = kNoTile;  // ... from this storage row
   bool planned = false;
   if (a.plan != nullptr) {
     const int32_t* hd = a.plan;
     planned = true;
 #pragma unroll
-    for (int i = 0; i < kPlanHeader; ++i) planned = planned && hd[i] == plan_header_word(a, i);
+    for (int i = 0; i < kPlanHeader; ++i) planned = planned && (i == kPlanLensWord || hd[i] == plan_header_word(a, i));
   }
   if (planned) {
     const int32_t* e = a.plan + kPlanHeader + (int64_t)j * kPlanEntry;
@@ -633,12 +649,16 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       tile_kv_at(r0 + ((uint32_t)h << bs_log2), lane);
       tile_scales_at(r0 + ((uint32_t)h << bs_log2), lane);
       pre_issued = true;
+      pre_r0 = r0 + ((uint32_t)h << bs_log2);
     }
   }
   // context lengths -> LDS (one global round trip for the whole prologue)
   for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
   __syncthreads();
   S8KV_TRACE_STAMP(kTrLens);
+  // a plan made from other lengths (the buffer rewritten in place since) is
+  // ignored; a first tile issued from it is issued again below when its row differs
+  if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != a.plan[kPlanLensWord]) planned = false;
   bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
   if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
@@ -1123,7 +1143,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       pre_issued = false;
       if (tb < t1) {
         const uint32_t r0 = tile_in_block ? tile_row0(tb) : 0u;
-        if (!pre) {
+        if (!pre || r0 != pre_r0) {  // (a tile issued from a plan that no longer applies is issued again)
           issue_kv(tb, r0);
           issue_scales(tb, r0);
         }
@@ -1367,8 +1387,12 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_plan_kernel(DecodeArgs 
   const int j = blockIdx.x * kDecWaves + wave;
   int32_t* plan = a.plan_out;
   for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
-  if (blockIdx.x == 0 && tid < kPlanHeader) plan[tid] = plan_header_word(a, tid);
+  if (blockIdx.x == 0 && tid < kPlanHeader && tid != kPlanLensWord) plan[tid] = plan_header_word(a, tid);
   __syncthreads();
+  if (blockIdx.x == 0 && wave == 0) {
+    const uint32_t cs = lens_checksum(a, lens_lds, lane);
+    if (lane == 0) plan[kPlanLensWord] = (int32_t)cs;
+  }
   if (j >= a.wg_per_head) return;
   SliceLoc s;
   if (!locate_slice<WIN>(a, lens_lds, j, lane, s)) {  // no segment: the launch's workgroup j returns at once

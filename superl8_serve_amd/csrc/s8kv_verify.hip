@@ -25,6 +25,7 @@
 //         (hi: the fp32 weight cut to fp16 precision, lo: the exact rest).
 // Rows past a sequence's query count are written as zeros.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -928,20 +929,19 @@ struct FreshDrafts {
 // each (sequence, KV head, query block) is split until about that many
 // exist, down to kMinSplitKeys keys per split; and one workgroup never
 // accumulates more than kMaxSplitKeys keys, which bounds the rounding of its
-// fp32 sums.  S8KV_VERIFY_SPLITS overrides the count (tests).
+// fp32 sums.  s8kv_verify_set_splits overrides the count (diagnostics).
 constexpr int kMinSplitKeys = 1024;
 constexpr int kMaxSplitKeys = 1 << 20;
 constexpr int kMaxSplits = 1024;
+static std::atomic<int> g_verify_splits{0};  // 0: planned per call
 static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3) {
   const int64_t natural = (int64_t)batch * num_kv_heads * n_qblocks;
   const int64_t resident = (int64_t)verify::wg_per_cu(k8v3) * device_cus();
   int64_t s = natural < resident ? (resident + natural - 1) / natural : 1;
   s = std::min<int64_t>(s, std::max(1, keys / kMinSplitKeys));
   s = std::max<int64_t>(s, ((int64_t)keys + kMaxSplitKeys - 1) / kMaxSplitKeys);
-  if (const char* env = getenv("S8KV_VERIFY_SPLITS")) {
-    const int v = atoi(env);
-    if (v > 0) s = v;
-  }
+  const int forced = g_verify_splits.load();
+  if (forced > 0) s = forced;
   return (int)std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
 }
 static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits, bool k8v3) {
@@ -969,17 +969,33 @@ extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int nu
 // The split for this call (keys: the most any block reads -- a window layer's
 // window and drafts), used when the caller's workspace holds its partials;
 // never more than s8kv_verify_workspace_size plans for, which counts
-// max_context_len keys.
-static void verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, void* workspace,
-                                 int64_t workspace_bytes) {
+// max_context_len keys.  A split made only to fill the GPU is dropped when
+// the workspace cannot hold it (the call is then slower, not different in
+// kind); a block reading more than kMaxSplitKeys keys must split, so then a
+// missing or short workspace is an error.
+static int verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, void* workspace,
+                                int64_t workspace_bytes) {
   const int keys = a.window > 0 ? (int)std::min<int64_t>(a.max_context_len, (int64_t)a.window + a.max_queries)
                                 : a.max_context_len;
   const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3);
   const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3);
-  if (s > 1 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0) {
+  const bool fits = workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0;
+  if (s > 1 && fits) {
     a.splits = s;
     a.part = (float*)workspace;
   }
+  S8KV_REQUIRE(fits || keys <= kMaxSplitKeys, S8KV_ERR_WORKSPACE,
+               "verify: %d keys per block exceed %d without a split: a 16-byte aligned workspace of %lld bytes "
+               "(s8kv_verify_workspace_size) is needed, %lld given", keys, kMaxSplitKeys, (long long)need,
+               (long long)(workspace ? workspace_bytes : 0));
+  return S8KV_OK;
+}
+
+extern "C" int s8kv_verify_set_splits(int splits) {
+  S8KV_REQUIRE(splits >= 0 && splits <= kMaxSplits, S8KV_ERR_INVALID, "verify_set_splits: %d not in [0, %d]", splits,
+               kMaxSplits);
+  g_verify_splits.store(splits);
+  return S8KV_OK;
 }
 
 // Checks and arguments shared by both layouts (everything but V).
@@ -1052,7 +1068,7 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  verify_use_workspace(a, head_dim, false, workspace, workspace_bytes);
+  if (const int rc = verify_use_workspace(a, head_dim, false, workspace, workspace_bytes)) return rc;
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -1144,7 +1160,7 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
                               prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  verify_use_workspace(a, head_dim, true, workspace, workspace_bytes);
+  if (const int rc = verify_use_workspace(a, head_dim, true, workspace, workspace_bytes)) return rc;
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&

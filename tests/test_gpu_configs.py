@@ -14,8 +14,10 @@ The inputs are the benchmark's own generators (``bench.py``).  Cache bytes
 are compared bit for bit: the appended tokens in full, the prefix of a
 seeded subset of rows (the oracle's append is ~0.2 ms per token on the
 host).  Attention outputs are compared with the float64 oracle over the
-dequantized cache: every row of the decode step, a seeded subset of rows for
-K8V3, chunked prefill and tree verify."""
+dequantized cache: every row of every workload.  Each comparison prints the
+plain max-abs error beside the scaled one the tolerance is stated in
+(``max |out - ref| / max(1, |ref|)``: an fp16 output holds ~11 significant
+bits, so above |ref| = 1 the bound is relative)."""
 
 from __future__ import annotations
 
@@ -72,6 +74,16 @@ def _check_k8v3_rows(cache, k, v, slots, codebook, what):
         assert _same(g[rows], w[rows]), f"{what}: {name} differ from the oracle"
 
 
+def _assert_close(got, ref, what):
+    """Tolerance against the float64 oracle, reporting the plain max-abs
+    error as well as the scaled one the bound applies to."""
+    mx, rel = O.attention_errors(got, ref)
+    plain = float(np.max(np.abs(np.asarray(got, np.float64) - ref))) if ref.size else 0.0
+    print(f"{what}: scaled max err {mx:.3e} (plain max-abs {plain:.3e}, max |ref| {np.abs(ref).max():.2f}), "
+          f"rel rms {rel:.3e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"{what}: max err {mx:.3e}, rel rms {rel:.3e}"
+
+
 def _unchanged_except(before, after, rows, what):
     """Every storage row but `rows` is byte-identical."""
     for b, a, name in zip(before, after, ("k_cache", "k_scale", "v_cache", "v_scale")):
@@ -116,14 +128,13 @@ def test_c2_int8_decode_step_batch64():
     _unchanged_except(pre, after, _rows_of(w["new_slots"]), "C2")
     print("C2: oracle attention over all 64 rows", flush=True)
     ref = O.paged_decode(_np(w["q"][0])[:, :, 0, :], O.LayerCache(*after), bt, lens, SCALE)
-    mx, rel = O.attention_errors(_np(got.float())[:, :, 0, :], ref)
-    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"C2: max err {mx:.3e}, rel rms {rel:.3e}"
+    _assert_close(_np(got.float())[:, :, 0, :], ref, "C2 (64 rows)")
 
 
 def test_c3_k8v3_decode_step_batch32_long_context():
     """K8V3 step, one layer: every appended token bit-exact, the first 2048
     prefix tokens of 2 seeded rows bit-exact, one launch == append kernel +
-    K8V3 decode for all 32 rows, 4 seeded rows against the oracle."""
+    K8V3 decode for all 32 rows, and all 32 rows against the oracle."""
     rng = np.random.default_rng(31)
     keep = tuple(int(x) for x in rng.choice(bench.K8V3_BATCH, 2, replace=False))
     print(f"C3: building the batch-32 K8V3 workload (1 layer), prefix rows {keep}", flush=True)
@@ -152,12 +163,10 @@ def test_c3_k8v3_decode_step_batch32_long_context():
         assert _same(a, _np(s)), f"C3: {name} differs from the append kernel's"
     _check_k8v3_rows(after, _np(w["k_new"][0]), _np(w["v_new"][0]), w["new_slots"], cb, "C3 appended tokens")
     _unchanged_except(pre, after, _rows_of(w["new_slots"]), "C3")
-    rows = np.sort(rng.choice(bench.K8V3_BATCH, 4, replace=False))
-    print(f"C3: oracle attention over rows {rows.tolist()}", flush=True)
+    print("C3: oracle attention over all 32 rows", flush=True)
     layer = O.LayerCache(after[0], after[1], v_packed=after[2], v_norm=after[3], v_codebook=cb)
-    ref = O.paged_decode(_np(w["q"][0])[rows, :, 0, :], layer, bt[rows], lens[rows], SCALE)
-    mx, rel = O.attention_errors(_np(got.float())[rows, :, 0, :], ref)
-    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"C3: max err {mx:.3e}, rel rms {rel:.3e}"
+    ref = O.paged_decode(_np(w["q"][0])[:, :, 0, :], layer, bt, lens, SCALE)
+    _assert_close(_np(got.float())[:, :, 0, :], ref, "C3 (32 rows)")
 
 
 def _fp16(gen, shape, ch):
@@ -170,7 +179,7 @@ def test_c4_chunked_prefill_prefix_cow_and_compaction():
     """16 sequences share a 4096-token prefix through the prefix cache;
     each copies its last shared block on write, appends a 512-token chunk and
     attends causally over 4608 keys; then a seeded 20 % of the blocks is freed
-    and the pool compacted.  Checks: chunk bytes, the copy, 3 seeded
+    and the pool compacted.  Checks: chunk bytes, the copy, all 16
     sequences' attention against the oracle, every read_dense and every
     sequence's attention unchanged by the compaction, the live blocks packed
     at the bottom of the pool."""
@@ -221,11 +230,10 @@ def test_c4_chunked_prefill_prefix_cow_and_compaction():
     out = cache.verify_attn(0, q, slots, [prefix_len] * nseq, scale=SCALE)
     torch.cuda.synchronize()
     bt = _np(cache.block_table(slots))
-    sel = np.sort(rng.choice(nseq, 3, replace=False))
-    print(f"C4: oracle attention of sequences {sel.tolist()}", flush=True)
-    ref = O.paged_verify(_np(q)[sel], O.LayerCache(*pool), bt[sel], np.full(len(sel), prefix_len), SCALE)
-    mx, rel = O.attention_errors(_np(out.float())[sel], ref)
-    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"C4: max err {mx:.3e}, rel rms {rel:.3e}"
+    rng.choice(nseq, 3, replace=False)  # (keeps the seeded draws below unchanged)
+    print("C4: oracle attention of all 16 sequences", flush=True)
+    ref = O.paged_verify(_np(q), O.LayerCache(*pool), bt, np.full(nseq, prefix_len), SCALE)
+    _assert_close(_np(out.float()), ref, "C4 (16 sequences)")
 
     # free a seeded 20 % of the allocated blocks (whole sequences: 3 private
     # blocks each), then compact the pool
@@ -268,7 +276,7 @@ def test_c4_chunked_prefill_prefix_cow_and_compaction():
 def test_c5_tree_verify_batch32(k8v3):
     """32 sequences with 8192-token prefixes append random draft trees of
     16-64 nodes (branching 1-4) and attend prefix + ancestors: appended bytes
-    bit-exact, 6 seeded rows against the oracle."""
+    bit-exact, all 32 rows against the oracle."""
     print(f"C5: building the tree-verify workload ({'k8v3' if k8v3 else 'int8'}, 1 layer)", flush=True)
     w, info = bench.verify_workload("tree", DEV, k8v3=k8v3, layers=1)
     before = [_np(w[k][0]) for k in ("kc", "ks", "vc", "vs")]
@@ -288,9 +296,8 @@ def test_c5_tree_verify_batch32(k8v3):
     else:
         _check_int8_rows(after, kn, vn, w["new_slots"], "C5 drafts")
     _unchanged_except(before, after, _rows_of(w["new_slots"]), "C5")
-    rng = np.random.default_rng(41)
-    rows = np.sort(rng.choice(info["batch"], 6, replace=False))
-    print(f"C5: oracle attention over rows {rows.tolist()}", flush=True)
+    rows = np.arange(info["batch"])
+    print("C5: oracle attention over all 32 rows", flush=True)
     if k8v3:
         layer = O.LayerCache(after[0], after[1], v_packed=after[2], v_norm=after[3], v_codebook=_np(w["cb"]))
     else:
@@ -300,5 +307,4 @@ def test_c5_tree_verify_batch32(k8v3):
     got = _np(out.float())[rows]
     for i, r in enumerate(rows):  # queries past a row's node count are zeros
         assert not got[i, :, w["nq_np"][r]:].any()
-    mx, rel = O.attention_errors(got, ref)
-    assert mx <= O.MAX_ABS_TOL and rel <= O.REL_RMS_TOL, f"C5: max err {mx:.3e}, rel rms {rel:.3e}"
+    _assert_close(got, ref, f"C5 {'k8v3' if k8v3 else 'int8'} (32 rows)")

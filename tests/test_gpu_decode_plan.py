@@ -154,6 +154,23 @@ def test_plan_for_other_buffers_or_geometry_is_ignored():
     _same(step.run(junk), ref, "garbage plan")
 
 
+def test_plan_of_lengths_rewritten_in_place_is_ignored():
+    """A plan records a checksum of the lengths it was made from.  After the
+    lengths buffer is rewritten in place (same buffer, same geometry, as a
+    serving loop's static buffers are), a launch given the old plan locates
+    its work itself, including the first tiles the plan named."""
+    rng = np.random.default_rng(21)
+    case = make_case(4646, 12, 32, 8, 128, 256, rng.integers(2000, 4000, size=12).tolist())
+    step = _Step(case, "int8")
+    stale = step.plan()
+    new_lens = (case.lens // 3 + rng.integers(1, 200, size=12)).astype(np.int32)
+    step.cl.copy_(_t(new_lens))
+    fresh = step.plan()
+    assert not torch.equal(fresh, stale), "the rewrite must change the plan"
+    _same(step.run(stale), step.run(None), "plan of lengths rewritten in place")
+    _same(step.run(fresh), step.run(None), "plan of the new lengths")
+
+
 def test_plan_entries_tile_the_stream():
     """The entries cut the token stream into consecutive slices, and each
     wave's first-tile row is the block-table row of its first tile."""

@@ -2,7 +2,7 @@
 C ABI: each (sequence, KV head, query block) split across workgroups whose
 partials a second kernel combines.  The split is taken when a call has fewer
 units than the GPU keeps resident (batch-1 speculative decoding) or more than
-2^20 keys per unit; S8KV_VERIFY_SPLITS forces a count here, including counts
+2^20 keys per unit; s8kv_verify_set_splits forces a count here, including counts
 that leave splits without keys."""
 
 from __future__ import annotations
@@ -17,6 +17,18 @@ from tests.kvcase import make_case
 from tests.kvgpu import CODEBOOK, alloc, append, assert_close, layer, t, to_np, verify
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def force_splits():
+    """Set the verify's split count (0: planned per call); reset on exit."""
+    lib = _lib.load()
+
+    def set_(n):
+        _lib.check(lib.s8kv_verify_set_splits(int(n)), "s8kv_verify_set_splits")
+
+    yield set_
+    set_(0)
 
 
 def _random_tree(rng, n):
@@ -51,41 +63,41 @@ def _run(kind, case, cache, qv, prefix, tree_mask=None, window=None, query_lens=
 @pytest.mark.parametrize("kind,d,splits", [
     ("int8", 128, 5), ("int8", 64, 3), ("int8", 256, 9), ("k8v3", 128, 7), ("k8v3", 256, 4),
 ])
-def test_forced_split_matches_oracle_and_unsplit(kind, d, splits, monkeypatch):
+def test_forced_split_matches_oracle_and_unsplit(kind, d, splits, force_splits):
     case, cache, host, qv, prefix = _case(900 + d + splits, kind, 8, 2, d, 16, [3000, 517, 40], 6)
     ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale)
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "1")
+    force_splits("1")
     whole = _run(kind, case, cache, qv, prefix)
     assert_close(whole, ref, f"{kind} D={d} unsplit")
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    force_splits(str(splits))
     split = _run(kind, case, cache, qv, prefix)
     assert_close(split, ref, f"{kind} D={d} {splits} splits")
     assert_close(split, whole.astype(np.float64), f"{kind} D={d} {splits} splits vs unsplit")
 
 
 @pytest.mark.parametrize("splits", [2, 31, 200])
-def test_split_tree_and_empty_splits(splits, monkeypatch):
+def test_split_tree_and_empty_splits(splits, force_splits):
     """Tree masks across splits; 200 splits of a few hundred keys leave most
     splits of the short rows without keys."""
     nq = 12
     case, cache, host, qv, prefix = _case(950 + splits, "int8", 16, 4, 128, 32, [4096, 33, 0, 700], nq)
     rng = np.random.default_rng(951)
     tm = np.stack([_random_tree(rng, nq) for _ in range(len(prefix))])
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    force_splits(str(splits))
     got = _run("int8", case, cache, qv, prefix, tree_mask=tm)
     ref = O.paged_verify(qv, layer("int8", host), case.block_table, prefix, case.scale, tree_mask=tm)
     assert_close(got, ref, f"tree verify, {splits} splits")
 
 
 @pytest.mark.parametrize("kind,splits", [("int8", 4), ("int8", 1), ("k8v3", 7)])
-def test_split_query_lens(kind, splits, monkeypatch):
+def test_split_query_lens(kind, splits, force_splits):
     """Rows past a sequence's query count are zeros also when they share a
     query block with live rows (G 4: positions 0-15 per 64-row block) and
     the block's keys are split; the live rows match the oracle."""
     nq = 24
     ql = np.array([5, 24, 0, 17])
     case, cache, host, qv, prefix = _case(990 + splits, kind, 16, 4, 128, 32, [3000, 2100, 1500, 2600], nq)
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", str(splits))
+    force_splits(str(splits))
     got = _run(kind, case, cache, qv, prefix, query_lens=ql)
     ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, query_lens=ql)
     for b, n in enumerate(ql):
@@ -94,9 +106,9 @@ def test_split_query_lens(kind, splits, monkeypatch):
 
 
 @pytest.mark.parametrize("kind", ["int8", "k8v3"])
-def test_split_window_verify(kind, monkeypatch):
+def test_split_window_verify(kind, force_splits):
     case, cache, host, qv, prefix = _case(960, kind, 8, 2, 128, 16, [5000, 300], 5)
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "6")
+    force_splits("6")
     got = _run(kind, case, cache, qv, prefix, window=1024)
     ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, window=1024)
     assert_close(got, ref, f"{kind} window verify, 6 splits")
@@ -118,10 +130,10 @@ def test_batch_one_long_context_plans_a_split(kind):
     assert_close(got, ref, f"{kind} batch-1 tree verify (planned split)")
 
 
-def test_split_graph_replays(monkeypatch):
+def test_split_graph_replays(force_splits):
     """Both launches of a split verify captured in a HIP graph: every replay
     returns the eager result."""
-    monkeypatch.setenv("S8KV_VERIFY_SPLITS", "8")
+    force_splits("8")
     case, cache, host, qv, prefix = _case(980, "int8", 8, 2, 128, 16, [2000, 900], 4)
     eager = _run("int8", case, cache, qv, prefix)
     q, bt, pl = t(qv), t(case.block_table), t(prefix.astype(np.int32))
