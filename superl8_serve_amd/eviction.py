@@ -64,7 +64,13 @@ class KVEviction:
         most, averaged over q heads (kv_cache.py:124-166): ``q_last``
         ``[num_heads, D]`` or ``[1, num_heads, 1, D]``, ``k_full``
         ``[Hkv, S, D]`` or ``[1, Hkv, S, D]`` on the GPU.  Every position when
-        ``S <= budget``."""
+        ``S <= budget``.
+
+        CHOICE: the logits, softmax and mean are computed in fp32 whatever
+        the input dtype; the reference computes them in the input dtype (fp16
+        in the engine).  For fp16 inputs, keys whose scores tie within fp16
+        rounding may therefore rank differently; the selections recorded from
+        the reference (fp32 inputs) are reproduced exactly."""
         seq_len = k_full.shape[-2]
         if seq_len <= budget:
             return list(range(seq_len))
