@@ -846,10 +846,21 @@ def run_append(steps: int, warmup: int, k8v3: bool = False) -> None:
     en.record()
     torch.cuda.synchronize()
     sec = st.elapsed_time(en) * 1e-3 / steps
+    # the same call timed alone: idle GPU before each call, events on either side
+    alone = []
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        st.record()
+        call()
+        en.record()
+        torch.cuda.synchronize()
+        alone.append(st.elapsed_time(en) * 1e-3)
+    sec_alone = float(np.median(alone))
     moved = T * HKV * (2 * D * 2 + out_bytes)  # fp16 K, V in; the cache bytes out
     fmt = "k8v3: int8 K + 3-bit V" if k8v3 else "int8 + scales"
     print(json.dumps({"metric": f"prefill append GB/s (fp16 K/V in, {fmt} out), 131,072 tokens x 8 KV heads",
                       "value": round(moved / sec / 1e9, 1), "unit": "GB/s", "us_per_call": round(sec * 1e6, 1),
+                      "us_per_call_alone_median": round(sec_alone * 1e6, 1),
                       "bytes_per_call": moved, "pct_of_hbm_peak": round(100 * moved / sec / 1e9 / HBM_PEAK_GBPS, 1)}))
 
 

@@ -120,24 +120,98 @@ __global__ __launch_bounds__(64 * kAppendWaves) void append_kernel(AppendArgs a)
 }
 
 // int8 append with several rows per wave: a row's D values sit on LPR = D/16
-// consecutive lanes, 16 consecutive values per lane, so each lane moves a row
-// part with two 16-byte loads and one 16-byte store per tensor and the
-// per-row work (slot lookup, addresses, reductions) is shared by 64/LPR rows
-// per instruction.  The K rotation runs the FWHT stages h = 1, 2, 4, 8
-// in-lane and h = 16 .. D/2 as lane ^ (h/16) butterflies: the stage order and
-// arithmetic of fwht_row, so the bytes equal the one-row-per-wave kernel's.
-// Needs 16-byte aligned K and V rows.
+// lanes, 16 consecutive values per lane, so each lane moves a row part with
+// two 16-byte loads and one 16-byte store per tensor and the per-row work
+// (slot lookup, addresses, reductions) is shared by 64/LPR rows per
+// instruction.  The K rotation runs the FWHT stages h = 1, 2, 4, 8 in-lane
+// and h = 16 .. D/2 across the row's lanes: the stage order and arithmetic of
+// fwht_row, so the bytes equal the one-row-per-wave kernel's.  Needs 16-byte
+// aligned K and V rows.
+//
+// Lane placement: part li (values 16 li .. 16 li + 15) of a row.  At head_dim
+// 128 li sits on lane bits (b3 b1 b0) and lane bits (b5 b4 b2) number the row,
+// so the partners of the three cross-lane stages (li ^ 1, ^ 2, ^ 4) are lanes
+// ^ 1, ^ 2, ^ 8, all DPP sources.  Other head dims: li = lane % LPR.
+template <int D>
+struct RowsLayout {
+  static constexpr int LPR = D / 16;   // lanes per row
+  static constexpr int RPW = 64 / LPR;  // rows per wave
+  static constexpr int LANE4 = D == 128 ? 8 : 4;  // lane xor of part xor 4
+  static __device__ __forceinline__ int part(int lane) {
+    return D == 128 ? (lane & 3) | ((lane >> 1) & 4) : lane % LPR;
+  }
+  static __device__ __forceinline__ int row(int lane) {
+    return D == 128 ? ((lane >> 2) & 1) | ((lane >> 3) & 6) : lane / LPR;
+  }
+};
+
+// max over the row's lanes (part xor 1, 2, 4, 8)
+template <int D>
+__device__ __forceinline__ float rows_max(float v) {
+  constexpr int LPR = D / 16;
+  if constexpr (LPR > 1) v = fmaxf(v, xor_partner<1>(v));
+  if constexpr (LPR > 2) v = fmaxf(v, xor_partner<2>(v));
+  if constexpr (LPR > 4) v = fmaxf(v, xor_partner<RowsLayout<D>::LANE4>(v));
+  if constexpr (LPR > 8) v = fmaxf(v, xor_partner<8>(v));
+  return v;
+}
+
+#define S8KV_FMAC_DPP16(CTRL)                                                         \
+  "s_nop 1\n"                                                                         \
+  "v_fmac_f32_dpp %0, %0, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %1, %1, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %2, %2, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %3, %3, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %4, %4, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %5, %5, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %6, %6, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %7, %7, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %8, %8, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %9, %9, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                  \
+  "v_fmac_f32_dpp %10, %10, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "v_fmac_f32_dpp %11, %11, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "v_fmac_f32_dpp %12, %12, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "v_fmac_f32_dpp %13, %13, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "v_fmac_f32_dpp %14, %14, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "v_fmac_f32_dpp %15, %15, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"                \
+  "s_nop 1"
+
+// One cross-lane FWHT stage over the lane's 16 values, sign-tracked: z += t *
+// (z of lane ^ M), t = -1 on the lanes whose part has the stage's bit set,
+// else +1.  The lanes hold sigma * (true values), sigma = (-1)^(number of
+// earlier stage bits set in the part); partners share sigma, so this is the
+// butterfly on the true values (low lane a + b, high lane a - b) with the
+// high lanes' sign flipped: RN(b - a) = -RN(a - b), and signed zeros aside
+// (a zero quantizes to code 0 either way) the values are the untracked
+// form's.  M = 1, 2, 8: one v_fmac_f32 with a DPP source per value (the s_nop
+// pairs cover the DPP read-after-VALU-write hazard at the block's edges);
+// M = 4 reads the partner through the LDS swizzle.
+template <int M>
+__device__ __forceinline__ void fwht_stage_tracked(float (&z)[16], float t) {
+  if constexpr (M == 4) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = __builtin_fmaf(xor_partner<4>(z[i]), t, z[i]);
+  } else {
+    static_assert(M == 1 || M == 2 || M == 8, "DPP partners: lane ^ 1, ^ 2, ^ 8");
+#define S8KV_FMAC_OPERANDS                                                                                       \
+  : "+v"(z[0]), "+v"(z[1]), "+v"(z[2]), "+v"(z[3]), "+v"(z[4]), "+v"(z[5]), "+v"(z[6]), "+v"(z[7]), "+v"(z[8]), \
+    "+v"(z[9]), "+v"(z[10]), "+v"(z[11]), "+v"(z[12]), "+v"(z[13]), "+v"(z[14]), "+v"(z[15])                    \
+  : "v"(t)
+    if constexpr (M == 1) asm(S8KV_FMAC_DPP16("quad_perm:[1,0,3,2]") S8KV_FMAC_OPERANDS);
+    else if constexpr (M == 2) asm(S8KV_FMAC_DPP16("quad_perm:[2,3,0,1]") S8KV_FMAC_OPERANDS);
+    else asm(S8KV_FMAC_DPP16("row_ror:8") S8KV_FMAC_OPERANDS);
+#undef S8KV_FMAC_OPERANDS
+  }
+}
+#undef S8KV_FMAC_DPP16
+
 template <int D, class QOut, class SOut>
 __device__ __forceinline__ void rows_rtn_store(const float (&y)[16], bool live, int li, const QOut& qout,
                                                const SOut& sout) {
-  constexpr int LPR = D / 16;
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(y[i]));
-  if constexpr (LPR > 1) amax = fmaxf(amax, xor_partner<1>(amax));
-  if constexpr (LPR > 2) amax = fmaxf(amax, xor_partner<2>(amax));
-  if constexpr (LPR > 4) amax = fmaxf(amax, xor_partner<4>(amax));
-  if constexpr (LPR > 8) amax = fmaxf(amax, xor_partner<8>(amax));
+  amax = rows_max<D>(amax);
   const float scale = amax / 127.0f;
   const float rscale = rtn_rscale(scale);
   uint32_t w[4];
@@ -161,19 +235,48 @@ __device__ __forceinline__ uint32_t shift_in_bit(uint32_t w, bool b) {
   return r;
 }
 
+// Ordered key of an fp32 bit pattern: key(x) < key(y) iff x < y, with -0
+// just below +0; the map is its own inverse.
+__device__ __forceinline__ int f32_key(int bits) { return bits ^ ((bits >> 31) & 0x7FFFFFFF); }
+
+// Threshold T of the codebook neighbours a = c_{j-1} < b = c_j: the least
+// fp32 u for which entry j is strictly nearer than entry j - 1 (fabsf(u - b) <
+// fabsf(u - a), lloyd3_search's test).  On [a, b] the two distances are
+// RN(b - u), non-increasing in u, and RN(u - a), non-decreasing, so the test
+// is monotone there -- false at a, true at b -- and bisection over the keys
+// finds T.  Below a the test is false (RN(b - u) >= RN(a - u)) and above b,
+// for a codebook accepted by lloyd3_search_ok and |u| <= 1, true; so for
+// every u the encoder sees, the test equals u >= T.  (T is never +0: -0 gives
+// the same distances and precedes it.)
+__device__ __forceinline__ float lloyd3_threshold(float a, float b) {
+  int lo = f32_key(__builtin_bit_cast(int, a)), hi = f32_key(__builtin_bit_cast(int, b));
+  for (int it = 0; it < 32; ++it) {
+    const uint32_t d = (uint32_t)hi - (uint32_t)lo;
+    if (d <= 1u) break;
+    const int mid = (int)((uint32_t)lo + (d >> 1));
+    const float u = __builtin_bit_cast(float, f32_key(mid));
+    if (fabsf(u - b) < fabsf(u - a)) hi = mid;
+    else lo = mid;
+  }
+  return __builtin_bit_cast(float, f32_key(hi));
+}
+
 // 3-bit Lloyd-Max V of the lane's 16 values (head_dim 128 or 256, blocks of
 // 128 = 8 lanes): the block's L2 norm adds the fp32 squares in the order of
 // lloydmax3_encode_row (a pairwise tree over neighbours: levels h = 1 .. 8
-// in-lane, h = 16, 32, 64 across lanes ^ 1, ^ 2, ^ 4), correctly rounded sqrt; u = v / norm
-// (0 for a zero norm) as the Markstein quotient from the block's reciprocal,
-// which equals the IEEE quotient for an fp16 v and any fp32 norm (checked for
-// every pair of significands); code = first index minimising |u - c_j|, by
-// lloyd3_search when the codebook allows it, else by the sequential scan.
-// Lanes 2g and 2g + 1 hold elements 32g .. 32g + 31: each builds 16 bits of
-// the three bit-plane words 3g + b, and the even lane stores them.
+// in-lane, h = 16, 32, 64 across the parts ^ 1, ^ 2, ^ 4), correctly rounded
+// sqrt; u = v / norm (0 for a zero norm) as the Markstein quotient from the
+// block's reciprocal, which equals the IEEE quotient for an fp16 v and any
+// fp32 norm (checked for every pair of significands); code = first index
+// minimising |u - c_j|: with `search` (a codebook accepted by
+// lloyd3_search_ok) lloyd3_search's three tests as compares against the
+// thresholds thr[j] = T_j, else the sequential scan.  Parts 2g and 2g + 1
+// (lanes l and l ^ 1) hold elements 32g .. 32g + 31: each builds 16 bits of
+// the three bit-plane words 3g + b, and the even part stores them.
 template <int D, class VOut, class NOut>
-__device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool live, int li, const float (&cb)[8],
-                                                     const VOut& vout, const NOut& nout) {
+__device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool live, int li, bool search,
+                                                     const float (&cb)[8], const float (&thr)[8], const VOut& vout,
+                                                     const NOut& nout) {
   float s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) s[i] = x[i] * x[i];
@@ -185,7 +288,7 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
   float t = s[0];  // the lane's 16 elements; partners hold the neighbouring groups
   t = t + xor_partner<1>(t);
   t = t + xor_partner<2>(t);
-  t = t + xor_partner<4>(t);
+  t = t + xor_partner<RowsLayout<D>::LANE4>(t);
   const float nrm = __builtin_sqrtf(t);
   const float rn = rtn_rscale(nrm);  // 1 / norm, 0 for a zero norm (then u = 0)
   float u[16];
@@ -197,11 +300,13 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
   }
   // bit i of pw[b] = bit b of element i's code (elements shifted in from 15 down)
   uint32_t pw[3] = {0u, 0u, 0u};
-  if (lloyd3_search_ok(cb)) {
+  if (search) {
 #pragma unroll
     for (int i = 15; i >= 0; --i) {
-      bool b2, b1, b0;
-      lloyd3_search(u[i], cb, b2, b1, b0);
+      const bool b2 = u[i] >= thr[4];
+      const bool b1 = u[i] >= (b2 ? thr[6] : thr[2]);
+      const float t_hi = b2 ? thr[7] : thr[3], t_lo = b2 ? thr[5] : thr[1];
+      const bool b0 = u[i] >= (b1 ? t_hi : t_lo);
       pw[0] = shift_in_bit(pw[0], b0);
       pw[1] = shift_in_bit(pw[1], b1);
       pw[2] = shift_in_bit(pw[2], b2);
@@ -236,91 +341,110 @@ __device__ __forceinline__ void rows_lloydmax3_store(const float (&x)[16], bool 
   if (live && (li & 7) == 0) nout.st32((uint32_t)(li / 8) * 4u, __builtin_bit_cast(uint32_t, nrm));
 }
 
+// Row groups (kAppendWaves waves of RPW rows) per workgroup: the K8V3 kernel
+// derives the codebook's thresholds once per workgroup and reuses them.
+template <bool K8V3>
+constexpr int kRowsIters = K8V3 ? 4 : 1;
+
 template <int D, bool K8V3, bool BIG>
 __global__ __launch_bounds__(64 * kAppendWaves) void append_rows_kernel(AppendArgs a) {
-  constexpr int LPR = D / 16;  // lanes per row
-  constexpr int RPW = 64 / LPR;  // rows per wave
+  using L = RowsLayout<D>;
+  constexpr int LPR = L::LPR;
+  constexpr int RPW = L::RPW;
   const int lane = threadIdx.x & 63;
-  const int li = lane % LPR;
-  const int64_t row_id = ((int64_t)blockIdx.x * kAppendWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
-  bool live = row_id < a.num_tokens * a.num_kv_heads;
-  int64_t t = 0;
-  int h = 0;
-  uint32_t row = 0;
-  if (live) {
-    t = row_id / a.num_kv_heads;
-    h = (int)(row_id - t * a.num_kv_heads);
-    const int32_t slot = a.slot_mapping[t];
-    const uint32_t blk = (uint32_t)slot >> a.block_size_log2;
-    live = slot >= 0 && (int64_t)blk < a.num_blocks;  // negative slots and slots outside the pool are skipped
-    row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) +
-          ((uint32_t)slot & ((1u << a.block_size_log2) - 1u));
-  }
-  // both row parts' loads in flight together
-  float x[16], y[16];
-  {
-    half8_t k0{}, k1{}, v0{}, v1{};
-    if (live) {
-      const _Float16* kp = a.k + t * a.k_stride_t + h * a.k_stride_h + li * 16;
-      const _Float16* vp = a.v + t * a.v_stride_t + h * a.v_stride_h + li * 16;
-      k0 = *reinterpret_cast<const half8_t*>(kp);
-      k1 = *reinterpret_cast<const half8_t*>(kp + 8);
-      v0 = *reinterpret_cast<const half8_t*>(vp);
-      v1 = *reinterpret_cast<const half8_t*>(vp + 8);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      x[i] = (float)k0[i];
-      x[8 + i] = (float)k1[i];
-      y[i] = (float)v0[i];
-      y[8 + i] = (float)v1[i];
-    }
-  }
+  const int li = L::part(lane);
+  // FWHT sign tracking: the stage multipliers of the lane, and the lane's
+  // final sign (-1)^popcount(li) folded into the 1/sqrt(D) multiply
+  const float t1 = (li & 1) ? -1.0f : 1.0f, t2 = (li & 2) ? -1.0f : 1.0f;
+  const float t4 = (li & 4) ? -1.0f : 1.0f, t8 = (li & 8) ? -1.0f : 1.0f;
+  const float srn = (__builtin_popcount(li) & 1) ? -a.rot_norm : a.rot_norm;
 
-  // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
-#pragma unroll
-  for (int hs = 1; hs < 16; hs <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if ((i & hs) == 0) {
-        const float p0 = x[i], p1 = x[i + hs];
-        x[i] = p0 + p1;
-        x[i + hs] = p0 - p1;
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (LPR > 1) x[i] = butterfly_xor<1>(x[i], lane);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (LPR > 2) x[i] = butterfly_xor<2>(x[i], lane);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (LPR > 4) x[i] = butterfly_xor<4>(x[i], lane);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (LPR > 8) x[i] = butterfly_xor<8>(x[i], lane);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) x[i] = (float)(_Float16)materialize(x[i] * a.rot_norm);
-  rows_rtn_store<D>(x, live, li, row_out<BIG>(a.k_cache, a.kc_bytes, (uint64_t)row * D),
-                    row_out<BIG>(a.k_scale, a.ks_bytes, (uint64_t)row * 4u));
-
-  // ---- V: RTN, or 3-bit Lloyd-Max ----
-  if constexpr (!K8V3) {
-    rows_rtn_store<D>(y, live, li, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * D),
-                      row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * 4u));
-  } else {
-    static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
-    float cb[8];
+  float cb[8], thr[8];
+  bool search = false;
+  if constexpr (K8V3) {
+    __shared__ float thr_lds[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) cb[i] = a.v_codebook[i];
-    rows_lloydmax3_store<D>(y, live, li, cb, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * (D / 32 * 3 * 4)),
-                            row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * (D / 128 * 4)));
+    search = lloyd3_search_ok(cb);  // uniform over the workgroup
+    if (search) {
+      if (threadIdx.x < 7) thr_lds[threadIdx.x + 1] = lloyd3_threshold(a.v_codebook[threadIdx.x], a.v_codebook[threadIdx.x + 1]);
+      __syncthreads();
+#pragma unroll
+      for (int j = 1; j < 8; ++j) thr[j] = thr_lds[j];
+    }
+    thr[0] = 0.0f;
+  }
+
+  const int64_t total = a.num_tokens * a.num_kv_heads;
+#pragma unroll 1
+  for (int it = 0; it < kRowsIters<K8V3>; ++it) {
+    const int64_t row_id =
+        (((int64_t)blockIdx.x * kRowsIters<K8V3> + it) * kAppendWaves + (threadIdx.x >> 6)) * RPW + L::row(lane);
+    bool live = row_id < total;
+    int64_t t = 0;
+    int h = 0;
+    uint32_t row = 0;
+    if (live) {
+      t = row_id / a.num_kv_heads;
+      h = (int)(row_id - t * a.num_kv_heads);
+      const int32_t slot = a.slot_mapping[t];
+      const uint32_t blk = (uint32_t)slot >> a.block_size_log2;
+      live = slot >= 0 && (int64_t)blk < a.num_blocks;  // negative slots and slots outside the pool are skipped
+      row = ((blk * (uint32_t)a.num_kv_heads + (uint32_t)h) << a.block_size_log2) +
+            ((uint32_t)slot & ((1u << a.block_size_log2) - 1u));
+    }
+    // both row parts' loads in flight together
+    float x[16], y[16];
+    {
+      half8_t k0{}, k1{}, v0{}, v1{};
+      if (live) {
+        const _Float16* kp = a.k + t * a.k_stride_t + h * a.k_stride_h + li * 16;
+        const _Float16* vp = a.v + t * a.v_stride_t + h * a.v_stride_h + li * 16;
+        k0 = *reinterpret_cast<const half8_t*>(kp);
+        k1 = *reinterpret_cast<const half8_t*>(kp + 8);
+        v0 = *reinterpret_cast<const half8_t*>(vp);
+        v1 = *reinterpret_cast<const half8_t*>(vp + 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x[i] = (float)k0[i];
+        x[8 + i] = (float)k1[i];
+        y[i] = (float)v0[i];
+        y[8 + i] = (float)v1[i];
+      }
+    }
+
+    // ---- K: rotate (fp32 FWHT, one multiply, RNE to fp16) then RTN ----
+#pragma unroll
+    for (int hs = 1; hs < 16; hs <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if ((i & hs) == 0) {
+          const float p0 = x[i], p1 = x[i + hs];
+          x[i] = p0 + p1;
+          x[i + hs] = p0 - p1;
+        }
+      }
+    }
+    if constexpr (LPR > 1) fwht_stage_tracked<1>(x, t1);
+    if constexpr (LPR > 2) fwht_stage_tracked<2>(x, t2);
+    if constexpr (LPR > 4) fwht_stage_tracked<L::LANE4>(x, t4);
+    if constexpr (LPR > 8) fwht_stage_tracked<8>(x, t8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = (float)(_Float16)materialize(x[i] * srn);
+    rows_rtn_store<D>(x, live, li, row_out<BIG>(a.k_cache, a.kc_bytes, (uint64_t)row * D),
+                      row_out<BIG>(a.k_scale, a.ks_bytes, (uint64_t)row * 4u));
+
+    // ---- V: RTN, or 3-bit Lloyd-Max ----
+    if constexpr (!K8V3) {
+      rows_rtn_store<D>(y, live, li, row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * D),
+                        row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * 4u));
+    } else {
+      static_assert(D == 128 || D == 256, "K8V3 needs head_dim 128 or 256");
+      rows_lloydmax3_store<D>(y, live, li, search, cb, thr,
+                              row_out<BIG>(a.v_cache, a.vc_bytes, (uint64_t)row * (D / 32 * 3 * 4)),
+                              row_out<BIG>(a.v_scale, a.vs_bytes, (uint64_t)row * (D / 128 * 4)));
+    }
   }
 }
 
@@ -331,7 +455,7 @@ static int launch_append_impl(const AppendArgs& a, int head_dim, hipStream_t str
   const bool rows16 = ((uintptr_t)a.k % 16 == 0) && ((uintptr_t)a.v % 16 == 0) && a.k_stride_t % 8 == 0 &&
                       a.k_stride_h % 8 == 0 && a.v_stride_t % 8 == 0 && a.v_stride_h % 8 == 0;
   if (rows16) {  // several rows per wave
-    const int rows_per_wg = kAppendWaves * 64 / (head_dim / 16);
+    const int rows_per_wg = kAppendWaves * 64 / (head_dim / 16) * kRowsIters<K8V3>;
     const int64_t grid = (rows + rows_per_wg - 1) / rows_per_wg;
     S8KV_REQUIRE(grid < (int64_t(1) << 31), S8KV_ERR_INVALID, "append: too many rows (%lld)", (long long)rows);
     dim3 g((unsigned)grid), b(64 * kAppendWaves);

@@ -1,12 +1,14 @@
 """The K8V3 append picks each value's codeword with three comparisons (a binary
 search over "entry j is strictly nearer than entry j - 1", lloyd3_search in
-s8kv_device.h) where the oracle scans all eight entries for the first
-minimum.  The two agree for codebooks that pass lloyd3_search_ok (ascending,
-within [-4, 4], neighbours at least 2^-19 apart) and |u| <= 1.  The C checker
-beside this test compares them on every fp32 u in [-1, 1] and NaN, for the
-package codebook, a codebook at the smallest allowed spacing, one reaching
-+-4 and random ones; it reports a mismatch when the last step's entries are
-swapped, and rejects a codebook outside the condition."""
+s8kv_device.h; the rows kernel of s8kv_append.hip compares u against
+per-codebook thresholds T_j, the least u where that test holds, found by
+bisection) where the oracle scans all eight entries for the first minimum.
+They agree for codebooks that pass lloyd3_search_ok (ascending, within
+[-4, 4], neighbours at least 2^-19 apart) and |u| <= 1.  The C checker beside
+this test compares both forms with the scan on every fp32 u in [-1, 1] and
+NaN, for the package codebook, a codebook at the smallest allowed spacing, one
+reaching +-4 and random ones; it reports mismatches when T_4 is moved one
+fp32 step down, and rejects a codebook outside the condition."""
 
 import os
 import shutil
@@ -58,3 +60,11 @@ def test_codebook_outside_condition_rejected(checker):
     for cb in ([0, 1, 2, 3, 4, 5, 6, 7], [0.0, 0.1, 0.2, 0.3, 0.3, 0.5, 0.6, 0.7]):
         out = subprocess.run([str(checker), *map(str, cb)], capture_output=True, text=True, timeout=60)
         assert out.returncode == 2 and out.stdout.strip() == "rejected"
+
+
+def test_threshold_one_step_low_reported(checker):
+    cb = gaussian_codebook()
+    out = subprocess.run([str(checker), *[float(c).hex() for c in cb], "lower"], capture_output=True, text=True,
+                         timeout=300)
+    last = out.stdout.strip().splitlines()[-1]
+    assert out.returncode == 1 and int(last.split()[-1]) >= 1, out.stdout
