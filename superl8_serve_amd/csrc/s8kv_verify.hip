@@ -793,10 +793,442 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
   }
 }
 
-// Query rows per workgroup at this head_dim and layout (Cfg<D, K8V3>::ROWS),
-// and the workgroups a CU keeps resident (the kernel's launch bounds).
-static int rows_per_wg(int head_dim, bool k8v3) { return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1); }
-static int wg_per_cu(bool k8v3) { return k8v3 ? 1 : 2; }
+// ---------------------------------------------------------------------------
+// Wide verify (head_dim 128, paged int8 or K8V3 cache): 32 query rows per wave
+// on v_mfma_f32_32x32x16_f16, so every K and V operand a wave reads from LDS
+// feeds twice the MFMAs of a 16-row wave.  Lane (j = lane % 32, hf = lane /
+// 32) holds query row j of its wave:
+//   QK  : S^T[key][row] with A = K rows from LDS (key lane % 32, dims 64 hf ..
+//         64 hf + 63, 8 per MFMA), B = the rotated, pre-scaled q of row j over
+//         the same dims as fp16 hi + lo; lane l's result register r is key
+//         8 (r / 4) + 4 hf + r % 4 of row j, so the softmax state of a row
+//         lives in one lane pair (lane, lane ^ 32).
+//   PV  : O^T[dim][row], A = V^T through ds_read_b64_tr_b16 from a plain
+//         row-major fp16 V tile, B = the weights of the lane's own keys --
+//         k-step t uses result registers 8t .. 8t + 7, whose keys are the
+//         sixteen 16t + 8 (e / 4) + 4 hf + e % 4 that the transpose reads
+//         deliver (rows 16t + 4 hf + 0..3 and 16t + 8 + 4 hf + 0..3).
+// Numerics are the 16-row kernel's: the same q rotation and hi + lo split,
+// the same lazy-max online softmax and hi + lo weights; only the order of
+// the fp32 sums differs.
+// ---------------------------------------------------------------------------
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// a * b with 0 * x = 0 for every x, inf and NaN included (v_mul_legacy_f32):
+// a softmax weight of 0 (a hidden key) stays 0 whatever the key's V scale.
+// Otherwise the IEEE product, and as an asm result it is never contracted
+// into a following subtraction (the hi + lo split needs the rounded product).
+__device__ __forceinline__ float mul_zero_wins(float a, float b) {
+  float r;
+  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// x *= s element by element, each product written over its factor (a tied
+// asm operand): a rescale inside a branch then leaves the accumulator in the
+// registers it occupies on the path that skips it, with no copies at the merge.
+__device__ __forceinline__ void scale_in_place(float16_t& x, float s) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float v = x[i];
+    asm("v_mul_f32 %0, %0, %1" : "+v"(v) : "v"(s));
+    x[i] = v;
+  }
+}
+
+template <bool K8V3>
+struct WideCfg {
+  static constexpr int D = 128;
+  static constexpr int WAVES = 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int ROWS = 32 * WAVES;  // query rows per workgroup
+  static constexpr int KROW = 2 * D + 16;  // LDS pitch of an fp16 K row (8 consecutive rows: distinct 16-byte slots)
+  static constexpr int VROW = 2 * D + 32;  // LDS pitch of an fp16 V row (4 rows of a transpose read: distinct banks)
+  static constexpr int KBYTES = kTile * KROW;
+  static constexpr int VBYTES = kTile * VROW;
+  static constexpr int SBYTES = 2 * kTile * 4;  // k_scale, then the V scale (int8) or block norm (K8V3) per key
+  static constexpr int BUF = KBYTES + VBYTES + SBYTES;
+  static constexpr int CHUNKS = kTile * D / 16;  // 16-byte int8 chunks per K (or V) tile: one per thread
+  static_assert(CHUNKS == THREADS, "one K chunk and one V chunk per thread");
+  static constexpr int NG = D / 32;      // K8V3: 32-value code groups per key
+  static constexpr int WORDS = 3 * NG;   // K8V3: packed words per key
+  static constexpr int VJOBS = 2 * kTile * NG;  // K8V3: two threads per code group (16 values each)
+  static_assert(VJOBS == THREADS, "one K8V3 expansion job per thread");
+  static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
+};
+
+template <bool K8V3>
+__global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
+  using C = WideCfg<K8V3>;
+  constexpr int D = C::D;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
+
+  // workgroups of one (sequence, KV head) pair share an XCD (and its L2)
+  const int P = a.batch * a.num_kv_heads;
+  const int xcd = blockIdx.x & 7;
+  const int rest = blockIdx.x >> 3;
+  const int qb = rest % a.n_qblocks;
+  const int rest2 = rest / a.n_qblocks;
+  const int sp = rest2 % a.splits;
+  const int p = (rest2 / a.splits) * 8 + xcd;
+  if (p >= P) return;
+  const int b = p / a.num_kv_heads;
+  const int h = p - b * a.num_kv_heads;
+  const int G = a.group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31;  // this lane's query row within the wave (and the K row of its QK A operand)
+  const int hf = lane >> 5;
+
+  const int nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
+  const int prefix = max(0, a.prefix_lens[b]);
+  const int row0 = qb * C::ROWS;
+  const int pos_hi = min(nq, (row0 + C::ROWS + G - 1) / G);
+  const bool tree = a.tree_mask != nullptr;
+  int kv_end = prefix + (tree ? nq : pos_hi);
+  kv_end = min(kv_end, a.max_context_len);
+  if (row0 / G >= nq) kv_end = 0;
+  const int vis_all = tree ? prefix : prefix + row0 / G + 1;
+
+  const int r = row0 + wave * 32 + j;
+  const int pos = r / G;
+  const int head = h * G + (r - pos * G);
+  const bool row_live = pos < nq;
+  const uint64_t tmask = (tree && row_live) ? (uint64_t)a.tree_mask[(int64_t)b * a.max_queries + pos] : 0ull;
+
+  // ---- q: rotate (FWHT over dims 64 hf .. 64 hf + 63 in-lane, then across
+  // the lane pair), pre-scale, split into fp16 hi + lo ----
+  half8_t qhi[8], qlo[8];
+  {
+    float x[64];
+    const _Float16* qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)head * a.q_stride_h +
+                         (int64_t)(row_live ? pos : 0) * a.q_stride_s + hf * 64;
+#pragma unroll
+    for (int i = 0; i < 64; i += 8) {
+      const half8_t v = *reinterpret_cast<const half8_t*>(qp + i);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[i + e] = row_live ? (float)v[e] : 0.0f;
+    }
+#pragma unroll
+    for (int hs = 1; hs < 64; hs <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        if ((i & hs) == 0) {
+          const float x0 = x[i], x1 = x[i + hs];
+          x[i] = x0 + x1;
+          x[i + hs] = x0 - x1;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 64; ++i) x[i] = butterfly_x32(x[i], lane);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // (materialized: hi and lo must both come from this one fp32 value)
+        const float val = materialize(x[8 * m + e] * a.qscale);
+        const _Float16 qh = (_Float16)val;
+        qhi[m][e] = qh;
+        qlo[m][e] = (_Float16)(val - (float)qh);
+      }
+    }
+  }
+
+  float m_ref = kMaxInit, l_run = 0.0f;
+  float16_t acc[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) acc[n] = float16_t{};
+  WeightShift ws(kMaxSlack);
+
+  const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
+  const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
+  const rsrc_t ks = make_rsrc(a.k_scale, a.ks_bytes);
+  const rsrc_t vs = make_rsrc(a.v_scale, a.vs_bytes);
+  uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
+  if constexpr (K8V3) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
+      const uint32_t lw = hb & 0xFFu, hw = hb >> 8;
+      if (i < 4) { tlo03 |= lw << (8 * i); thi03 |= hw << (8 * i); }
+      else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
+    }
+  }
+  const int bs_log2 = a.bs_log2;
+  const uint32_t bsm = (1u << bs_log2) - 1u;
+  const uint32_t hkv = (uint32_t)a.num_kv_heads;
+  const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
+
+  int k_lo = 0, k_hi = kv_end;
+  if (a.splits > 1) {
+    const int chunk = ((max(0, kv_end) + a.splits - 1) / a.splits + kTile - 1) & ~(kTile - 1);
+    k_lo = sp * chunk;
+    k_hi = min(kv_end, k_lo + chunk);
+  }
+  for (int u0 = k_lo; u0 < k_hi; u0 += kSubKeys) {
+    const int u1 = min(k_hi, u0 + kSubKeys);
+    const int fb = u0 >> bs_log2;
+    const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
+    __syncthreads();  // previous users of bt_lds and the tile buffers are done
+    for (int i = tid; i < nblk; i += C::THREADS) bt_lds[i] = bt_row[fb + i];
+    __syncthreads();
+
+    auto row_of = [&](int kk) -> uint32_t {
+      kk = min(kk, u1 - 1);
+      const uint32_t blk = (uint32_t)bt_lds[(kk >> bs_log2) - fb];
+      return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)kk & bsm);
+    };
+
+    struct TileRegs {
+      u32x4_t k, v;
+      float s;
+    };
+    // one 16-byte K chunk and one V chunk (K8V3: a half code group's three
+    // words) per thread, and the tile's 2 x 32 scales in threads 0..63
+    auto load_tile = [&](TileRegs& R, int base) {
+      const int tt = tid >> 3, part = tid & 7;
+      const uint32_t row = row_of(base + tt);
+      R.k = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
+      if constexpr (K8V3) {
+        const int grp = tid >> 1;
+        const int gt = grp / C::NG, gi = grp % C::NG;
+        const uint32_t off = row_of(base + gt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
+        R.v.x = bload32(vc, off);
+        R.v.y = bload32(vc, off + 4);
+        R.v.z = bload32(vc, off + 8);
+      } else {
+        R.v = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
+      }
+      // (two loads, each with one descriptor: a descriptor chosen per lane
+      // would be issued lane by lane)
+      if (tid < kTile) R.s = __builtin_bit_cast(float, bload32(ks, row_of(base + tid) * 4u));
+      else if (tid < 2 * kTile) R.s = __builtin_bit_cast(float, bload32(vs, row_of(base + tid - kTile) * 4u));
+    };
+    auto store_tile = [&](const TileRegs& R, int buf) {
+      char* kb = smem + buf * C::BUF;
+      char* vb = kb + C::KBYTES;
+      float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
+      const int tt = tid >> 3, part = tid & 7;
+      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k.x, R.k.y});
+      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k.z, R.k.w});
+      if constexpr (K8V3) {  // 16 codes of one group -> fp16 codebook entries
+        const int grp = tid >> 1, half = tid & 1;
+        const int gt = grp / C::NG, gi = grp % C::NG;
+        const int sh = half * 16;
+        const uint32_t w0 = R.v.x >> sh, w1 = R.v.y >> sh, w2 = R.v.z >> sh;
+        char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4 += 2) {
+          u32x4_t o;
+          const uint32_t sel0 =
+              spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
+          const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
+                                (spread4(w2 >> (4 * q4 + 4)) << 2);
+          const u32x2_t r0 = codebook_lookup4(sel0, tlo03, tlo47, thi03, thi47);
+          const u32x2_t r1 = codebook_lookup4(sel1, tlo03, tlo47, thi03, thi47);
+          o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+          *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
+        }
+      } else {
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v.x, R.v.y});
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v.z, R.v.w});
+      }
+      if (tid < 2 * kTile) sb[tid] = R.s;
+    };
+
+    // ---- one 32-key tile from LDS buffer `buf` ----
+    // Only the scores depend on the tile's kind (keys hidden from some row:
+    // masked, as -inf); the rescale, the weights and the PV are one code path
+    // for every tile, so the accumulators keep their registers throughout.
+    auto process = [&](int buf, int base, bool masked) {
+      const char* kb = smem + buf * C::BUF;
+      const char* vb = kb + C::KBYTES;
+      const float* sb = reinterpret_cast<const float*>(vb + C::VBYTES);
+      float16_t sc = float16_t{};
+      {
+        const char* krow = kb + j * C::KROW + hf * 128;
+        half8_t ka[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) ka[m] = *reinterpret_cast<const half8_t*>(krow + 16 * m);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          sc = mfma32x32x16(ka[m], qhi[m], sc);
+          sc = mfma32x32x16(ka[m], qlo[m], sc);
+        }
+      }
+      // this lane's keys: register r is key 8 (r / 4) + 4 hf + r % 4
+      float4_t ks4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ks4[q] = *reinterpret_cast<const float4_t*>(sb + 8 * q + 4 * hf);
+      auto kscale = [&](int rr) -> float { return ks4[rr >> 2][rr & 3]; };
+      float y[16];  // score relative to the running max, log2 domain; -inf: hidden from this row
+      if (masked) {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+          const int kk = base + 8 * (rr >> 2) + 4 * hf + (rr & 3);
+          const int di = kk - prefix;
+          const bool dvis = tree ? ((uint32_t)di < 64u && ((tmask >> (di & 63)) & 1ull)) : di <= pos;
+          const bool vis = kk < kv_end && row_live && (di < 0 || dvis);
+          const float v = __builtin_fmaf(sc[rr], kscale(rr), -m_ref);
+          y[rr] = vis ? v : kNegInf;
+        }
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) y[rr] = __builtin_fmaf(sc[rr], kscale(rr), -m_ref);
+      }
+      float my = y[0];
+#pragma unroll
+      for (int rr = 1; rr < 16; ++rr) my = fmaxf(my, y[rr]);
+      my = max_x32(my);
+      // V-scale bound test: lane l checks the V scale of key l % 32
+      const float vp = sb[kTile + j];
+      if (__builtin_amdgcn_ballot_w64(my > ws.thr() || vp > ws.vbound()) != 0) {
+        // rare: a V scale above the bound lowers the weight shift (by d, a
+        // power of two folded into alpha), or a score passes the lazy slack:
+        // the running max rises to the tile's (from the products, exactly),
+        // l and the accumulators are rescaled, the scores re-referenced
+        int d = 0;
+        if (__builtin_amdgcn_ballot_w64(vp > ws.vbound()) != 0) {
+          float vmx = fmaxf(vp, shfl_xor_f(vp, 1));
+          vmx = fmaxf(vmx, shfl_xor_f(vmx, 2));
+          vmx = fmaxf(vmx, shfl_xor_f(vmx, 4));
+          vmx = fmaxf(vmx, shfl_xor_f(vmx, 8));
+          d = ws.raise(max_x16(vmx), kMaxSlack);
+        }
+        m_ref -= (float)d;
+        float mt = kNegInf;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) mt = fmaxf(mt, y[rr] != kNegInf ? sc[rr] * kscale(rr) : kNegInf);
+        mt = max_x32(mt);
+        const float m_new = fmaxf(m_ref, mt - (float)ws.esh);
+        const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new) * __builtin_ldexpf(1.0f, d);
+        l_run *= alpha;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) scale_in_place(acc[n], alpha);
+        m_ref = m_new;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) y[rr] = y[rr] != kNegInf ? __builtin_fmaf(sc[rr], kscale(rr), -m_new) : kNegInf;
+      }
+      const int li = lane & 15;
+      const char* vrow = vb + (4 * hf + (li >> 2)) * C::VROW + (16 * ((lane >> 4) & 1) + 4 * (li & 3)) * 2;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        // weights p * (V scale | block norm) of keys 16t .. 16t + 15 as fp16
+        // hi + lo (hi: the top 11 significant bits, exact in fp16 over its
+        // normal range; lo: the rest); hidden keys weigh 0 whatever their
+        // scale (inf and NaN included)
+        const float4_t vs0 = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * t + 4 * hf);
+        const float4_t vs1 = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * t + 8 + 4 * hf);
+        half8_t pbh, pbl;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float wh[2], wl[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int rr = 8 * t + e + u;
+            const float ev = __builtin_amdgcn_exp2f(y[rr]);  // 0 for hidden keys
+            l_run += ev;
+            const float w = mul_zero_wins(ev, e + u < 4 ? vs0[e + u] : vs1[e + u - 4]);
+            wh[u] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & 0xFFFFE000u);
+            wl[u] = w - wh[u];
+          }
+          const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh[0], wh[1]));
+          const half2_t l2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl[0], wl[1]));
+          pbh[e] = h2[0];
+          pbh[e + 1] = h2[1];
+          pbl[e] = l2[0];
+          pbl[e + 1] = l2[1];
+        }
+        // PV: V^T operands by transpose reads; lane (li, group G) reads row
+        // 16t + 4 hf + li / 4 (+ 8), dims 32 n + 16 (G & 1) + 4 (li % 4) .. + 3
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const char* src = vrow + 16 * t * C::VROW + 64 * n;
+          const i16x4_t lw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(src));
+          const i16x4_t hw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((S8KV_LDS i16x4_t*)(src + 8 * C::VROW));
+          const half4_t l4 = __builtin_bit_cast(half4_t, lw), h4 = __builtin_bit_cast(half4_t, hw);
+          const half8_t va = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+          acc[n] = mfma32x32x16(va, pbh, acc[n]);
+          acc[n] = mfma32x32x16(va, pbl, acc[n]);
+        }
+      }
+    };
+
+    // a tile is masked when it reaches keys that some row of the block does
+    // not see, or the end of the visible keys (wave-uniform)
+    auto compute = [&](int buf, int base) { process(buf, base, !(base + kTile <= vis_all && base + kTile <= kv_end)); };
+    const int ntiles = (u1 - u0 + kTile - 1) / kTile;
+    TileRegs ra, rb;
+    load_tile(ra, u0);
+    if (ntiles > 1) load_tile(rb, u0 + kTile);
+    store_tile(ra, 0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {  // (one exit: the accumulators keep their registers)
+      const int base = u0 + t * kTile;
+      if (t + 2 < ntiles) load_tile(ra, base + 2 * kTile);
+      compute(0, base);
+      if (t + 1 < ntiles) store_tile(rb, 1);
+      __syncthreads();
+      if (t + 1 < ntiles) {
+        if (t + 3 < ntiles) load_tile(rb, base + 3 * kTile);
+        compute(1, base + kTile);
+        if (t + 2 < ntiles) store_tile(ra, 0);
+        __syncthreads();
+      }
+    }
+  }
+
+  const float l_tot = sum_x32(l_run);
+  // ---- split: this wave's unnormalized rows to the partials ----
+  if (a.splits > 1) {
+    const int rl = wave * 32 + j;
+    float* pr = a.part + ((((int64_t)p * a.n_qblocks + qb) * a.splits + sp) * C::ROWS + rl) * (D + 4);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4_t*>(pr + 32 * n + 8 * q + 4 * hf) =
+            float4_t{acc[n][4 * q], acc[n][4 * q + 1], acc[n][4 * q + 2], acc[n][4 * q + 3]};
+    }
+    if (hf == 0) {
+      pr[D] = m_ref;
+      pr[D + 1] = l_tot;
+    }
+    return;
+  }
+
+  // ---- normalize and write this lane's half of row j ----
+  if (pos < a.max_queries) {
+    const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    _Float16* op = a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        half4_t o;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[rr] = (_Float16)(acc[n][4 * q + rr] * inv);
+        *reinterpret_cast<half4_t*>(op + 32 * n + 8 * q + 4 * hf) = o;
+      }
+    }
+  }
+}
+
+// Query rows per workgroup at this head_dim and layout (Cfg<D, K8V3>::ROWS,
+// or WideCfg::ROWS for the wide kernel), and the workgroups a CU keeps
+// resident (the kernels' launch bounds).  The wide kernel serves the paged
+// head_dim-128 calls without a window whose tensors fit 32-bit offsets.
+static bool use_wide(int head_dim, bool windowed, bool big) { return head_dim == 128 && !windowed && !big; }
+static int rows_per_wg(int head_dim, bool k8v3, bool wide = false) {
+  if (wide) return WideCfg<false>::ROWS;
+  return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1);
+}
+static int wg_per_cu(bool k8v3, bool wide = false) { return wide ? 2 : (k8v3 ? 1 : 2); }
 
 // Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
 // KV head, query block) merges the row's `splits` partials -- each relative to
@@ -909,6 +1341,37 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
                  : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
+template <bool K8V3>
+static int launch_wide(VerifyArgs& a, hipStream_t stream) {
+  using C = WideCfg<K8V3>;
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
+      set_error("s8kv_verify: cannot set the dynamic LDS size");
+      return S8KV_ERR_LAUNCH;
+    }
+    attr = true;
+  }
+  const int P = a.batch * a.num_kv_heads;
+  const int64_t grid = (int64_t)8 * a.n_qblocks * a.splits * ((P + 7) / 8);
+  if (grid > INT32_MAX) {
+    set_error("s8kv_verify: grid too large");
+    return S8KV_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((verify_wide_kernel<K8V3>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream, a);
+  if (a.splits > 1) {
+    const int rc = check_launch("s8kv_verify");
+    if (rc != S8KV_OK) return rc;
+    const int64_t units = (int64_t)P * a.n_qblocks;
+    hipLaunchKernelGGL((verify_combine_kernel<C::D, C::ROWS>),
+                       dim3((unsigned)(units * (C::ROWS * (C::D / 4) / kCombineThreads))), dim3(kCombineThreads), 0,
+                       stream, a);
+    return check_launch("s8kv_verify_combine");
+  }
+  return check_launch("s8kv_verify");
+}
+
 }  // namespace verify
 }  // namespace s8kv
 
@@ -934,9 +1397,9 @@ constexpr int kMinSplitKeys = 1024;
 constexpr int kMaxSplitKeys = 1 << 20;
 constexpr int kMaxSplits = 1024;
 static std::atomic<int> g_verify_splits{0};  // 0: planned per call
-static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3) {
+static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3, bool wide) {
   const int64_t natural = (int64_t)batch * num_kv_heads * n_qblocks;
-  const int64_t resident = (int64_t)verify::wg_per_cu(k8v3) * device_cus();
+  const int64_t resident = (int64_t)verify::wg_per_cu(k8v3, wide) * device_cus();
   int64_t s = natural < resident ? (resident + natural - 1) / natural : 1;
   s = std::min<int64_t>(s, std::max(1, keys / kMinSplitKeys));
   s = std::max<int64_t>(s, ((int64_t)keys + kMaxSplitKeys - 1) / kMaxSplitKeys);
@@ -944,9 +1407,11 @@ static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int ke
   if (forced > 0) s = forced;
   return (int)std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
 }
-static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits, bool k8v3) {
+static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits, bool k8v3,
+                                 bool wide) {
   if (splits <= 1) return 0;
-  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim, k8v3) * (head_dim + 4) * 4;
+  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim, k8v3, wide) *
+         (head_dim + 4) * 4;
 }
 
 extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int num_kv_heads, int head_dim,
@@ -954,14 +1419,18 @@ extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int nu
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_queries <= 0 ||
       max_context_len < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
-  // either layout (its workgroups differ in query rows): the larger need
+  // either layout and kernel (their workgroups differ in query rows): the larger need
   int64_t need = 0;
   for (const bool k8v3 : {false, true}) {
-    const int rows_wg = verify::rows_per_wg(head_dim, k8v3);
-    const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
-    need = std::max(need, verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
-                                            verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len, k8v3),
-                                            k8v3));
+    for (const bool wide : {false, true}) {
+      if (wide && head_dim != 128) continue;
+      const int rows_wg = verify::rows_per_wg(head_dim, k8v3, wide);
+      const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
+      need = std::max(need, verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
+                                              verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len,
+                                                                 k8v3, wide),
+                                              k8v3, wide));
+    }
   }
   return need;
 }
@@ -973,12 +1442,12 @@ extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int nu
 // the workspace cannot hold it (the call is then slower, not different in
 // kind); a block reading more than kMaxSplitKeys keys must split, so then a
 // missing or short workspace is an error.
-static int verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, void* workspace,
+static int verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, bool wide, void* workspace,
                                 int64_t workspace_bytes) {
   const int keys = a.window > 0 ? (int)std::min<int64_t>(a.max_context_len, (int64_t)a.window + a.max_queries)
                                 : a.max_context_len;
-  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3);
-  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3);
+  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3, wide);
+  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3, wide);
   const bool fits = workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0;
   if (s > 1 && fits) {
     a.splits = s;
@@ -1004,7 +1473,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
                         const int8_t* k_cache, const float* k_scale, int64_t num_blocks, int block_size,
                         const int32_t* block_table, int64_t block_table_stride, const int32_t* prefix_lens,
                         const int32_t* query_lens, const int64_t* tree_mask, int max_context_len, float scale,
-                        void* out, bool k8v3) {
+                        void* out, bool k8v3, bool windowed) {
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
@@ -1044,7 +1513,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  const int rows_wg = verify::rows_per_wg(head_dim, k8v3);
+  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, windowed, a.big));
   a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
@@ -1065,10 +1534,11 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false, window > 0);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  if (const int rc = verify_use_workspace(a, head_dim, false, workspace, workspace_bytes)) return rc;
+  const bool wide = verify::use_wide(head_dim, window > 0, a.big);
+  if (const int rc = verify_use_workspace(a, head_dim, false, wide, workspace, workspace_bytes)) return rc;
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -1100,6 +1570,7 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
     }
     return S8KV_ERR_UNSUPPORTED;
   }
+  if (wide) return verify::launch_wide<false>(a, s);
   switch (head_dim) {
     case 64: return verify::launch<64, false>(a, s);
     case 128: return verify::launch<128, false>(a, s);
@@ -1157,10 +1628,11 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true, window > 0);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  if (const int rc = verify_use_workspace(a, head_dim, true, workspace, workspace_bytes)) return rc;
+  const bool wide = verify::use_wide(head_dim, window > 0, a.big);
+  if (const int rc = verify_use_workspace(a, head_dim, true, wide, workspace, workspace_bytes)) return rc;
   if (fresh != nullptr && fresh->k != nullptr) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
@@ -1188,6 +1660,7 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   hipStream_t s = (hipStream_t)stream;
   if (a.window > 0)
     return head_dim == 128 ? verify::launch<128, true, true>(a, s) : verify::launch<256, true, true>(a, s);
+  if (wide) return verify::launch_wide<true>(a, s);
   return head_dim == 128 ? verify::launch<128, true>(a, s) : verify::launch<256, true>(a, s);
 }
 
