@@ -817,25 +817,19 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
-// a * b with 0 * x = 0 for every x, inf and NaN included (v_mul_legacy_f32):
-// a softmax weight of 0 (a hidden key) stays 0 whatever the key's V scale.
-// Otherwise the IEEE product, and as an asm result it is never contracted
-// into a following subtraction (the hi + lo split needs the rounded product).
-__device__ __forceinline__ float mul_zero_wins(float a, float b) {
-  float r;
-  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-// x *= s element by element, each product written over its factor (a tied
-// asm operand): a rescale inside a branch then leaves the accumulator in the
-// registers it occupies on the path that skips it, with no copies at the merge.
-__device__ __forceinline__ void scale_in_place(float16_t& x, float s) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float v = x[i];
-    asm("v_mul_f32 %0, %0, %1" : "+v"(v) : "v"(s));
-    x[i] = v;
-  }
+// Two fp32 weights as fp16 hi + lo pairs: hi = w rounded toward zero to fp16
+// (its top 11 significant bits in fp16's normal range), lo = w - hi exactly
+// (v_fma_mix_f32 reads hi as fp16 out of the packed register), then rounded
+// toward zero to fp16.  The asm reads only results of ordinary VALU
+// instructions (no transcendental or MFMA result, whose wait states the
+// compiler inserts for its own instructions only), and the rounded w it
+// takes cannot be contracted into the subtraction.
+__device__ __forceinline__ void split_pair(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w0, w1));
+  float l0, l1;
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l0) : "v"(hi), "v"(w0));
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(l1) : "v"(hi), "v"(w1));
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
 }
 
 template <bool K8V3>
@@ -1038,7 +1032,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v.x, R.v.y});
         *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v.z, R.v.w});
       }
-      if (tid < 2 * kTile) sb[tid] = R.s;
+      // a V scale is staged finite (NaN and inf -> 2^100): the weight of a
+      // hidden key, exp2(-inf) * scale, is then 0 whatever was stored there
+      // (clamped here, where the load is consumed, not where it is issued)
+      if (tid < 2 * kTile) sb[tid] = tid < kTile ? R.s : fminf(R.s, 0x1p100f);
     };
 
     // ---- one 32-key tile from LDS buffer `buf` ----
@@ -1109,7 +1106,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new) * __builtin_ldexpf(1.0f, d);
         l_run *= alpha;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) scale_in_place(acc[n], alpha);
+        for (int n = 0; n < 4; ++n) acc[n] *= alpha;  // (plain VALU: its MFMA hazards are the compiler's)
         m_ref = m_new;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) y[rr] = y[rr] != kNegInf ? __builtin_fmaf(sc[rr], kscale(rr), -m_new) : kNegInf;
@@ -1124,26 +1121,23 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         // scale (inf and NaN included)
         const float4_t vs0 = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * t + 4 * hf);
         const float4_t vs1 = *reinterpret_cast<const float4_t*>(sb + kTile + 16 * t + 8 + 4 * hf);
-        half8_t pbh, pbl;
+        u32x4_t hi4, lo4;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          float wh[2], wl[2];
+          float w[2];
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int rr = 8 * t + e + u;
             const float ev = __builtin_amdgcn_exp2f(y[rr]);  // 0 for hidden keys
             l_run += ev;
-            const float w = mul_zero_wins(ev, e + u < 4 ? vs0[e + u] : vs1[e + u - 4]);
-            wh[u] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & 0xFFFFE000u);
-            wl[u] = w - wh[u];
+            w[u] = ev * (e + u < 4 ? vs0[e + u] : vs1[e + u - 4]);  // (finite scales: 0 for hidden keys)
           }
-          const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wh[0], wh[1]));
-          const half2_t l2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(wl[0], wl[1]));
-          pbh[e] = h2[0];
-          pbh[e + 1] = h2[1];
-          pbl[e] = l2[0];
-          pbl[e + 1] = l2[1];
+          uint32_t hw, lw;
+          split_pair(w[0], w[1], hw, lw);
+          hi4[e / 2] = hw;
+          lo4[e / 2] = lw;
         }
+        const half8_t pbh = __builtin_bit_cast(half8_t, hi4), pbl = __builtin_bit_cast(half8_t, lo4);
         // PV: V^T operands by transpose reads; lane (li, group G) reads row
         // 16t + 4 hf + li / 4 (+ 8), dims 32 n + 16 (G & 1) + 4 (li % 4) .. + 3
 #pragma unroll
