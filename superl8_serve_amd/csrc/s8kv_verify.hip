@@ -964,6 +964,13 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
     k_lo = sp * chunk;
     k_hi = min(kv_end, k_lo + chunk);
   }
+  // A wave whose 32 rows are all past the query count (a short draft tree,
+  // the last block of a chunk) takes part in the tile loads, conversions and
+  // barriers only; its rows are written as zeros.  The key loop is
+  // instantiated for both kinds of wave, so neither carries the other's branch.
+  const bool wave_live = (row0 + wave * 32) / G < nq;
+  auto key_loop = [&](auto live_tag) {
+  constexpr bool LIVE = decltype(live_tag)::value;
   for (int u0 = k_lo; u0 < k_hi; u0 += kSubKeys) {
     const int u1 = min(k_hi, u0 + kSubKeys);
     const int fb = u0 >> bs_log2;
@@ -1155,7 +1162,9 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 
     // a tile is masked when it reaches keys that some row of the block does
     // not see, or the end of the visible keys (wave-uniform)
-    auto compute = [&](int buf, int base) { process(buf, base, !(base + kTile <= vis_all && base + kTile <= kv_end)); };
+    auto compute = [&](int buf, int base) {
+      if constexpr (LIVE) process(buf, base, !(base + kTile <= vis_all && base + kTile <= kv_end));
+    };
     const int ntiles = (u1 - u0 + kTile - 1) / kTile;
     TileRegs ra, rb;
     load_tile(ra, u0);
@@ -1176,6 +1185,11 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       }
     }
   }
+  };
+  if (wave_live)
+    key_loop(std::true_type{});
+  else
+    key_loop(std::false_type{});
 
   const float l_tot = sum_x32(l_run);
   // ---- split: this wave's unnormalized rows to the partials ----
