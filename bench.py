@@ -172,21 +172,27 @@ def decode_layer(w, layer: int, fused: bool, plan=None):
                                         w["bt"], w["cl"], BS, max_context_len=MAX_LEN, scale=scale)
 
 
-def step_plan(w):
+def step_plan(w, adaptive: bool = False):
     """The step's slice plan: one launch, shared by the 36 layers' launches
-    (every layer decodes the same rows)."""
+    (every layer decodes the same rows).  `adaptive`: made into the
+    workload's one plan tensor, whose slice bounds follow the last step's
+    measured workgroup times (two launches: bounds, then plan)."""
     from superl8_serve_amd import ops
 
-    return ops.attn_paged_decode_plan(w["kc"][0], w["bt"], w["cl"], BS, num_q_heads=HQ, max_context_len=MAX_LEN)
+    if not adaptive:
+        return ops.attn_paged_decode_plan(w["kc"][0], w["bt"], w["cl"], BS, num_q_heads=HQ, max_context_len=MAX_LEN)
+    w["plan"] = ops.attn_paged_decode_plan(w["kc"][0], w["bt"], w["cl"], BS, num_q_heads=HQ, max_context_len=MAX_LEN,
+                                           adaptive=True, plan=w.get("plan"))
+    return w["plan"]
 
 
-def make_step(w, fused: bool, planned: bool = True):
+def make_step(w, fused: bool, planned: bool = True, adaptive: bool = False):
     """The 36-layer step; the fused form starts with the step's plan launch
-    when `planned`."""
+    when `planned` (adaptive slice bounds when `adaptive`)."""
     outs = [None] * NUM_LAYERS
 
     def step():
-        plan = step_plan(w) if fused and planned else None
+        plan = step_plan(w, adaptive) if fused and planned else None
         for layer in range(NUM_LAYERS):
             outs[layer] = decode_layer(w, layer, fused, plan)
         return outs
@@ -194,14 +200,15 @@ def make_step(w, fused: bool, planned: bool = True):
     return step
 
 
-def time_decode_kernel(w, reps: int, fused: bool, planned: bool = True) -> dict:
+def time_decode_kernel(w, reps: int, fused: bool, planned: bool = True, adaptive: bool = False) -> dict:
     """Average duration of the decode attention kernel (which also combines
     the partials of rows split across workgroups), from HIP events the library
     records on the launch stream around each launch (s8kv_timing_begin/end),
     over `reps` eager passes of the 36
     decode calls (the one-launch step when `fused`: its append rewrites the
-    same bytes).  A preceding spin kernel keeps the GPU ahead of the host so
-    host launch latency never enters an interval."""
+    same bytes; an adaptive plan is made again before each pass).  A
+    preceding spin kernel keeps the GPU ahead of the host so host launch
+    latency never enters an interval."""
     import ctypes
 
     import torch
@@ -210,11 +217,13 @@ def time_decode_kernel(w, reps: int, fused: bool, planned: bool = True) -> dict:
 
     lib = _lib.load()
     scale = 1.0 / math.sqrt(D)
-    plan = step_plan(w) if fused and planned else None
+    plan = step_plan(w, adaptive) if fused and planned else None
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2e8))  # ~0.1 s of GPU spin while the host enqueues
     _lib.check(lib.s8kv_timing_begin(), "s8kv_timing_begin")
     for _ in range(reps):
+        if fused and planned and adaptive:
+            plan = step_plan(w, True)
         for layer in range(NUM_LAYERS):
             if fused:
                 decode_layer(w, layer, True, plan)
@@ -340,7 +349,7 @@ def read_ceiling(w, steps: int) -> dict:
 TRACE_WORDS = 16  # per-workgroup record of the decode trace build
 
 
-def trace_decode(steps: int, warmup: int) -> dict:
+def trace_decode(steps: int, warmup: int, adaptive: bool = True) -> dict:
     """Per-launch breakdown of the one-launch decode step from the trace
     build of the library (libsuperl8_kv_trace.so: the same kernels, the decode
     kernel stamping the device's 100 MHz clock at fixed points of each
@@ -364,7 +373,7 @@ def trace_decode(steps: int, warmup: int) -> dict:
     stride = cus * 8 * TRACE_WORDS  # the largest grid the decode launches (8 workgroups per CU)
     buf = torch.zeros(NUM_LAYERS * stride, dtype=torch.int64, device="cuda")
     _lib.check(fn(buf.data_ptr(), stride, NUM_LAYERS), "s8kv_decode_trace_set")
-    step = make_step(w, True)
+    step = make_step(w, True, True, adaptive)
     sec = _time_graph(step, steps, warmup)
     _lib.check(fn(None, 0, 0), "s8kv_decode_trace_set")
     rec = buf.view(NUM_LAYERS, cus * 8, TRACE_WORDS).cpu().numpy().view(np.uint64)
@@ -406,6 +415,7 @@ def trace_decode(steps: int, warmup: int) -> dict:
     gaps = [us(np.uint64(starts[i + 1] - ends[i])) for i in range(NUM_LAYERS - 1)]
     return {
         "trace": "decode_kernel<128, int8, fused append>, Qwen3-8B batch-64 step, trace build",
+        "slice_plan": "adaptive" if adaptive else "fixed split",
         "step_ms_trace_build": round(sec * 1e3, 4),
         "workgroups_per_launch": int(((rec[0][:, 9] & np.uint64(1)) == 1).sum()),
         "prologue_us_from_workgroup_start": {k: round(med(v), 2) for k, v in phases.items()},
@@ -728,12 +738,12 @@ def k8v3_workload(dev, layers: int = NUM_LAYERS, keep_rows=()):
             "prefix_kv": kept}
 
 
-def run_k8v3(steps: int, warmup: int, fused: bool, planned: bool = True) -> None:
+def run_k8v3(steps: int, warmup: int, fused: bool, planned: bool = True, adaptive: bool = False) -> None:
     """Qwen3-8B K8V3 decode step, batch 32, contexts U{8192..32768} (seed 2):
     36 layers x (append 1 token per sequence + decode), pool 1.2x the blocks
     needed, distinct storage per layer; one launch per layer
     (attn_paged_decode_append_k8v3, after the step's one plan launch when
-    `planned`) unless `fused` is False."""
+    `planned`, adaptive when `adaptive`) unless `fused` is False."""
     import torch
 
     from superl8_serve_amd import ops
@@ -746,8 +756,12 @@ def run_k8v3(steps: int, warmup: int, fused: bool, planned: bool = True) -> None
     scale = 1.0 / math.sqrt(D)
 
     def step():
-        plan = (ops.attn_paged_decode_plan(kc[0], btd, cl, BS, num_q_heads=HQ, max_context_len=max_ctx,
-                                           layout="k8v3") if fused and planned else None)
+        plan = None
+        if fused and planned:
+            plan = ops.attn_paged_decode_plan(kc[0], btd, cl, BS, num_q_heads=HQ, max_context_len=max_ctx,
+                                              layout="k8v3", adaptive=adaptive, plan=w.get("plan"))
+            if adaptive:
+                w["plan"] = plan
         for layer in range(NUM_LAYERS):
             if fused:
                 ops.attn_paged_decode_append_k8v3(q[layer], k_new[layer], v_new[layer], kc[layer], ks[layer],
@@ -787,7 +801,10 @@ def run_k8v3(steps: int, warmup: int, fused: bool, planned: bool = True) -> None
                    "batch": t, "sum_context_tokens": int(lens.sum()), "pool_blocks_per_layer": n_blocks,
                    "bytes_per_step": step_b,
                    "append": "in the decode launch (attn_paged_decode_append_k8v3)" if fused
-                             else "separate kernel (quantize_kv_write_paged_k8v3)"},
+                             else "separate kernel (quantize_kv_write_paged_k8v3)",
+                   "slice_plan": ("none" if not (fused and planned) else
+                                  "adaptive (bounds from the last step's workgroup times)" if adaptive
+                                  else "fixed split")},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2)}))
 
 
@@ -1047,6 +1064,9 @@ def main():
                     help="graph replays per read-ceiling probe (0 = skip the read-ceiling leg)")
     ap.add_argument("--no-plan", action="store_true",
                     help="fused step without the per-step slice plan (every launch locates its own work)")
+    ap.add_argument("--fixed-split", action="store_true",
+                    help="the step's plan with the fixed slice split (default: adaptive slice bounds that follow "
+                         "the last step's measured workgroup times)")
     ap.add_argument("--separate-append", action="store_true",
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
@@ -1081,7 +1101,7 @@ def main():
         from superl8_serve_amd import build_ext
 
         _lib.LIB_PATH = build_ext.TRACE_LIB_PATH
-        print(json.dumps(trace_decode(args.steps, args.warmup)))
+        print(json.dumps(trace_decode(args.steps, args.warmup, not args.fixed_split)))
         return
     _lib.load()
     if args.calibrate_copy_mib:
@@ -1091,7 +1111,7 @@ def main():
         run_verify(args.workload.removesuffix("_k8v3"), args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
         return
     if args.workload == "k8v3":
-        run_k8v3(args.steps, args.warmup, not args.separate_append, not args.no_plan)
+        run_k8v3(args.steps, args.warmup, not args.separate_append, not args.no_plan, not args.fixed_split)
         return
     if args.workload == "copy":
         run_copy(args.steps)
@@ -1110,7 +1130,8 @@ def main():
     w = build(device)
     fused = not args.separate_append
     planned = fused and not args.no_plan
-    step = make_step(w, fused, planned)
+    adaptive = planned and not args.fixed_split
+    step = make_step(w, fused, planned, adaptive)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -1138,7 +1159,7 @@ def main():
     b = step_bytes(w["lens"])
     value = b["step"] / (ms * 1e-3) / 1e9
     # eager per-launch timing: required for the two-call step, a cross-check otherwise
-    kt = (time_decode_kernel(w, args.kernel_reps, fused, planned) if args.kernel_reps > 0 or not fused
+    kt = (time_decode_kernel(w, args.kernel_reps, fused, planned, adaptive) if args.kernel_reps > 0 or not fused
           else {"decode_s": None, "launches": 0})
     kernel = "decode_kernel<128, int8, fused append>" if fused else "decode_kernel<128, int8>"
     kernel_bytes = b["fused_layer"] if fused else b["decode_layer"]
@@ -1178,8 +1199,10 @@ def main():
             "bytes_per_step": b["step"],
             "append": "in the decode launch (attn_paged_decode_append)" if fused
                       else "separate kernel (quantize_kv_write_paged)",
-            "slice_plan": "one attn_paged_decode_plan launch per step, read by the 36 launches" if planned
-                          else "none (every launch locates its own work)",
+            "slice_plan": ("none (every launch locates its own work)" if not planned else
+                           "one adaptive attn_paged_decode_plan per step (slice bounds from the last step's "
+                           "workgroup times), read by the 36 launches" if adaptive else
+                           "one attn_paged_decode_plan launch per step (fixed split), read by the 36 launches"),
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "roofline": {

@@ -196,6 +196,26 @@ int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                      const int32_t* context_lens, int max_context_len, void* plan, int64_t plan_bytes, void* stream);
 
 /*
+ * s8kv_decode_plan with slice bounds that follow the measured workgroup
+ * times.  No counterpart in the reference; same callers as s8kv_decode_plan.
+ * The planned decode launches reading an adaptive plan record each
+ * workgroup's start and end time in the plan buffer, so `plan` is written by
+ * them (launches running at the same time just overwrite each other's
+ * times).  The next s8kv_decode_plan_adaptive call into the same buffer
+ * moves every workgroup column's share of the token stream a quarter of the
+ * way towards the share that equalizes finish times (at most 25% per step).
+ * It falls back to the fixed split when the buffer holds no earlier adaptive
+ * plan of this geometry, the stream length moved by more than a sixteenth,
+ * or some workgroup's times are missing.  Any buffer contents yield a valid
+ * split.  Cache bytes are the same as with the fixed split; outputs differ
+ * only by the rounding of combining rows split across workgroups.
+ */
+int s8kv_decode_plan_adaptive(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
+                              int64_t num_blocks, int block_size, const int32_t* block_table,
+                              int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                              void* plan, int64_t plan_bytes, void* stream);
+
+/*
  * s8kv_decode_append_int8 / s8kv_decode_append_k8v3 reading a plan made by
  * s8kv_decode_plan for the same geometry and the same block_table and
  * context_lens buffers, whose contents must not have changed since: the
@@ -205,7 +225,8 @@ int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim,
  * ignored (the launch locates its work itself).  plan_bytes: the plan
  * buffer's size, at least s8kv_decode_plan_size(num_kv_heads) (smaller:
  * S8KV_ERR_INVALID).  Replace the same reference calls as the unplanned
- * forms.
+ * forms.  A plan made by s8kv_decode_plan_adaptive is also written: each
+ * workgroup records its start and end time in it.
  */
 int s8kv_decode_append_int8_planned(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                     int64_t q_stride_b, int64_t q_stride_h, const void* k_new,

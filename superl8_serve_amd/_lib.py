@@ -88,6 +88,11 @@ SIGNATURES: dict[str, tuple] = {
         _i64, _i32, _c_void_p, _i64, _c_void_p, _i32,
         _c_void_p, _i64, _c_void_p,
     ]),
+    "s8kv_decode_plan_adaptive": (_i32, [
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64, _i32, _c_void_p, _i64, _c_void_p, _i32,
+        _c_void_p, _i64, _c_void_p,
+    ]),
     "s8kv_decode_k8v3": (_i32, [
         _c_void_p, _i32, _i32, _i32, _i32,
         _i64, _i64,

@@ -196,7 +196,10 @@ struct DecodeArgs {
   int window;
   // per-step slice plan (decode_plan_kernel; null: the prologue computes it)
   const int32_t* plan;
+  int plan_wmax;      // workgroup columns the plan buffer's layout is sized for (max_wg_per_head)
   int32_t* plan_out;  // host only: s8kv_decode_plan writes the plan here instead of decoding
+  int plan_adapt;     // host only: s8kv_decode_plan_adaptive (slice bounds from the launches' feedback)
+  float adapt_gain;   // decode_bounds_kernel: fraction of the way to the measured shares a step moves
   int untimed;  // host only: never stamp this launch with timing events
 #ifdef S8KV_DECODE_TRACE
   unsigned long long* trace;  // [grid][kTraceWords] per-workgroup records, or null
@@ -356,9 +359,21 @@ struct SliceLoc {
 };
 // Plan layout (int32 words): a header naming the launch geometry the plan was
 // made for, then one entry per workgroup column j.
-constexpr int kPlanHeader = 16;
+constexpr int kPlanHeader = 32;       // words before the entries (entries stay 64-byte aligned)
+constexpr int kPlanHeaderWords = 17;  // header words in use
 constexpr int kPlanEntry = 16;
 constexpr int kPlanMagic = 0x50384B53;
+constexpr int kPlanAdaptWord = 16;  // header word: 1 when the slice bounds come from the adaptive area
+// Adaptive plans (s8kv_decode_plan_adaptive) keep, after the entries, the
+// slice bounds they were made with and the launches' feedback: every
+// workgroup (column j, KV head h) of a launch reading the plan records its
+// run time and slice length there, tagged with the plan's epoch, and the
+// next step's plan moves the bounds towards equal run times.
+constexpr int kAdaptMagic = 0x41445053;
+enum AdaptWord { kAdMagic = 0, kAdWg, kAdHkv, kAdBatch, kAdEpoch, kAdTotal, kAdBounds = 8 };
+constexpr int kFbWords = 3;  // feedback entry (KV head h, column j): epoch, start and end (s_memrealtime, low words)
+__host__ __device__ inline int64_t plan_adapt_off(int wmax) { return kPlanHeader + (int64_t)kPlanEntry * wmax; }
+__host__ __device__ inline int64_t plan_fb_off(int wmax) { return plan_adapt_off(wmax) + kAdBounds + wmax + 1; }
 constexpr uint32_t kNoTile = 0xFFFFFFFFu;
 enum PlanWord {  // entry words
   kPwTotal = 0, kPwLo, kPwHi, kPwB, kPwPb, kPwL, kPwBFirst, kPwPbFirst, kPwLFirst, kPwBStop, kPwReordered,
@@ -401,23 +416,37 @@ __device__ __forceinline__ int find_segment(const DecodeArgs& a, const int* lens
   return 0;
 }
 
+// The head's stream length (every lane).
+template <bool WIN>
+__device__ __forceinline__ int stream_total(const DecodeArgs& a, const int* lens_lds, int lane) {
+  int total = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64)
+    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len<WIN>(a, lens_lds, c0, lane)), 63);
+  return __builtin_amdgcn_readfirstlane(total);
+}
+template <bool WIN>
+__device__ __forceinline__ bool slice_segments(const DecodeArgs& a, const int* lens_lds, int lane, SliceLoc& s);
 // Column j's slice and the segment it processes first, from the context
 // lengths in LDS (all lanes of a wave; the results are wave-uniform).
 // Returns false when the slice holds no segment.
 template <bool WIN>
 __device__ __forceinline__ bool locate_slice(const DecodeArgs& a, const int* lens_lds, int j, int lane, SliceLoc& s) {
-  // stream positions: prefix of the rows' stream lengths
-  const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
-  const int incl0 = wave_incl_scan(v0);  // rows 0..63
-  int total = __builtin_amdgcn_readlane(incl0, 63);
-  for (int c0 = 64; c0 < a.batch; c0 += 64)
-    total += __builtin_amdgcn_readlane(wave_incl_scan(row_stream_len<WIN>(a, lens_lds, c0, lane)), 63);
-  s.total = __builtin_amdgcn_readfirstlane(total);
+  s.total = stream_total<WIN>(a, lens_lds, lane);
   s.L = 0;
   const SliceLayout sl = slice_layout(s.total, a.wg_per_head, a.slot_classes, a.slot_skew, lane);
   s.lo = slice_start(sl, j);
   if (s.lo >= s.total) return false;
   s.hi = j + 1 >= a.wg_per_head ? s.total : min(s.total, slice_start(sl, j + 1));
+  return slice_segments<WIN>(a, lens_lds, lane, s);
+}
+// The first segment (and the segment order) of the slice [s.lo, s.hi) of a
+// stream of s.total tokens; false when the slice holds no segment.
+template <bool WIN>
+__device__ __forceinline__ bool slice_segments(const DecodeArgs& a, const int* lens_lds, int lane, SliceLoc& s) {
+  s.L = 0;
+  if (s.lo >= s.hi) return false;
+  const int v0 = row_stream_len<WIN>(a, lens_lds, 0, lane);
+  const int incl0 = wave_incl_scan(v0);  // rows 0..63
 
   // the row whose stream range holds position pos (< total), and the start of that range
   auto find_row = [&](int pos, int& rb, int& rpb) {
@@ -511,6 +540,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   int* bt_lds = reinterpret_cast<int*>(smem + a.smem_main);
   int* lens_lds = bt_lds + kMaxSubBlocks;
 
+  const uint32_t t_start = (uint32_t)__builtin_amdgcn_s_memrealtime();  // adaptive plans: this workgroup's start
   const int Hkv = a.num_kv_heads;
   const int h = blockIdx.x % Hkv;
   const int j = blockIdx.x / Hkv;
@@ -621,12 +651,26 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   bool pre_issued = false;  // this wave's first tile of the first segment is in flight
   uint32_t pre_r0 = kNoTile;  // ... from this storage row
   bool planned = false;
+  bool adapt = false;  // the plan's slices come from its adaptive bounds: record this workgroup's times
+  int epoch = 0;
   if (a.plan != nullptr) {
     const int32_t* hd = a.plan;
     planned = true;
 #pragma unroll
-    for (int i = 0; i < kPlanHeader; ++i) planned = planned && (i == kPlanLensWord || hd[i] == plan_header_word(a, i));
+    for (int i = 0; i < kPlanHeaderWords; ++i)
+      planned = planned && (i == kPlanLensWord || i == kPlanAdaptWord || hd[i] == plan_header_word(a, i));
+    adapt = planned && hd[kPlanAdaptWord] == 1;
+    if (adapt) epoch = a.plan[plan_adapt_off(a.plan_wmax) + kAdEpoch];
   }
+  // the workgroup's times, tagged with the plan's epoch (thread 0, at the workgroup's end)
+  auto record_times = [&]() {
+    if (adapt && tid == 0) {
+      int32_t* f = const_cast<int32_t*>(a.plan) + plan_fb_off(a.plan_wmax) + ((int64_t)h * a.plan_wmax + j) * kFbWords;
+      f[0] = epoch;
+      f[1] = (int32_t)t_start;
+      f[2] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+    }
+  };
   if (planned) {
     const int32_t* e = a.plan + kPlanHeader + (int64_t)j * kPlanEntry;
     sl.total = e[kPwTotal];
@@ -659,6 +703,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   // a plan made from other lengths (the buffer rewritten in place since) is
   // ignored; a first tile issued from it is issued again below when its row differs
   if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != a.plan[kPlanLensWord]) planned = false;
+  adapt = adapt && planned;
   bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
   if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
@@ -671,7 +716,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       }
     }
   }
-  if (!has_seg) return;
+  if (!has_seg) {
+    record_times();
+    return;
+  }
   const int total = sl.total, lo = sl.lo, hi = sl.hi;
 
   // K8V3 codebook byte tables (fp16 of the fp32 codebook).
@@ -1322,10 +1370,30 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         // slices jf..jl hold the row's segments; their partials are at slots j + b
         // (recomputed here from opaque copies of its inputs, so that no part of
         // it is hoisted from the prologue and kept live across the tile loop)
-        const SliceLayout sm = slice_layout(opaque_int(total), opaque_int(a.wg_per_head), opaque_int(a.slot_classes),
-                                            opaque_int(a.slot_skew), opaque_int(threadIdx.x) & 63);
-        const int jf = slice_of(sm, rs);
-        const int jl = slice_of(sm, rs + padL - 1);
+        int jf, jl;
+        if (adapt) {  // the largest columns whose bounds are at or before the row's first and last tokens
+          const int32_t* bd = a.plan + plan_adapt_off(a.plan_wmax) + kAdBounds;
+          const int ln = opaque_int(threadIdx.x) & 63, W = a.wg_per_head;
+          int nf = 0, nl = 0;
+          for (int c0 = 0; c0 < W; c0 += 256) {  // four loads in flight
+            int v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = c0 + 64 * u + ln < W ? bd[c0 + 64 * u + ln] : 0x7FFFFFFF;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              nf += __builtin_popcountll(__builtin_amdgcn_ballot_w64(v[u] <= rs));
+              nl += __builtin_popcountll(__builtin_amdgcn_ballot_w64(v[u] <= rs + padL - 1));
+            }
+          }
+          jf = nf - 1;
+          jl = nl - 1;
+        } else {
+          const SliceLayout sm = slice_layout(opaque_int(total), opaque_int(a.wg_per_head),
+                                              opaque_int(a.slot_classes), opaque_int(a.slot_skew),
+                                              opaque_int(threadIdx.x) & 63);
+          jf = slice_of(sm, rs);
+          jl = slice_of(sm, rs + padL - 1);
+        }
         for (int i = tid; i < G * D; i += 64 * kDecWaves) {
           const int cc = i / D, d = i - cc * D;
           float M = kNegInf, num = 0.0f, den = 0.0f;
@@ -1363,6 +1431,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     pb = npb;
     L = nL;
   }
+  if (adapt) {  // (workgroup-uniform) the end: when the last wave is done
+    __syncthreads();
+    record_times();
+  }
 #ifdef S8KV_DECODE_TRACE
   S8KV_TRACE_STAMP(kTrExit);
   S8KV_TRACE_SET(kTrWork, tr_tok | (tr_seg << 32));
@@ -1373,12 +1445,160 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 #endif
 }
 
+// ---- adaptive slice bounds ----
+// Wave sums and prefix sums of floats (ds_swizzle / DPP-free shuffles; the
+// bounds kernel is one wave and runs once per step).
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_incl_scan_f(float v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float t = __shfl_up(v, off, 64);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+// slice_start for a per-lane column j (0 <= j < W).
+__device__ __forceinline__ int slice_start_lane(const SliceLayout& s, int j) {
+  int r = 0;
+#pragma unroll
+  for (int c = 0; c < kMaxResidentPerCU; ++c) {
+    const int f0 = __builtin_amdgcn_readlane(s.f0, c), f1 = __builtin_amdgcn_readlane(s.f1, c);
+    if (f0 <= j && j < f1) r = __builtin_amdgcn_readlane(s.start, c) + (j - f0) * __builtin_amdgcn_readlane(s.sz, c);
+  }
+  return r;
+}
+
+// Slice bounds of an adaptive plan, bd[0..W] (one wave).  When the plan
+// buffer holds this geometry's bounds, its stream total moved by at most a
+// sixteenth, and every workgroup of the last launch that read the plan
+// recorded its times under the plan's epoch, each column's share of the
+// stream moves a fraction kAdaptGain (S8KV_DECODE_ADAPT_GAIN overrides it)
+// of the way from its last share towards the share its measured rate earns
+// -- slice length over finish time, the end stamp minus the launch's
+// earliest start, summed over the KV heads -- changing by at most kAdaptStep
+// of itself and staying at or above kAdaptFloor of an even share (where a
+// column the formula left past the stream's end starts from).  At the fixed
+// point every column finishes at the same time.  Otherwise the bounds are
+// the formula's (those of the unplanned slicing).  Bounds are multiples of
+// 32 (the last one is the stream total), non-decreasing, with bd[0] = 0; the
+// epoch advances by one.
+constexpr int kAdaptMaxCols = 2048;
+constexpr float kAdaptGain = 0.25f;
+constexpr float kAdaptStep = 0.25f;
+constexpr float kAdaptFloor = 0.25f;
+constexpr int kAdaptMinTokens = 128;  // stream tokens per column below which the formula is kept
+template <bool WIN>
+__global__ __launch_bounds__(64) void decode_bounds_kernel(DecodeArgs a) {
+  __shared__ int lens_lds[kLensLds];
+  __shared__ float len_lds[kAdaptMaxCols];
+  __shared__ float rate_lds[kAdaptMaxCols];
+  const int lane = threadIdx.x;
+  for (int i = lane; i < min(a.batch, kLensLds); i += 64) lens_lds[i] = a.context_lens[i];
+  __syncthreads();
+  int32_t* ad = a.plan_out + plan_adapt_off(a.plan_wmax);
+  int32_t* bd = ad + kAdBounds;
+  const int32_t* fb = a.plan_out + plan_fb_off(a.plan_wmax);
+  const int W = a.wg_per_head, Hkv = a.num_kv_heads;
+  const int total = stream_total<WIN>(a, lens_lds, lane);
+  const bool known = ad[kAdMagic] == kAdaptMagic;
+  const int epoch = ad[kAdEpoch];
+  const int64_t old_total = ad[kAdTotal];
+  bool ok = known && ad[kAdWg] == W && ad[kAdHkv] == Hkv && ad[kAdBatch] == a.batch && W <= kAdaptMaxCols &&
+            W <= a.plan_wmax && (int64_t)total >= (int64_t)kAdaptMinTokens * W && old_total > 0 &&
+            16 * (int64_t)abs(total - (int)old_total) <= old_total && bd[0] == 0 && bd[W] == (int)old_total;
+  // every entry is the last launch's; its earliest start, relative to entry (0, 0)'s
+  const uint32_t ref = ok ? (uint32_t)fb[1] : 0u;
+  int dmin = 0;
+  if (ok) {
+    bool mine = true;
+    for (int i = lane; i < W * Hkv; i += 64) {
+      const int hh = i / W, jj = i - hh * W;
+      const int32_t* f = fb + ((int64_t)hh * a.plan_wmax + jj) * kFbWords;
+      mine = mine && f[0] == epoch;
+      dmin = min(dmin, (int)((uint32_t)f[1] - ref));
+    }
+    ok = __builtin_amdgcn_ballot_w64(!mine) == 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) dmin = min(dmin, __shfl_xor(dmin, off, 64));
+  }
+  // each column's last slice length and rate
+  float sum_len = 0.0f, sum_rate = 0.0f;
+  if (ok) {
+    bool sane = true;
+    for (int c0 = 0; c0 < W; c0 += 64) {
+      const int jj = c0 + lane;
+      float len = 0.0f, rate = 0.0f;
+      if (jj < W) {
+        const int lo = bd[jj], hi = bd[jj + 1];
+        float t = 0.0f;
+        for (int hh = 0; hh < Hkv; ++hh) {
+          const int32_t* f = fb + ((int64_t)hh * a.plan_wmax + jj) * kFbWords;
+          t += (float)((int)((uint32_t)f[2] - ref) - dmin);
+        }
+        sane = sane && hi >= lo && (hi == lo || t > 0.0f);
+        len = (float)(hi - lo);
+        rate = hi > lo ? len / t : 0.0f;  // a column past the stream's end: rate 0 (it gets the floor share)
+        len_lds[jj] = len;
+        rate_lds[jj] = rate;
+      }
+      sum_len += wave_sum_f(len);
+      sum_rate += wave_sum_f(rate);
+    }
+    ok = __builtin_amdgcn_ballot_w64(!sane) == 0 && sum_len > 0.0f && sum_rate > 0.0f;
+  }
+  if (ok) {
+    // the new shares (in len_lds), then their prefix sums scaled to the stream
+    const float floor_share = kAdaptFloor / (float)W;
+    float sum_new = 0.0f;
+    for (int c0 = 0; c0 < W; c0 += 64) {
+      const int jj = c0 + lane;
+      float f = 0.0f;
+      if (jj < W) {
+        const float fo = len_lds[jj] / sum_len, ft = rate_lds[jj] / sum_rate;
+        f = fo + a.adapt_gain * (ft - fo);
+        f = fminf(fmaxf(f, fo * (1.0f - kAdaptStep)), fo * (1.0f + kAdaptStep));
+        f = fmaxf(f, floor_share);
+        len_lds[jj] = f;
+      }
+      sum_new += wave_sum_f(f);
+    }
+    const float units = (float)(total >> 5) / sum_new;
+    float carry = 0.0f;
+    for (int c0 = 0; c0 < W; c0 += 64) {
+      const int jj = c0 + lane;
+      const float incl = wave_incl_scan_f(jj < W ? len_lds[jj] : 0.0f, lane) + carry;
+      if (jj + 1 < W) bd[jj + 1] = min(total, 32 * (int)rintf(incl * units));
+      carry = __shfl(incl, 63, 64);
+    }
+  } else {
+    const SliceLayout sl = slice_layout(total, W, a.slot_classes, a.slot_skew, lane);
+    for (int c0 = 1; c0 < W; c0 += 64) {
+      const int jj = c0 + lane;
+      if (jj < W) bd[jj] = min(total, slice_start_lane(sl, jj));
+    }
+  }
+  if (lane == 0) {
+    bd[0] = 0;
+    bd[W] = total;
+    ad[kAdMagic] = kAdaptMagic;
+    ad[kAdWg] = W;
+    ad[kAdHkv] = Hkv;
+    ad[kAdBatch] = a.batch;
+    ad[kAdEpoch] = known ? epoch + 1 : 1;
+    ad[kAdTotal] = total;
+  }
+}
+
 // The step's slice plan: one wave per workgroup column j, the decode
 // prologue's arithmetic on the same lengths (locate_slice), plus the storage
 // row (KV head 0) of each wave's first tile in the segment processed first --
 // tile s0 + 32 w of the segment's first sub-split, when it exists and the
 // block size keeps a tile inside one block.  Block 0 also writes the header.
-template <bool WIN>
+template <bool WIN, bool ADAPT = false>
 __global__ __launch_bounds__(64 * kDecWaves) void decode_plan_kernel(DecodeArgs a) {
   __shared__ int lens_lds[kLensLds];
   const int tid = threadIdx.x;
@@ -1387,7 +1607,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_plan_kernel(DecodeArgs 
   const int j = blockIdx.x * kDecWaves + wave;
   int32_t* plan = a.plan_out;
   for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
-  if (blockIdx.x == 0 && tid < kPlanHeader && tid != kPlanLensWord) plan[tid] = plan_header_word(a, tid);
+  if (blockIdx.x == 0 && tid < kPlanHeader && tid != kPlanLensWord)
+    plan[tid] = tid == kPlanAdaptWord ? (ADAPT ? 1 : 0) : plan_header_word(a, tid);
   __syncthreads();
   if (blockIdx.x == 0 && wave == 0) {
     const uint32_t cs = lens_checksum(a, lens_lds, lane);
@@ -1395,7 +1616,17 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_plan_kernel(DecodeArgs 
   }
   if (j >= a.wg_per_head) return;
   SliceLoc s;
-  if (!locate_slice<WIN>(a, lens_lds, j, lane, s)) {  // no segment: the launch's workgroup j returns at once
+  bool found;
+  if constexpr (ADAPT) {  // the slice bounds decode_bounds_kernel wrote for this step
+    const int32_t* bd = plan + plan_adapt_off(a.plan_wmax) + kAdBounds;
+    s.total = stream_total<WIN>(a, lens_lds, lane);
+    s.lo = min(bd[j], s.total);
+    s.hi = min(bd[j + 1], s.total);
+    found = slice_segments<WIN>(a, lens_lds, lane, s);
+  } else {
+    found = locate_slice<WIN>(a, lens_lds, j, lane, s);
+  }
+  if (!found) {  // no segment: the launch's workgroup j returns at once
     if (s.lo >= s.total) s.lo = s.hi = s.total;
     s.L = 0;
     s.b = s.pb = s.b_first = s.pb_first = s.L_first = s.reordered = 0;
@@ -1555,8 +1786,22 @@ static int launch_decode_impl(DecodeArgs& a, hipStream_t stream) {
   a.slots = a.batch + a.wg_per_head;
   if (a.plan_out != nullptr) {  // s8kv_decode_plan: the slice plan of this launch geometry
     const dim3 pgrid((a.wg_per_head + kDecWaves - 1) / kDecWaves);
-    hipLaunchKernelGGL((decode_plan_kernel<WIN>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
-    return check_launch("s8kv_decode_plan");
+    if (a.plan_adapt) {
+      if (a.wg_per_head > kAdaptMaxCols) {
+        set_error("s8kv_decode_plan_adaptive: %d workgroups per KV head > %d", a.wg_per_head, kAdaptMaxCols);
+        return S8KV_ERR_UNSUPPORTED;
+      }
+      a.adapt_gain = kAdaptGain;
+      if (const char* env = getenv("S8KV_DECODE_ADAPT_GAIN")) {
+        const float g = (float)atof(env);
+        a.adapt_gain = g < 0.0f ? 0.0f : (g > 1.0f ? 1.0f : g);
+      }
+      hipLaunchKernelGGL((decode_bounds_kernel<WIN>), dim3(1), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL((decode_plan_kernel<WIN, true>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((decode_plan_kernel<WIN>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
+    }
+    return check_launch(a.plan_adapt ? "s8kv_decode_plan_adaptive" : "s8kv_decode_plan");
   }
   const dim3 grid(a.wg_per_head * a.num_kv_heads);
 #ifdef S8KV_DECODE_TRACE
@@ -1588,8 +1833,11 @@ static int64_t workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int
 }
 // Slice plan: header + one entry per workgroup column, for the largest grid
 // a launch of this geometry may use.
+// Adaptive plans also hold the slice bounds and one feedback entry per
+// (KV head, column).
 static int64_t plan_bytes_for(int num_kv_heads) {
-  return (int64_t)(kPlanHeader + kPlanEntry * max_wg_per_head(num_kv_heads)) * 4;
+  const int w = max_wg_per_head(num_kv_heads);
+  return (plan_fb_off(w) + (int64_t)kFbWords * num_kv_heads * w) * 4;
 }
 
 
@@ -1639,6 +1887,7 @@ static int decode_common(DecodeArgs& a, bool k8v3, bool fuse, int batch, int num
   a.vs_bytes = cap_u32(a.vs_total);
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
+  a.plan_wmax = max_wg_per_head(num_kv_heads);
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.rot_norm = (float)(1.0 / __builtin_sqrt((double)head_dim));
   if (plan_only) {
@@ -1974,10 +2223,10 @@ extern "C" int64_t s8kv_decode_plan_size(int num_kv_heads) {
   return num_kv_heads > 0 ? plan_bytes_for(num_kv_heads) : 0;
 }
 
-extern "C" int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
-                                int64_t num_blocks, int block_size, const int32_t* block_table,
-                                int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
-                                void* plan, int64_t plan_bytes_given, void* stream) {
+static int decode_plan_common(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
+                              int64_t num_blocks, int block_size, const int32_t* block_table,
+                              int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                              void* plan, int64_t plan_bytes_given, void* stream, bool adaptive) {
   S8KV_REQUIRE(layout == 0 || layout == 1, S8KV_ERR_INVALID, "decode_plan: layout %d is neither 0 (int8) nor 1 (k8v3)",
                layout);
   S8KV_REQUIRE(plan != nullptr, S8KV_ERR_INVALID, "decode_plan: null plan");
@@ -1986,9 +2235,26 @@ extern "C" int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, in
   a.bt_stride = block_table_stride;
   a.context_lens = context_lens;
   a.plan_out = static_cast<int32_t*>(plan);
+  a.plan_adapt = adaptive ? 1 : 0;
   a.untimed = 1;
   return decode_common(a, layout == 1, fused != 0, batch, num_q_heads, num_kv_heads, head_dim, num_blocks, block_size,
                        max_context_len, 1.0f, plan, plan_bytes_given, stream);
+}
+extern "C" int s8kv_decode_plan(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout, int fused,
+                                int64_t num_blocks, int block_size, const int32_t* block_table,
+                                int64_t block_table_stride, const int32_t* context_lens, int max_context_len,
+                                void* plan, int64_t plan_bytes_given, void* stream) {
+  return decode_plan_common(batch, num_q_heads, num_kv_heads, head_dim, layout, fused, num_blocks, block_size,
+                            block_table, block_table_stride, context_lens, max_context_len, plan, plan_bytes_given,
+                            stream, false);
+}
+extern "C" int s8kv_decode_plan_adaptive(int batch, int num_q_heads, int num_kv_heads, int head_dim, int layout,
+                                         int fused, int64_t num_blocks, int block_size, const int32_t* block_table,
+                                         int64_t block_table_stride, const int32_t* context_lens,
+                                         int max_context_len, void* plan, int64_t plan_bytes_given, void* stream) {
+  return decode_plan_common(batch, num_q_heads, num_kv_heads, head_dim, layout, fused, num_blocks, block_size,
+                            block_table, block_table_stride, context_lens, max_context_len, plan, plan_bytes_given,
+                            stream, true);
 }
 
 extern "C" int s8kv_decode_k8v3(const void* q, int batch, int num_q_heads, int num_kv_heads, int head_dim,

@@ -256,7 +256,7 @@ def attn_paged_decode_window(q, k_cache, k_scale, v_cache, v_scale, block_table,
 
 
 def attn_paged_decode_plan(k_cache, block_table, context_lens, block_size, *, num_q_heads, max_context_len,
-                           layout: str = "int8", fused: bool = True):
+                           layout: str = "int8", fused: bool = True, adaptive: bool = False, plan=None):
     """Slice plan of one decode step, shared by its per-layer launches.
 
     Every layer of a step decodes the same rows: the same ``block_table`` and
@@ -266,7 +266,18 @@ def attn_paged_decode_plan(k_cache, block_table, context_lens, block_size, *, nu
     ``attn_paged_decode_append(..., plan=)`` / ``attn_paged_decode_append_k8v3(
     ..., plan=)`` read it instead of recomputing it.  ``k_cache`` is any
     layer's cache (geometry only); ``layout`` "int8" or "k8v3"; ``fused``
-    the one-launch step ops.  Capturable (no host synchronization)."""
+    the one-launch step ops.  Capturable (no host synchronization).
+
+    ``adaptive``: the split follows the last step's measured workgroup times
+    instead of the fixed formula.  The launches reading the plan record each
+    workgroup's start and end in it; the next adaptive plan made into the
+    same tensor (pass it back as ``plan``) moves the slice bounds a quarter
+    of the way towards equal finish times, falling back to the formula when the
+    geometry changed, the lengths moved by more than a sixteenth, or the
+    times are missing.  Same cache bytes as the fixed split; outputs differ
+    from it only by the rounding of the split rows' combine.  ``plan``: a
+    tensor from an earlier call to write into (reused as is), else a new one
+    (zeroed when adaptive)."""
     dev = k_cache.device
     _on_gpu("k_cache", k_cache, torch.int8, dev)
     _on_gpu("block_table", block_table, torch.int32, dev)
@@ -281,10 +292,17 @@ def attn_paged_decode_plan(k_cache, block_table, context_lens, block_size, *, nu
              f"context_lens must be a contiguous [{b}] tensor")
     lib = _lib.load()
     nbytes = int(lib.s8kv_decode_plan_size(hkv))
-    plan = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
-    rc = lib.s8kv_decode_plan(b, int(num_q_heads), hkv, d, 1 if layout == "k8v3" else 0, 1 if fused else 0, n, bs,
-                              block_table.data_ptr(), block_table.stride(0), context_lens.data_ptr(),
-                              int(max_context_len), plan.data_ptr(), nbytes, _stream(k_cache))
+    if plan is None:
+        plan = (torch.zeros if adaptive else torch.empty)(nbytes // 4, dtype=torch.int32, device=dev)
+    else:
+        _on_gpu("plan", plan, torch.int32, dev)
+        _require(plan.is_contiguous() and plan.numel() * 4 >= nbytes,
+                 f"plan must be a contiguous int32 tensor of at least {nbytes // 4} elements")
+        nbytes = plan.numel() * 4
+    entry = lib.s8kv_decode_plan_adaptive if adaptive else lib.s8kv_decode_plan
+    rc = entry(b, int(num_q_heads), hkv, d, 1 if layout == "k8v3" else 0, 1 if fused else 0, n, bs,
+               block_table.data_ptr(), block_table.stride(0), context_lens.data_ptr(), int(max_context_len),
+               plan.data_ptr(), nbytes, _stream(k_cache))
     _lib.check(rc, "attn_paged_decode_plan")
     return plan
 

@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 CODEBOOK = O.gaussian_codebook(3, 128)
-HEADER, ENTRY = 16, 16  # plan words: header, then one entry per workgroup column
+HEADER, ENTRY = 32, 16  # plan words: header, then one entry per workgroup column
 
 
 def _t(x):
@@ -279,6 +279,121 @@ def test_host_cache_decode_step_with_plan(v_quant):
              else ("k_cache", "k_scale", "v_packed", "v_norm"))
     for name in names:
         assert torch.equal(getattr(caches[0], name), getattr(caches[1], name)), name
+
+
+# ---- adaptive plans (attn_paged_decode_plan(adaptive=True)) ----
+AD_MAGIC, AD_BOUNDS = 0x41445053, 8  # adaptive area: magic, W, Hkv, batch, epoch, total, -, -, bounds[W + 1]
+
+
+def _adaptive_area(plan, hkv):
+    """(words of the adaptive area, its bounds, the feedback [hkv, w, 3]:
+    epoch, start, end) of a plan tensor."""
+    p = _np(plan).astype(np.int64)
+    w = int(p[3])
+    # header, wmax entries, the adaptive words and wmax + 1 bounds, 3 feedback words per (head, column)
+    wmax = (len(p) - HEADER - AD_BOUNDS - 1) // (ENTRY + 1 + 3 * hkv)
+    assert HEADER + ENTRY * wmax + AD_BOUNDS + wmax + 1 + 3 * hkv * wmax == len(p)
+    ad = p[HEADER + ENTRY * wmax:]
+    fb = ad[AD_BOUNDS + wmax + 1:].reshape(hkv, wmax, 3)[:, :w]
+    return ad, ad[AD_BOUNDS: AD_BOUNDS + w + 1], fb
+
+
+def _check_close(a, b, what):
+    """Same cache bytes; outputs within the attention tolerance."""
+    from tests.kvgpu import assert_close
+
+    out_a, cache_a = a
+    out_b, cache_b = b
+    for x, y, name in zip(cache_a, cache_b, ("k_cache", "k_scale", "v", "v_scale")):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"{what}: {name} differs"
+    assert_close(out_a, out_b, what)
+
+
+def _qwen_like_case(seed, batch, layout="int8"):
+    lens = np.random.default_rng(seed).integers(1500, 5000, size=batch).tolist()
+    return _Step(make_case(seed, batch, 32, 8, 128, 256, lens, outlier_channels=2), layout)
+
+
+@pytest.mark.parametrize("layout", ["int8", "k8v3"])
+def test_adaptive_plan_steps(layout):
+    """Steps with one adaptive plan tensor: the first plan (zeroed buffer) is
+    the fixed split, bit for bit; later ones move the bounds (multiples of 32,
+    from 0 to the stream total) and keep the cache bytes, with outputs within
+    the attention tolerance of the fixed split's."""
+    step = _qwen_like_case(5150, 24, layout)
+    ref = step.run(None)
+    fixed = _np(step.plan()).astype(np.int64)
+    plan = step.plan(adaptive=True)
+    ad, bd, _ = _adaptive_area(plan, 8)
+    w = int(fixed[3])
+    ent = fixed[HEADER: HEADER + ENTRY * w].reshape(w, ENTRY)
+    total = int(ent[0, 0])
+    assert ad[0] == AD_MAGIC and ad[4] == 1 and ad[5] == total
+    assert (np.minimum(ent[:, 1], total) == bd[:w]).all() and bd[w] == total, "first adaptive plan: the fixed split"
+    _same(step.run(plan), ref, f"{layout} first adaptive step")
+    moved = False
+    for k in range(2, 8):
+        fb = _adaptive_area(plan, 8)[2]
+        assert (fb[:, :, 0] == k - 1).all(), "every workgroup of the last launch recorded its times"
+        step.plan(adaptive=True, plan=plan)
+        ad, bd, _ = _adaptive_area(plan, 8)
+        assert ad[4] == k, "epoch"
+        assert bd[0] == 0 and bd[w] == total and (np.diff(bd) >= 0).all() and (bd % 32 == 0).all()
+        moved = moved or not (np.minimum(ent[:, 1], total) == bd[:w]).all()
+        _check_close(step.run(plan), ref, f"{layout} adaptive step {k}")
+    assert moved, f"the bounds never left the fixed split (adaptive words {ad[:8].tolist()})"
+
+
+def test_adaptive_plan_falls_back_on_new_lengths():
+    """After the lengths are rewritten in place (the stream total moves by
+    more than a sixteenth), the next adaptive plan is the fixed split again:
+    bit-identical outputs to the unplanned launch on the new lengths."""
+    rng = np.random.default_rng(31)
+    step = _qwen_like_case(5252, 24)
+    plan = step.plan(adaptive=True)
+    for _ in range(4):
+        step.run(plan)
+        step.plan(adaptive=True, plan=plan)
+    new_lens = (step.case.lens // 2 + rng.integers(1, 200, size=24)).astype(np.int32)
+    step.cl.copy_(_t(new_lens))
+    step.plan(adaptive=True, plan=plan)
+    _same(step.run(plan), step.run(None), "adaptive plan after a length rewrite")
+
+
+def test_adaptive_plan_graph_replays():
+    """The adaptive plan launch and three layers' planned decode launches in
+    one graph, replayed: the bounds adapt from replay to replay, every replay
+    keeps the cache bytes and stays within tolerance of the eager outputs."""
+    step = _qwen_like_case(5353, 24)
+    eager = step.run(None)
+    caches = [[_t(x) for x in step.pre] for _ in range(3)]
+    c = step.case
+    plan = step.plan(adaptive=True)
+
+    def body():
+        ops.attn_paged_decode_plan(caches[0][0], step.bt, step.cl, c.block_size, num_q_heads=c.num_q_heads,
+                                   max_context_len=step.max_ctx, adaptive=True, plan=plan)
+        return [ops.attn_paged_decode_append(step.q, step.kn, step.vn, *cache, step.bt, step.cl, c.block_size,
+                                             max_context_len=step.max_ctx, scale=c.scale, plan=plan)
+                for cache in caches]
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = body()
+    epochs = []
+    for _ in range(4):
+        torch.zeros(1 << 20, device=DEV).add_(1.0)  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        epochs.append(int(_adaptive_area(plan, 8)[0][4]))
+        for out, cache in zip(outs, caches):
+            _check_close((_np(out.float()), [_np(x) for x in cache]), eager, "adaptive graph replay")
+    assert epochs == list(range(epochs[0], epochs[0] + 4))
 
 
 def test_plan_smaller_than_the_geometry_needs_is_rejected():
