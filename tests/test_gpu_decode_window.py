@@ -208,8 +208,19 @@ def test_window_tree_verify():
 
 
 def test_window_verify_covering_the_prefix_equals_verify():
+    """A window covering every row's prefix masks nothing.  The windowed call
+    runs the 16-row verify kernel and the unwindowed head_dim-128 paged call
+    the 32-row one, whose sums round differently: equal within the attention
+    tolerance (a masking error would be far outside it), and both match the
+    oracle."""
+    from tests.kvgpu import assert_close
+
     case, cache, q, pre = _verify_case(621, 3, 8, 2, 128, 16, [300, 37, 256], 7)
-    assert np.array_equal(_verify(case, cache, q, pre, 300), _verify(case, cache, q, pre, None))
+    windowed, plain = _verify(case, cache, q, pre, 300), _verify(case, cache, q, pre, None)
+    assert_close(windowed, plain, "window covering the prefix vs no window")
+    ref = _verify_ref(case, cache, q, pre, None)
+    assert_close(windowed, ref, "windowed vs oracle")
+    assert_close(plain, ref, "unwindowed vs oracle")
 
 
 def test_window_verify_ignores_keys_before_the_window():
