@@ -375,6 +375,15 @@ constexpr int kFbWords = 3;  // feedback entry (KV head h, column j): epoch, sta
 __host__ __device__ inline int64_t plan_adapt_off(int wmax) { return kPlanHeader + (int64_t)kPlanEntry * wmax; }
 __host__ __device__ inline int64_t plan_fb_off(int wmax) { return plan_adapt_off(wmax) + kAdBounds + wmax + 1; }
 constexpr uint32_t kNoTile = 0xFFFFFFFFu;
+// Word i of a plan, read through the constant address space so that a
+// wave-uniform index becomes a scalar load: the decode prologue's header,
+// entry and epoch reads are then issued together instead of as a chain of
+// vector loads each waited on before the next (the decode launch writes only
+// the plan's feedback words, which it never reads).
+using plan_word_t = const __attribute__((address_space(4))) int32_t;
+__device__ __forceinline__ int32_t plan_word(const int32_t* plan, int64_t i) {
+  return ((plan_word_t*)plan)[i];  // (an address-space cast: C-style)
+}
 enum PlanWord {  // entry words
   kPwTotal = 0, kPwLo, kPwHi, kPwB, kPwPb, kPwL, kPwBFirst, kPwPbFirst, kPwLFirst, kPwBStop, kPwReordered,
   kPwTile0 = 12,  // kPwTile0 + w: wave w's first tile row at KV head 0, or kNoTile
@@ -646,94 +655,6 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     }
   };
 
-  // ---- the slice and its first segment: from the step's plan, or located here ----
-  SliceLoc sl;
-  bool pre_issued = false;  // this wave's first tile of the first segment is in flight
-  uint32_t pre_r0 = kNoTile;  // ... from this storage row
-  bool planned = false;
-  bool adapt = false;  // the plan's slices come from its adaptive bounds: record this workgroup's times
-  int epoch = 0;
-  if (a.plan != nullptr) {
-    const int32_t* hd = a.plan;
-    planned = true;
-#pragma unroll
-    for (int i = 0; i < kPlanHeaderWords; ++i)
-      planned = planned && (i == kPlanLensWord || i == kPlanAdaptWord || hd[i] == plan_header_word(a, i));
-    adapt = planned && hd[kPlanAdaptWord] == 1;
-    if (adapt) epoch = a.plan[plan_adapt_off(a.plan_wmax) + kAdEpoch];
-  }
-  // the workgroup's times, tagged with the plan's epoch (thread 0, at the workgroup's end)
-  auto record_times = [&]() {
-    if (adapt && tid == 0) {
-      int32_t* f = const_cast<int32_t*>(a.plan) + plan_fb_off(a.plan_wmax) + ((int64_t)h * a.plan_wmax + j) * kFbWords;
-      f[0] = epoch;
-      f[1] = (int32_t)t_start;
-      f[2] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
-    }
-  };
-  if (planned) {
-    const int32_t* e = a.plan + kPlanHeader + (int64_t)j * kPlanEntry;
-    sl.total = e[kPwTotal];
-    sl.lo = e[kPwLo];
-    sl.hi = e[kPwHi];
-    sl.b = e[kPwB];
-    sl.pb = e[kPwPb];
-    sl.L = e[kPwL];
-    sl.b_first = e[kPwBFirst];
-    sl.pb_first = e[kPwPbFirst];
-    sl.L_first = e[kPwLFirst];
-    sl.b_stop = e[kPwBStop];
-    sl.reordered = e[kPwReordered];
-    const uint32_t r0 = (uint32_t)e[kPwTile0 + wave];
-    // (rows outside the batch would index outputs and partials out of range)
-    if (sl.L > 0 && !(sl.b >= 0 && sl.b < a.batch && sl.b_first >= 0 && sl.b_first < a.batch && sl.b_stop >= 0 &&
-                      sl.b_stop <= a.batch))
-      planned = false;
-    else if (sl.L > 0 && r0 != kNoTile && tile_in_block) {
-      tile_kv_at(r0 + ((uint32_t)h << bs_log2), lane);
-      tile_scales_at(r0 + ((uint32_t)h << bs_log2), lane);
-      pre_issued = true;
-      pre_r0 = r0 + ((uint32_t)h << bs_log2);
-    }
-  }
-  // context lengths -> LDS (one global round trip for the whole prologue)
-  for (int i = tid; i < min(a.batch, kLensLds); i += 64 * kDecWaves) lens_lds[i] = a.context_lens[i];
-  __syncthreads();
-  S8KV_TRACE_STAMP(kTrLens);
-  // a plan made from other lengths (the buffer rewritten in place since) is
-  // ignored; a first tile issued from it is issued again below when its row differs
-  if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != a.plan[kPlanLensWord]) planned = false;
-  adapt = adapt && planned;
-  bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
-  if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
-    for (int c0 = 0; c0 < a.batch; c0 += 64) {
-      uint64_t m = __builtin_amdgcn_ballot_w64(c0 + lane < a.batch && lens_at(a, lens_lds, c0 + lane) == 0);
-      while (m != 0) {
-        const int b = c0 + (int)__builtin_ctzll(m);
-        m &= m - 1;
-        for (int i = tid; i < G * D; i += 64 * kDecWaves)
-          a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
-      }
-    }
-  }
-  if (!has_seg) {
-    record_times();
-    return;
-  }
-  const int total = sl.total, lo = sl.lo, hi = sl.hi;
-
-  // K8V3 codebook byte tables (fp16 of the fp32 codebook).
-  uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
-  if constexpr (K8V3) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
-      const uint32_t lw = hb & 0xFFu, hw = hb >> 8;
-      if (i < 4) { tlo03 |= lw << (8 * i); thi03 |= hw << (8 * i); }
-      else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
-    }
-  }
-
   // Set-up loads of a segment that starts at token 0 of row rb (or at s0 for
   // the slice's first row): the lane's raw q fragment and the first
   // sub-split's block ids, issued early so their latency overlaps other work.
@@ -782,12 +703,130 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     }
   };
 
+  // context lengths, loaded first so that they return ahead of the set-up and
+  // tile loads issued below (one global round trip for the whole prologue)
+  constexpr int kLensRegs = kLensLds / (64 * kDecWaves);
+  const int n_lens = min(a.batch, kLensLds);
+  int lens_r[kLensRegs];
+#pragma unroll
+  for (int k = 0; k < kLensRegs; ++k) {
+    const int i = tid + k * 64 * kDecWaves;
+    lens_r[k] = i < n_lens ? a.context_lens[i] : 0;
+  }
+
+  // ---- the slice and its first segment: from the step's plan, or located here ----
+  SliceLoc sl;
+  bool early_setup = false;  // the planned first segment's set-up loads are in flight
+  bool pre_issued = false;  // this wave's first tile of the first segment is in flight
+  uint32_t pre_r0 = kNoTile;  // ... from this storage row
+  bool planned = false;
+  bool adapt = false;  // the plan's slices come from its adaptive bounds: record this workgroup's times
+  int epoch = 0;
+  int32_t ew[kPlanEntry];  // this column's plan entry
+  if (a.plan != nullptr) {
+    // every plan word the prologue reads, loaded together (the host checked
+    // that the buffer holds the whole layout): no chain of dependent loads
+    planned = true;
+#pragma unroll
+    for (int i = 0; i < kPlanHeaderWords; ++i)
+      planned &= i == kPlanLensWord || i == kPlanAdaptWord || plan_word(a.plan, i) == plan_header_word(a, i);
+    const int32_t aw = plan_word(a.plan, kPlanAdaptWord);
+    const int32_t ep = plan_word(a.plan, plan_adapt_off(a.plan_wmax) + kAdEpoch);
+#pragma unroll
+    for (int i = 0; i < kPlanEntry; ++i) ew[i] = plan_word(a.plan, kPlanHeader + (int64_t)j * kPlanEntry + i);
+    adapt = planned && aw == 1;
+    epoch = ep;
+  }
+  // the workgroup's times, tagged with the plan's epoch (thread 0, at the workgroup's end)
+  auto record_times = [&]() {
+    if (adapt && tid == 0) {
+      int32_t* f = const_cast<int32_t*>(a.plan) + plan_fb_off(a.plan_wmax) + ((int64_t)h * a.plan_wmax + j) * kFbWords;
+      f[0] = epoch;
+      f[1] = (int32_t)t_start;
+      f[2] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
+    }
+  };
+  if (planned) {
+    sl.total = ew[kPwTotal];
+    sl.lo = ew[kPwLo];
+    sl.hi = ew[kPwHi];
+    sl.b = ew[kPwB];
+    sl.pb = ew[kPwPb];
+    sl.L = ew[kPwL];
+    sl.b_first = ew[kPwBFirst];
+    sl.pb_first = ew[kPwPbFirst];
+    sl.L_first = ew[kPwLFirst];
+    sl.b_stop = ew[kPwBStop];
+    sl.reordered = ew[kPwReordered];
+    const uint32_t r0 = (uint32_t)(wave == 0 ? ew[kPwTile0] : wave == 1 ? ew[kPwTile0 + 1]
+                                   : wave == 2 ? ew[kPwTile0 + 2] : ew[kPwTile0 + 3]);
+    // (rows outside the batch would index outputs and partials out of range)
+    if (sl.L > 0 && !(sl.b >= 0 && sl.b < a.batch && sl.b_first >= 0 && sl.b_first < a.batch && sl.b_stop >= 0 &&
+                      sl.b_stop <= a.batch))
+      planned = false;
+    else if (sl.L > 0) {
+      // the first segment's q and block ids (before the tile, so that they
+      // return first: the q set-up then overlaps the tile's latency)
+      if constexpr (!WIN) {  // (a sliding window needs the lengths for the block ids; such launches take no plan)
+        prefetch_segment(sl.b, max(sl.lo, sl.pb + a.ghost) - (sl.pb + a.ghost));
+        early_setup = true;
+      }
+      if (r0 != kNoTile && tile_in_block) {
+        tile_kv_at(r0 + ((uint32_t)h << bs_log2), lane);
+        tile_scales_at(r0 + ((uint32_t)h << bs_log2), lane);
+        pre_issued = true;
+        pre_r0 = r0 + ((uint32_t)h << bs_log2);
+      }
+    }
+  }
+  // context lengths -> LDS
+#pragma unroll
+  for (int k = 0; k < kLensRegs; ++k) {
+    const int i = tid + k * 64 * kDecWaves;
+    if (i < n_lens) lens_lds[i] = lens_r[k];
+  }
+  __syncthreads();
+  S8KV_TRACE_STAMP(kTrLens);
+  // a plan made from other lengths (the buffer rewritten in place since) is
+  // ignored; a first tile issued from it is issued again below when its row differs
+  if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != plan_word(a.plan, kPlanLensWord)) planned = false;
+  adapt = adapt && planned;
+  bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
+  if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      uint64_t m = __builtin_amdgcn_ballot_w64(c0 + lane < a.batch && lens_at(a, lens_lds, c0 + lane) == 0);
+      while (m != 0) {
+        const int b = c0 + (int)__builtin_ctzll(m);
+        m &= m - 1;
+        for (int i = tid; i < G * D; i += 64 * kDecWaves)
+          a.out[((int64_t)b * a.num_q_heads + h * G) * D + i] = (_Float16)0.0f;
+      }
+    }
+  }
+  if (!has_seg) {
+    record_times();
+    return;
+  }
+  const int total = sl.total, lo = sl.lo, hi = sl.hi;
+
+  // K8V3 codebook byte tables (fp16 of the fp32 codebook).
+  uint32_t tlo03 = 0, tlo47 = 0, thi03 = 0, thi47 = 0;
+  if constexpr (K8V3) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t hb = __builtin_bit_cast(uint16_t, (_Float16)a.v_codebook[i]);
+      const uint32_t lw = hb & 0xFFu, hw = hb >> 8;
+      if (i < 4) { tlo03 |= lw << (8 * i); thi03 |= hw << (8 * i); }
+      else { tlo47 |= lw << (8 * (i - 4)); thi47 |= hw << (8 * (i - 4)); }
+    }
+  }
+
   int b = sl.b, pb = sl.pb, L = sl.L;
   const int b_first = sl.b_first, pb_first = sl.pb_first, L_first = sl.L_first;
   const int b_stop = sl.b_stop;  // rows from here on are left to the reordered segment
   bool reordered = sl.reordered != 0;
   S8KV_TRACE_STAMP(kTrFound);
-  prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
+  if (!(early_setup && planned)) prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
   store_prefetched_bt();
   S8KV_TRACE_STAMP(kTrStaged);
 
