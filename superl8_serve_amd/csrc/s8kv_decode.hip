@@ -702,6 +702,36 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       if (i < bt_first) bt_lds[i] = btv[k];
     }
   };
+  // q: each wave rotates the heads c = wave + 4k of the group (lane l holds
+  // dims l + 64e: the append's fp32 FWHT, stages h = 1 .. D/2 in order),
+  // splits the scaled values into fp16 hi + lo and publishes them in LDS
+  // ([hi, lo][G][D]; a barrier later, every wave takes its MFMA B fragments)
+  auto publish_q = [&]() {
+    const int lane_q = opaque_int(threadIdx.x) & 63;
+    _Float16* qs = reinterpret_cast<_Float16*>(smem + C::SMEM_Q);
+#pragma unroll
+    for (int k = 0; k < kQHeadsPerWave; ++k) {
+      const int cq = wave + kDecWaves * k;
+      if (cq < G) {
+        float x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = (float)qraw[k][e];
+        fwht_row<D>(x, lane_q);
+        if (lane_q < RowLayout<D>::ACTIVE) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            // (materialized: hi and lo must both come from this one fp32 value;
+            // a fused fp16(x*s) for the lo term can differ from fp16(val) by one
+            // ulp, which would leave hi + lo off by 2^-11)
+            const float val = materialize(x[e] * a.qscale);
+            const _Float16 qh = (_Float16)val;
+            qs[cq * D + lane_q + 64 * e] = qh;
+            qs[(G + cq) * D + lane_q + 64 * e] = (_Float16)(val - (float)qh);
+          }
+        }
+      }
+    }
+  };
 
   // context lengths, loaded first so that they return ahead of the set-up and
   // tile loads issued below (one global round trip for the whole prologue)
@@ -716,13 +746,14 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
 
   // ---- the slice and its first segment: from the step's plan, or located here ----
   SliceLoc sl;
-  bool early_setup = false;  // the planned first segment's set-up loads are in flight
+  bool q_ready = false;  // the first segment's rotated q is published (planned prologue)
   bool pre_issued = false;  // this wave's first tile of the first segment is in flight
   uint32_t pre_r0 = kNoTile;  // ... from this storage row
   bool planned = false;
   bool adapt = false;  // the plan's slices come from its adaptive bounds: record this workgroup's times
   int epoch = 0;
   int32_t ew[kPlanEntry];  // this column's plan entry
+  int32_t plan_lens_cs = 0;  // the plan's lens_checksum
   if (a.plan != nullptr) {
     // every plan word the prologue reads, loaded together (the host checked
     // that the buffer holds the whole layout): no chain of dependent loads
@@ -731,6 +762,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     for (int i = 0; i < kPlanHeaderWords; ++i)
       planned &= i == kPlanLensWord || i == kPlanAdaptWord || plan_word(a.plan, i) == plan_header_word(a, i);
     const int32_t aw = plan_word(a.plan, kPlanAdaptWord);
+    plan_lens_cs = plan_word(a.plan, kPlanLensWord);
     const int32_t ep = plan_word(a.plan, plan_adapt_off(a.plan_wmax) + kAdEpoch);
 #pragma unroll
     for (int i = 0; i < kPlanEntry; ++i) ew[i] = plan_word(a.plan, kPlanHeader + (int64_t)j * kPlanEntry + i);
@@ -746,6 +778,7 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       f[2] = (int32_t)(uint32_t)__builtin_amdgcn_s_memrealtime();
     }
   };
+  uint32_t r0 = kNoTile;  // this wave's first tile row at KV head 0, from the plan
   if (planned) {
     sl.total = ew[kPwTotal];
     sl.lo = ew[kPwLo];
@@ -758,38 +791,49 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
     sl.L_first = ew[kPwLFirst];
     sl.b_stop = ew[kPwBStop];
     sl.reordered = ew[kPwReordered];
-    const uint32_t r0 = (uint32_t)(wave == 0 ? ew[kPwTile0] : wave == 1 ? ew[kPwTile0 + 1]
-                                   : wave == 2 ? ew[kPwTile0 + 2] : ew[kPwTile0 + 3]);
+    r0 = (uint32_t)(wave == 0 ? ew[kPwTile0] : wave == 1 ? ew[kPwTile0 + 1]
+                    : wave == 2 ? ew[kPwTile0 + 2] : ew[kPwTile0 + 3]);
     // (rows outside the batch would index outputs and partials out of range)
     if (sl.L > 0 && !(sl.b >= 0 && sl.b < a.batch && sl.b_first >= 0 && sl.b_first < a.batch && sl.b_stop >= 0 &&
                       sl.b_stop <= a.batch))
       planned = false;
-    else if (sl.L > 0) {
-      // the first segment's q and block ids (before the tile, so that they
-      // return first: the q set-up then overlaps the tile's latency)
-      if constexpr (!WIN) {  // (a sliding window needs the lengths for the block ids; such launches take no plan)
-        prefetch_segment(sl.b, max(sl.lo, sl.pb + a.ghost) - (sl.pb + a.ghost));
-        early_setup = true;
-      }
-      if (r0 != kNoTile && tile_in_block) {
-        tile_kv_at(r0 + ((uint32_t)h << bs_log2), lane);
-        tile_scales_at(r0 + ((uint32_t)h << bs_log2), lane);
-        pre_issued = true;
-        pre_r0 = r0 + ((uint32_t)h << bs_log2);
-      }
-    }
   }
-  // context lengths -> LDS
+  auto stage_lens = [&]() {
 #pragma unroll
-  for (int k = 0; k < kLensRegs; ++k) {
-    const int i = tid + k * 64 * kDecWaves;
-    if (i < n_lens) lens_lds[i] = lens_r[k];
-  }
-  __syncthreads();
-  S8KV_TRACE_STAMP(kTrLens);
+    for (int k = 0; k < kLensRegs; ++k) {
+      const int i = tid + k * 64 * kDecWaves;
+      if (i < n_lens) lens_lds[i] = lens_r[k];
+    }
+    __syncthreads();
+    S8KV_TRACE_STAMP(kTrLens);
+  };
   // a plan made from other lengths (the buffer rewritten in place since) is
   // ignored; a first tile issued from it is issued again below when its row differs
-  if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != plan_word(a.plan, kPlanLensWord)) planned = false;
+  if (!WIN && planned && sl.L > 0 && tile_in_block) {
+    // planned prologue, straight-line so that each wait covers only what it
+    // needs: the first segment's set-up loads (q, block ids, the new token's
+    // rows), then this wave's first tile (storage row 0 as a stand-in when the
+    // wave has none, so that every wave has the same loads in flight), then
+    // the lengths (loaded first) -> LDS, the plan's checksum, the block ids
+    // -> LDS and q rotated and published while the tile is in flight
+    prefetch_segment(sl.b, max(sl.lo, sl.pb + a.ghost) - (sl.pb + a.ghost));
+    const uint32_t rr = r0 != kNoTile ? r0 + ((uint32_t)h << bs_log2) : 0u;
+    tile_kv_at(rr, lane);
+    tile_scales_at(rr, lane);
+    pre_issued = r0 != kNoTile;
+    pre_r0 = rr;
+    stage_lens();
+    if ((int32_t)lens_checksum(a, lens_lds, lane) == plan_lens_cs) {
+      store_prefetched_bt();
+      publish_q();
+      q_ready = true;
+    } else {
+      planned = false;
+    }
+  } else {
+    stage_lens();
+    if (planned && (int32_t)lens_checksum(a, lens_lds, lane) != plan_lens_cs) planned = false;
+  }
   adapt = adapt && planned;
   bool has_seg = planned ? sl.L > 0 : locate_slice<WIN>(a, lens_lds, j, lane, sl);
   if (j == 0) {  // empty rows attend nothing: their output is defined as zeros
@@ -826,8 +870,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
   const int b_stop = sl.b_stop;  // rows from here on are left to the reordered segment
   bool reordered = sl.reordered != 0;
   S8KV_TRACE_STAMP(kTrFound);
-  if (!(early_setup && planned)) prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
-  store_prefetched_bt();
+  if (!q_ready) {
+    prefetch_segment(b, max(lo, pb + a.ghost) - (pb + a.ghost));
+    store_prefetched_bt();
+  }
   S8KV_TRACE_STAMP(kTrStaged);
 
   // ---- segments: rows overlapping [lo, hi) ----
@@ -855,34 +901,12 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
       lo_tok = max(0, Lf - a.window) - al;
     }
 
-    // q: each wave rotates the heads c = wave + 4k of the group (lane l holds
-    // dims l + 64e: the append's fp32 FWHT, stages h = 1 .. D/2 in order),
-    // splits the scaled values into fp16 hi + lo and publishes them in LDS;
+    // q rotated and published (the planned prologue did the first segment's),
     // then every wave takes its MFMA B fragments (lane (c, g): dims
-    // g*KCH + 8m .. +8 of head c).
-    _Float16* qs = reinterpret_cast<_Float16*>(smem + C::SMEM_Q);  // [hi, lo][G][D]
-#pragma unroll
-    for (int k = 0; k < kQHeadsPerWave; ++k) {
-      const int cq = wave + kDecWaves * k;
-      if (cq < G) {
-        float x[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) x[e] = (float)qraw[k][e];
-        fwht_row<D>(x, lane);
-        if (lane < RowLayout<D>::ACTIVE) {
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            // (materialized: hi and lo must both come from this one fp32 value;
-            // a fused fp16(x*s) for the lo term can differ from fp16(val) by one
-            // ulp, which would leave hi + lo off by 2^-11)
-            const float val = materialize(x[e] * a.qscale);
-            const _Float16 qh = (_Float16)val;
-            qs[cq * D + lane + 64 * e] = qh;
-            qs[(G + cq) * D + lane + 64 * e] = (_Float16)(val - (float)qh);
-          }
-        }
-      }
-    }
+    // g*KCH + 8m .. +8 of head c)
+    if (!q_ready) publish_q();
+    q_ready = false;
+    const _Float16* qs = reinterpret_cast<const _Float16*>(smem + C::SMEM_Q);  // [hi, lo][G][D]
     __syncthreads();  // every head of q published
     S8KV_TRACE_STAMP_ONCE(kTrQ);
     half8_t qhi[C::NQK], qlo[C::NQK];
