@@ -349,7 +349,7 @@ def read_ceiling(w, steps: int) -> dict:
 TRACE_WORDS = 16  # per-workgroup record of the decode trace build
 
 
-def trace_decode(steps: int, warmup: int, adaptive: bool = True) -> dict:
+def trace_decode(steps: int, warmup: int, adaptive: bool = False) -> dict:
     """Per-launch breakdown of the one-launch decode step from the trace
     build of the library (libsuperl8_kv_trace.so: the same kernels, the decode
     kernel stamping the device's 100 MHz clock at fixed points of each
@@ -1064,9 +1064,9 @@ def main():
                     help="graph replays per read-ceiling probe (0 = skip the read-ceiling leg)")
     ap.add_argument("--no-plan", action="store_true",
                     help="fused step without the per-step slice plan (every launch locates its own work)")
-    ap.add_argument("--fixed-split", action="store_true",
-                    help="the step's plan with the fixed slice split (default: adaptive slice bounds that follow "
-                         "the last step's measured workgroup times)")
+    ap.add_argument("--adaptive-split", action="store_true",
+                    help="the step's plan with adaptive slice bounds that follow the last step's measured "
+                         "workgroup times (default: the fixed split)")
     ap.add_argument("--separate-append", action="store_true",
                     help="decode step as the reference's two calls per layer (append kernel, then decode) instead "
                          "of the one-launch append + decode")
@@ -1101,7 +1101,7 @@ def main():
         from superl8_serve_amd import build_ext
 
         _lib.LIB_PATH = build_ext.TRACE_LIB_PATH
-        print(json.dumps(trace_decode(args.steps, args.warmup, not args.fixed_split)))
+        print(json.dumps(trace_decode(args.steps, args.warmup, args.adaptive_split)))
         return
     _lib.load()
     if args.calibrate_copy_mib:
@@ -1111,7 +1111,7 @@ def main():
         run_verify(args.workload.removesuffix("_k8v3"), args.steps, args.warmup, k8v3=args.workload.endswith("_k8v3"))
         return
     if args.workload == "k8v3":
-        run_k8v3(args.steps, args.warmup, not args.separate_append, not args.no_plan, not args.fixed_split)
+        run_k8v3(args.steps, args.warmup, not args.separate_append, not args.no_plan, args.adaptive_split)
         return
     if args.workload == "copy":
         run_copy(args.steps)
@@ -1130,7 +1130,7 @@ def main():
     w = build(device)
     fused = not args.separate_append
     planned = fused and not args.no_plan
-    adaptive = planned and not args.fixed_split
+    adaptive = planned and args.adaptive_split
     step = make_step(w, fused, planned, adaptive)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

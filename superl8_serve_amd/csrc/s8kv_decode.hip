@@ -1535,7 +1535,7 @@ __device__ __forceinline__ int slice_start_lane(const SliceLayout& s, int j) {
   return r;
 }
 
-// Slice bounds of an adaptive plan, bd[0..W] (one wave).  When the plan
+// Slice bounds of an adaptive plan, bd[0..W] (one workgroup).  When the plan
 // buffer holds this geometry's bounds, its stream total moved by at most a
 // sixteenth, and every workgroup of the last launch that read the plan
 // recorded its times under the plan's epoch, each column's share of the
@@ -1555,12 +1555,17 @@ constexpr float kAdaptStep = 0.25f;
 constexpr float kAdaptFloor = 0.25f;
 constexpr int kAdaptMinTokens = 128;  // stream tokens per column below which the formula is kept
 template <bool WIN>
-__global__ __launch_bounds__(64) void decode_bounds_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kDecWaves) void decode_bounds_kernel(DecodeArgs a) {
+  constexpr int NT = 64 * kDecWaves;
   __shared__ int lens_lds[kLensLds];
   __shared__ float len_lds[kAdaptMaxCols];
   __shared__ float rate_lds[kAdaptMaxCols];
-  const int lane = threadIdx.x;
-  for (int i = lane; i < min(a.batch, kLensLds); i += 64) lens_lds[i] = a.context_lens[i];
+  __shared__ int red_i[2 * kDecWaves];
+  __shared__ float red_f[2 * kDecWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int i = tid; i < min(a.batch, kLensLds); i += NT) lens_lds[i] = a.context_lens[i];
   __syncthreads();
   int32_t* ad = a.plan_out + plan_adapt_off(a.plan_wmax);
   int32_t* bd = ad + kAdBounds;
@@ -1575,27 +1580,37 @@ __global__ __launch_bounds__(64) void decode_bounds_kernel(DecodeArgs a) {
             16 * (int64_t)abs(total - (int)old_total) <= old_total && bd[0] == 0 && bd[W] == (int)old_total;
   // every entry is the last launch's; its earliest start, relative to entry (0, 0)'s
   const uint32_t ref = ok ? (uint32_t)fb[1] : 0u;
-  int dmin = 0;
-  if (ok) {
+  {
     bool mine = true;
-    for (int i = lane; i < W * Hkv; i += 64) {
-      const int hh = i / W, jj = i - hh * W;
-      const int32_t* f = fb + ((int64_t)hh * a.plan_wmax + jj) * kFbWords;
-      mine = mine && f[0] == epoch;
-      dmin = min(dmin, (int)((uint32_t)f[1] - ref));
+    int dmin = 0;
+    if (ok) {
+      for (int i = tid; i < W * Hkv; i += NT) {
+        const int hh = i / W, jj = i - hh * W;
+        const int32_t* f = fb + ((int64_t)hh * a.plan_wmax + jj) * kFbWords;
+        mine = mine && f[0] == epoch;
+        dmin = min(dmin, (int)((uint32_t)f[1] - ref));
+      }
     }
-    ok = __builtin_amdgcn_ballot_w64(!mine) == 0;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) dmin = min(dmin, __shfl_xor(dmin, off, 64));
+    if (lane == 0) {
+      red_i[wave] = __builtin_amdgcn_ballot_w64(!mine) == 0;
+      red_i[kDecWaves + wave] = dmin;
+    }
+  }
+  __syncthreads();
+  int dmin = 0;
+#pragma unroll
+  for (int w = 0; w < kDecWaves; ++w) {
+    ok = ok && red_i[w] != 0;
+    dmin = min(dmin, red_i[kDecWaves + w]);
   }
   // each column's last slice length and rate
-  float sum_len = 0.0f, sum_rate = 0.0f;
-  if (ok) {
+  {
     bool sane = true;
-    for (int c0 = 0; c0 < W; c0 += 64) {
-      const int jj = c0 + lane;
-      float len = 0.0f, rate = 0.0f;
-      if (jj < W) {
+    float sum_len = 0.0f, sum_rate = 0.0f;
+    if (ok) {
+      for (int jj = tid; jj < W; jj += NT) {
         const int lo = bd[jj], hi = bd[jj + 1];
         float t = 0.0f;
         for (int hh = 0; hh < Hkv; ++hh) {
@@ -1603,16 +1618,33 @@ __global__ __launch_bounds__(64) void decode_bounds_kernel(DecodeArgs a) {
           t += (float)((int)((uint32_t)f[2] - ref) - dmin);
         }
         sane = sane && hi >= lo && (hi == lo || t > 0.0f);
-        len = (float)(hi - lo);
-        rate = hi > lo ? len / t : 0.0f;  // a column past the stream's end: rate 0 (it gets the floor share)
+        const float len = (float)(hi - lo);
+        const float rate = hi > lo ? len / t : 0.0f;  // a column past the stream's end: rate 0 (it gets the floor share)
         len_lds[jj] = len;
         rate_lds[jj] = rate;
+        sum_len += len;
+        sum_rate += rate;
       }
-      sum_len += wave_sum_f(len);
-      sum_rate += wave_sum_f(rate);
     }
-    ok = __builtin_amdgcn_ballot_w64(!sane) == 0 && sum_len > 0.0f && sum_rate > 0.0f;
+    sum_len = wave_sum_f(sum_len);
+    sum_rate = wave_sum_f(sum_rate);
+    __syncthreads();  // (red_i read by every thread above)
+    if (lane == 0) {
+      red_i[wave] = __builtin_amdgcn_ballot_w64(!sane) == 0;
+      red_f[wave] = sum_len;
+      red_f[kDecWaves + wave] = sum_rate;
+    }
   }
+  __syncthreads();
+  float sum_len = 0.0f, sum_rate = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kDecWaves; ++w) {  // (fixed order)
+    ok = ok && red_i[w] != 0;
+    sum_len += red_f[w];
+    sum_rate += red_f[kDecWaves + w];
+  }
+  ok = ok && sum_len > 0.0f && sum_rate > 0.0f;
+  if (wave != 0) return;
   if (ok) {
     // the new shares (in len_lds), then their prefix sums scaled to the stream
     const float floor_share = kAdaptFloor / (float)W;
@@ -1859,7 +1891,7 @@ static int launch_decode_impl(DecodeArgs& a, hipStream_t stream) {
         const float g = (float)atof(env);
         a.adapt_gain = g < 0.0f ? 0.0f : (g > 1.0f ? 1.0f : g);
       }
-      hipLaunchKernelGGL((decode_bounds_kernel<WIN>), dim3(1), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL((decode_bounds_kernel<WIN>), dim3(1), dim3(64 * kDecWaves), 0, stream, a);
       hipLaunchKernelGGL((decode_plan_kernel<WIN, true>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
     } else {
       hipLaunchKernelGGL((decode_plan_kernel<WIN>), pgrid, dim3(64 * kDecWaves), 0, stream, a);
