@@ -1562,6 +1562,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_bounds_kernel(DecodeArg
   __shared__ float rate_lds[kAdaptMaxCols];
   __shared__ int red_i[2 * kDecWaves];
   __shared__ float red_f[2 * kDecWaves];
+  __shared__ int nb_lds[kAdaptMaxCols + 1];  // the new bounds before spacing
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1666,8 +1667,29 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_bounds_kernel(DecodeArg
     for (int c0 = 0; c0 < W; c0 += 64) {
       const int jj = c0 + lane;
       const float incl = wave_incl_scan_f(jj < W ? len_lds[jj] : 0.0f, lane) + carry;
-      if (jj + 1 < W) bd[jj + 1] = min(total, 32 * (int)rintf(incl * units));
+      if (jj + 1 < W) {
+        const int nb = min(total, 32 * (int)rintf(incl * units));
+        nb_lds[jj + 1] = nb;
+      }
       carry = __shfl(incl, 63, 64);
+    }
+    // every slice inside the stream holds at least a tile: bd[j] = max over
+    // i <= j of (b[i] + 32 (j - i)), capped at the total (an empty slice in
+    // the middle of a row would hold no segment of it, and the row's
+    // combine would read that column's slot, which no launch wrote)
+    if (lane == 0) nb_lds[0] = 0;
+    int run = 0;  // max over the earlier chunks of b[i] - 32 i
+    for (int c0 = 0; c0 < W; c0 += 64) {
+      const int jj = c0 + lane;
+      int v = jj < W ? nb_lds[jj] - kTile * jj : -0x7FFFFFFF;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off, 64);
+        if (lane >= off) v = max(v, t);
+      }
+      v = max(v, run);
+      if (jj > 0 && jj < W) bd[jj] = min(total, v + kTile * jj);
+      run = __shfl(v, 63, 64);
     }
   } else {
     const SliceLayout sl = slice_layout(total, W, a.slot_classes, a.slot_skew, lane);

@@ -339,6 +339,8 @@ def test_adaptive_plan_steps(layout):
         ad, bd, _ = _adaptive_area(plan, 8)
         assert ad[4] == k, "epoch"
         assert bd[0] == 0 and bd[w] == total and (np.diff(bd) >= 0).all() and (bd % 32 == 0).all()
+        inner = bd[:w] < total  # slices that start inside the stream hold at least a tile
+        assert (np.diff(bd)[inner] >= 32).all()
         moved = moved or not (np.minimum(ent[:, 1], total) == bd[:w]).all()
         _check_close(step.run(plan), ref, f"{layout} adaptive step {k}")
     assert moved, f"the bounds never left the fixed split (adaptive words {ad[:8].tolist()})"
