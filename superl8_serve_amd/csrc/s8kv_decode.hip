@@ -606,9 +606,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
         for (int jj = 0; jj < C::VLOADS; ++jj) {
           const int job = jj * 64 + ln;
           const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
-          io.v[jj].x = bload32<kPol>(vt, off);
-          io.v[jj].y = bload32<kPol>(vt, off + 4);
-          io.v[jj].z = bload32<kPol>(vt, off + 8);
+          const u32x3_t w = bload96<kPol>(vt, off);
+          io.v[jj].x = w.x;
+          io.v[jj].y = w.y;
+          io.v[jj].z = w.z;
         }
       }
     } else {
@@ -625,9 +626,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
           const int job = jj * 64 + ln;
           const uint32_t off = (uint32_t)(((job / C::NG) * C::WORDS + (job % C::NG) * 3) * 4);
           const uint32_t so = r0 * (uint32_t)(C::WORDS * 4);
-          io.v[jj].x = bload32<kPol>(vc, off, so);
-          io.v[jj].y = bload32<kPol>(vc, off + 4, so);
-          io.v[jj].z = bload32<kPol>(vc, off + 8, so);
+          const u32x3_t w = bload96<kPol>(vc, off, so);
+          io.v[jj].x = w.x;
+          io.v[jj].y = w.y;
+          io.v[jj].z = w.z;
         }
       }
     }
@@ -995,9 +997,10 @@ __global__ __launch_bounds__(64 * kDecWaves, D >= 256 ? 2 : 3) void decode_kerne
             const int job = jj * 64 + lane;
             const uint32_t row = row_of(min(tb + job / C::NG, last));
             const uint32_t base = row * (uint32_t)(C::WORDS * 4) + (uint32_t)((job % C::NG) * 12);
-            io.v[jj].x = bload32<kPol>(vc, base);
-            io.v[jj].y = bload32<kPol>(vc, base + 4);
-            io.v[jj].z = bload32<kPol>(vc, base + 8);
+            const u32x3_t w = bload96<kPol>(vc, base);
+            io.v[jj].x = w.x;
+            io.v[jj].y = w.y;
+            io.v[jj].z = w.z;
           }
         }
       };

@@ -54,6 +54,11 @@ template <int AUX = 0>
 __device__ __forceinline__ u32x2_t bload64(rsrc_t r, uint32_t off, uint32_t soff = 0) {
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, AUX));
 }
+// Three consecutive dwords (a K8V3 code group's bit-plane words) in one load.
+template <int AUX = 0>
+__device__ __forceinline__ u32x3_t bload96(rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  return __builtin_bit_cast(u32x3_t, __builtin_amdgcn_raw_buffer_load_b96(r, off, soff, AUX));
+}
 template <int AUX = 0>
 __device__ __forceinline__ uint32_t bload32(rsrc_t r, uint32_t off, uint32_t soff = 0) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, AUX);

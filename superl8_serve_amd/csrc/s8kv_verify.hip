@@ -355,9 +355,10 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
             const int grp = tid / C::SPLIT;
             const int tt = grp / C::NG, gi = grp % C::NG;
             const uint32_t off = local(tt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
-            R.v[0].x = bload32(vt, off);
-            R.v[0].y = bload32(vt, off + 4);
-            R.v[0].z = bload32(vt, off + 8);
+            const u32x3_t w = bload96(vt, off);
+            R.v[0].x = w.x;
+            R.v[0].y = w.y;
+            R.v[0].z = w.z;
           }
         }
         if (tid < (1 + C::NB) * kTile) {
@@ -382,9 +383,10 @@ __global__ __launch_bounds__(64 * kWavesOf<K8V3>, K8V3 ? 1 : 2) void verify_kern
           const int grp = tid / C::SPLIT;
           const int tt = grp / C::NG, gi = grp % C::NG;
           const uint32_t off = row_of(base + tt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
-          R.v[0].x = bload32(vc, off);
-          R.v[0].y = bload32(vc, off + 4);
-          R.v[0].z = bload32(vc, off + 8);
+          const u32x3_t w = bload96(vc, off);
+          R.v[0].x = w.x;
+          R.v[0].y = w.y;
+          R.v[0].z = w.z;
         }
       }
       if (tid < (1 + C::NB) * kTile) {  // k_scale of key tid, then block (tid/32 - 1)'s V scale
@@ -999,9 +1001,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         const int grp = tid >> 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
         const uint32_t off = row_of(base + gt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
-        R.v.x = bload32(vc, off);
-        R.v.y = bload32(vc, off + 4);
-        R.v.z = bload32(vc, off + 8);
+        const u32x3_t w = bload96(vc, off);
+        R.v.x = w.x;
+        R.v.y = w.y;
+        R.v.z = w.z;
       } else {
         R.v = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
       }
