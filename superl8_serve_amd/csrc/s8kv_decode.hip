@@ -111,9 +111,9 @@ constexpr int kTraceWords = 16;
 constexpr int kDecWaves = 4;
 // Cache policy of the tile loads (K, V, scales): non-temporal for the int8
 // layout, whose loads read whole lines once (a read-only sweep over the
-// decode's tiles: 5.6 -> 6.3 TB/s); the default for K8V3, whose V words a
-// tile reads as three dword loads over the same lines (non-temporal there
-// measured 4-13 % slower).
+// decode's tiles: 5.6 -> 6.3 TB/s); the default for K8V3, where
+// non-temporal loads measured slower (4-13 % with each code group's words
+// as three dword loads, 2 % with one dwordx3 load).
 template <bool K8V3>
 constexpr int kTilePolicy = K8V3 ? 0 : kNT;
 constexpr int kTile = 32;
