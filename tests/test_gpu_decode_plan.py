@@ -346,6 +346,46 @@ def test_adaptive_plan_steps(layout):
     assert moved, f"the bounds never left the fixed split (adaptive words {ad[:8].tolist()})"
 
 
+@pytest.mark.parametrize("lens_range", [(1500, 5000), (260, 480)])
+def test_adaptive_plan_random_feedback(lens_range):
+    """Feedback times planted in the plan buffer (random per workgroup, under
+    the plan's epoch) steer the next bounds to skewed splits -- with short
+    rows, streams close to the least length that adapts, where shares sit at
+    their floor: the bounds stay a partition of the stream (multiples of 32,
+    every slice inside the stream at least a tile), cache bytes equal the
+    fixed split's and outputs stay within the attention tolerance."""
+    rng = np.random.default_rng(77 + lens_range[0])
+    lens = rng.integers(lens_range[0], lens_range[1], size=24).tolist()
+    step = _Step(make_case(5454 + lens_range[0], 24, 32, 8, 128, 256, lens, outlier_channels=2), "int8")
+    ref = step.run(None)
+    plan = step.plan(adaptive=True)
+    p = _np(plan).astype(np.int64)
+    w = int(p[3])
+    wmax = (len(p) - HEADER - AD_BOUNDS - 1) // (ENTRY + 1 + 3 * 8)
+    fb0 = HEADER + ENTRY * wmax + AD_BOUNDS + wmax + 1
+    adapted = 0
+    for trial in range(5):
+        host = _np(plan).copy()
+        ad, bd, _ = _adaptive_area(plan, 8)
+        epoch = int(ad[4])
+        fb = host[fb0: fb0 + 3 * 8 * wmax].reshape(8, wmax, 3)
+        fb[:, :w, 0] = epoch
+        fb[:, :w, 1] = 1000
+        fb[:, :w, 2] = 1000 + rng.integers(100, 100000, size=(8, w))
+        plan.copy_(_t(host))
+        step.plan(adaptive=True, plan=plan)
+        ad, bd, _ = _adaptive_area(plan, 8)
+        total = int(ad[5])
+        assert ad[4] == epoch + 1
+        assert bd[0] == 0 and bd[w] == total and (np.diff(bd) >= 0).all() and (bd % 32 == 0).all()
+        inner = bd[:w] < total
+        assert (np.diff(bd)[inner] >= 32).all(), f"trial {trial}: an empty slice inside the stream"
+        fixed = _np(step.plan()).astype(np.int64)[HEADER: HEADER + ENTRY * w].reshape(w, ENTRY)
+        adapted += int(not (np.minimum(fixed[:, 1], total) == bd[:w]).all())
+        _check_close(step.run(plan), ref, f"random feedback trial {trial}")
+    assert adapted > 0, "no trial left the fixed split"
+
+
 def test_adaptive_plan_falls_back_on_new_lengths():
     """After the lengths are rewritten in place (the stream total moves by
     more than a sixteenth), the next adaptive plan is the fixed split again:
