@@ -156,12 +156,15 @@ def test_unsupported_codec_parameters_are_rejected():
         lloydmax.quantize_lloydmax(torch.zeros(1, 128), dim=0)
 
 
+_GUIDE = "INTEGRATION.md"  # the maintainer's binding guide at the repository root
+
+
 def _integration_calls():
-    """Every ``superl8.X`` / ``ops.X`` attribute named in INTEGRATION.md's
-    code blocks (comments included: they show calls too)."""
+    """Every ``superl8.X`` / ``ops.X`` attribute named in the binding
+    guide's Python code blocks (comments included: they show calls too)."""
     import re
 
-    text = (Path(__file__).resolve().parent.parent / "INTEGRATION.md").read_text()
+    text = (Path(__file__).resolve().parent.parent / _GUIDE).read_text()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     names = set()
     for blk in blocks:
@@ -180,7 +183,7 @@ def test_integration_examples_name_only_real_functions():
         root, *attrs = name.split(".")
         obj = superl8 if root == "superl8" else ops
         for attr in attrs:
-            assert hasattr(obj, attr), f"INTEGRATION.md calls {name}, which does not resolve"
+            assert hasattr(obj, attr), f"the binding guide calls {name}, which does not resolve"
             obj = getattr(obj, attr)
         assert callable(obj) or inspect.ismodule(obj), name
 
