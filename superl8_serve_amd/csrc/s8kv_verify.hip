@@ -855,8 +855,12 @@ struct WideCfg {
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
 };
 
-template <bool K8V3>
+// DENSE: fresh fp16 K / V (attn_varlen), token-major with cu_seqlens, not
+// rotated: q is the exact fp16 input (one QK MFMA per fragment) and the
+// softmax scale multiplies the fp32 score through the staged K scales.
+template <bool K8V3, bool DENSE = false>
 __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
+  static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
   using C = WideCfg<K8V3>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -880,13 +884,26 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   const int j = lane & 31;  // this lane's query row within the wave (and the K row of its QK A operand)
   const int hf = lane >> 5;
 
-  const int nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
-  const int prefix = max(0, a.prefix_lens[b]);
+  // dense: sequence b's queries are tokens cu_q[b] .., its keys cu_k[b] ..;
+  // causal is bottom-right aligned (query s sees keys j <= s + nk - nq, which
+  // may be none), else every key is visible
+  int nq, prefix, nk = 0, q0 = 0, k0 = 0;
+  if constexpr (DENSE) {
+    q0 = a.cu_q[b];
+    k0 = a.cu_k[b];
+    const int nq_seq = max(0, a.cu_q[b + 1] - q0);
+    nk = max(0, a.cu_k[b + 1] - k0);
+    nq = min(nq_seq, a.max_queries);
+    prefix = a.causal ? nk - nq_seq : nk;
+  } else {
+    nq = a.query_lens ? max(0, min(a.query_lens[b], a.max_queries)) : a.max_queries;
+    prefix = max(0, a.prefix_lens[b]);
+  }
   const int row0 = qb * C::ROWS;
   const int pos_hi = min(nq, (row0 + C::ROWS + G - 1) / G);
   const bool tree = a.tree_mask != nullptr;
   int kv_end = prefix + (tree ? nq : pos_hi);
-  kv_end = min(kv_end, a.max_context_len);
+  kv_end = min(kv_end, DENSE ? nk : a.max_context_len);
   if (row0 / G >= nq) kv_end = 0;
   const int vis_all = tree ? prefix : prefix + row0 / G + 1;
 
@@ -897,9 +914,14 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   const uint64_t tmask = (tree && row_live) ? (uint64_t)a.tree_mask[(int64_t)b * a.max_queries + pos] : 0ull;
 
   // ---- q: rotate (FWHT over dims 64 hf .. 64 hf + 63 in-lane, then across
-  // the lane pair), pre-scale, split into fp16 hi + lo ----
-  half8_t qhi[8], qlo[8];
-  {
+  // the lane pair), pre-scale, split into fp16 hi + lo; dense: the fp16 input ----
+  half8_t qhi[8], qlo[DENSE ? 1 : 8];
+  if constexpr (DENSE) {
+    const _Float16* qp = a.q + (int64_t)q0 * a.q_stride_s + (int64_t)head * a.q_stride_h +
+                         (int64_t)(row_live ? pos : 0) * a.q_stride_s + hf * 64;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qhi[m] = row_live ? *reinterpret_cast<const half8_t*>(qp + 8 * m) : half8_t{};
+  } else {
     float x[64];
     const _Float16* qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)head * a.q_stride_h +
                          (int64_t)(row_live ? pos : 0) * a.q_stride_s + hf * 64;
@@ -940,6 +962,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 #pragma unroll
   for (int n = 0; n < 4; ++n) acc[n] = float16_t{};
   WeightShift ws(kMaxSlack);
+  if constexpr (DENSE) ws.raise(1.0f, kMaxSlack);  // fp16 K / V: every V scale is 1
 
   const rsrc_t kc = make_rsrc(a.k_cache, a.kc_bytes);
   const rsrc_t vc = make_rsrc(a.v_cache, a.vc_bytes);
@@ -978,7 +1001,8 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
     const int fb = u0 >> bs_log2;
     const int nblk = ((u1 - 1) >> bs_log2) - fb + 1;
     __syncthreads();  // previous users of bt_lds and the tile buffers are done
-    for (int i = tid; i < nblk; i += C::THREADS) bt_lds[i] = bt_row[fb + i];
+    if constexpr (!DENSE)
+      for (int i = tid; i < nblk; i += C::THREADS) bt_lds[i] = bt_row[fb + i];
     __syncthreads();
 
     auto row_of = [&](int kk) -> uint32_t {
@@ -987,26 +1011,39 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)kk & bsm);
     };
 
+    // dense: two 16-byte fp16 K chunks and two V chunks per thread
+    constexpr int NCH = DENSE ? 2 : 1;
     struct TileRegs {
-      u32x4_t k, v;
+      u32x4_t k[NCH], v[NCH];
       float s;
     };
     // one 16-byte K chunk and one V chunk (K8V3: a half code group's three
     // words) per thread, and the tile's 2 x 32 scales in threads 0..63
     auto load_tile = [&](TileRegs& R, int base) {
+      if constexpr (DENSE) {  // fp16 rows of keys base .. base + 31 (clamped to the last key)
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+          const int ch = tid + i * C::THREADS, tt = ch >> 4, part = ch & 15;
+          const int64_t tok = k0 + min(base + tt, nk - 1);
+          R.k[i] = *reinterpret_cast<const u32x4_t*>(a.k_f16 + tok * a.k_stride_t + h * a.k_stride_h + part * 8);
+          R.v[i] = *reinterpret_cast<const u32x4_t*>(a.v_f16 + tok * a.v_stride_t + h * a.v_stride_h + part * 8);
+        }
+        R.s = 1.0f;
+        return;
+      }
       const int tt = tid >> 3, part = tid & 7;
       const uint32_t row = row_of(base + tt);
-      R.k = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
+      R.k[0] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
       if constexpr (K8V3) {
         const int grp = tid >> 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
         const uint32_t off = row_of(base + gt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
         const u32x3_t w = bload96(vc, off);
-        R.v.x = w.x;
-        R.v.y = w.y;
-        R.v.z = w.z;
+        R.v[0].x = w.x;
+        R.v[0].y = w.y;
+        R.v[0].z = w.z;
       } else {
-        R.v = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
+        R.v[0] = bload128(vc, row * (uint32_t)D + (uint32_t)part * 16u);
       }
       // (two loads, each with one descriptor: a descriptor chosen per lane
       // would be issued lane by lane)
@@ -1017,14 +1054,24 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       char* kb = smem + buf * C::BUF;
       char* vb = kb + C::KBYTES;
       float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
+      if constexpr (DENSE) {  // fp16 rows as they are; K "scales" carry the softmax scale, V scales are 1
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+          const int ch = tid + i * C::THREADS, tt = ch >> 4, part = ch & 15;
+          *reinterpret_cast<u32x4_t*>(kb + tt * C::KROW + part * 16) = R.k[i];
+          *reinterpret_cast<u32x4_t*>(vb + tt * C::VROW + part * 16) = R.v[i];
+        }
+        if (tid < 2 * kTile) sb[tid] = tid < kTile ? a.qscale : 1.0f;
+        return;
+      }
       const int tt = tid >> 3, part = tid & 7;
-      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k.x, R.k.y});
-      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k.z, R.k.w});
+      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k[0].x, R.k[0].y});
+      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k[0].z, R.k[0].w});
       if constexpr (K8V3) {  // 16 codes of one group -> fp16 codebook entries
         const int grp = tid >> 1, half = tid & 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
         const int sh = half * 16;
-        const uint32_t w0 = R.v.x >> sh, w1 = R.v.y >> sh, w2 = R.v.z >> sh;
+        const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
         char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4 += 2) {
@@ -1039,8 +1086,8 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
           *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
         }
       } else {
-        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v.x, R.v.y});
-        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v.z, R.v.w});
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v[0].x, R.v[0].y});
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v[0].z, R.v[0].w});
       }
       // a V scale is staged finite (NaN and inf -> 2^100): the weight of a
       // hidden key, exp2(-inf) * scale, is then 0 whatever was stored there
@@ -1065,7 +1112,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
           sc = mfma32x32x16(ka[m], qhi[m], sc);
-          sc = mfma32x32x16(ka[m], qlo[m], sc);
+          if constexpr (!DENSE) sc = mfma32x32x16(ka[m], qlo[m], sc);
         }
       }
       // this lane's keys: register r is key 8 (r / 4) + 4 hf + r % 4
@@ -1214,9 +1261,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   }
 
   // ---- normalize and write this lane's half of row j ----
-  if (pos < a.max_queries) {
+  if (DENSE ? row_live : pos < a.max_queries) {
     const float inv = (row_live && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    _Float16* op = a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
+    _Float16* op = DENSE ? a.out + (int64_t)(q0 + pos) * a.o_stride_t + (int64_t)head * a.o_stride_h
+                         : a.out + (((int64_t)b * a.num_q_heads + head) * a.max_queries + pos) * D;
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
@@ -1352,12 +1400,12 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
                  : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
-template <bool K8V3>
+template <bool K8V3, bool DENSE = false>
 static int launch_wide(VerifyArgs& a, hipStream_t stream) {
   using C = WideCfg<K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -1370,7 +1418,7 @@ static int launch_wide(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_wide_kernel<K8V3>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream, a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
@@ -1766,6 +1814,13 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
       case 256: return verify::launch<256, false, true, true>(a, s);
     }
     return S8KV_ERR_UNSUPPORTED;
+  }
+  // head_dim 128: the wide kernel (32 query rows per wave) when its vector
+  // q loads (16 bytes) and output stores (8 bytes) are aligned
+  if (head_dim == 128 && (uintptr_t)q % 16 == 0 && q_stride_t % 8 == 0 && q_stride_h % 8 == 0 &&
+      (uintptr_t)out % 8 == 0 && o_stride_t % 4 == 0 && o_stride_h % 4 == 0) {
+    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false>::ROWS - 1) / verify::WideCfg<false>::ROWS;
+    return verify::launch_wide<false, true>(a, s);
   }
   switch (head_dim) {
     case 64: return verify::launch<64, false, false, true>(a, s);
