@@ -858,9 +858,11 @@ struct WideCfg {
 // DENSE: fresh fp16 K / V (attn_varlen), token-major with cu_seqlens, not
 // rotated: q is the exact fp16 input (one QK MFMA per fragment) and the
 // softmax scale multiplies the fp32 score through the staged K scales.
-template <bool K8V3, bool DENSE = false>
+// WIN (dense only): a band -- query s sees keys j >= prefix + s - window.
+template <bool K8V3, bool DENSE = false, bool WIN = false>
 __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
+  static_assert(!WIN || DENSE, "the paged window verify runs the 16-row kernel");
   using C = WideCfg<K8V3>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -906,6 +908,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   kv_end = min(kv_end, DENSE ? nk : a.max_context_len);
   if (row0 / G >= nq) kv_end = 0;
   const int vis_all = tree ? prefix : prefix + row0 / G + 1;
+  // band: keys below lo_key are hidden from every row of the block (the key
+  // loop starts at the tile holding it), keys from lo_all on from none
+  const int lo_key = WIN ? max(0, prefix + row0 / G - a.window) : 0;
+  const int lo_all = WIN ? prefix + min(nq - 1, (row0 + C::ROWS - 1) / G) - a.window : 0;
 
   const int r = row0 + wave * 32 + j;
   const int pos = r / G;
@@ -983,7 +989,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   const uint32_t hkv = (uint32_t)a.num_kv_heads;
   const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
 
-  int k_lo = 0, k_hi = kv_end;
+  int k_lo = lo_key & ~(kTile - 1), k_hi = kv_end;
   if (a.splits > 1) {
     const int chunk = ((max(0, kv_end) + a.splits - 1) / a.splits + kTile - 1) & ~(kTile - 1);
     k_lo = sp * chunk;
@@ -1127,7 +1133,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
           const int kk = base + 8 * (rr >> 2) + 4 * hf + (rr & 3);
           const int di = kk - prefix;
           const bool dvis = tree ? ((uint32_t)di < 64u && ((tmask >> (di & 63)) & 1ull)) : di <= pos;
-          const bool vis = kk < kv_end && row_live && (di < 0 || dvis);
+          const bool vis = kk < kv_end && row_live && (di < 0 || dvis) && (!WIN || kk >= prefix + pos - a.window);
           const float v = __builtin_fmaf(sc[rr], kscale(rr), -m_ref);
           y[rr] = vis ? v : kNegInf;
         }
@@ -1213,7 +1219,8 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
     // a tile is masked when it reaches keys that some row of the block does
     // not see, or the end of the visible keys (wave-uniform)
     auto compute = [&](int buf, int base) {
-      if constexpr (LIVE) process(buf, base, !(base + kTile <= vis_all && base + kTile <= kv_end));
+      if constexpr (LIVE)
+        process(buf, base, !(base + kTile <= vis_all && base + kTile <= kv_end && (!WIN || base >= lo_all)));
     };
     const int ntiles = (u1 - u0 + kTile - 1) / kTile;
     TileRegs ra, rb;
@@ -1400,12 +1407,12 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
                  : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
-template <bool K8V3, bool DENSE = false>
+template <bool K8V3, bool DENSE = false, bool WIN = false>
 static int launch_wide(VerifyArgs& a, hipStream_t stream) {
   using C = WideCfg<K8V3>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE, WIN>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -1418,7 +1425,8 @@ static int launch_wide(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream, a);
+  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE, WIN>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream,
+                     a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
@@ -1806,8 +1814,15 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.causal = causal ? 1 : 0;
   a.out = (_Float16*)out;
   hipStream_t s = (hipStream_t)stream;
+  // head_dim 128: the wide kernel (32 query rows per wave) when its vector
+  // q loads (16 bytes) and output stores (8 bytes) are aligned
+  const bool wide = head_dim == 128 && (uintptr_t)q % 16 == 0 && q_stride_t % 8 == 0 && q_stride_h % 8 == 0 &&
+                    (uintptr_t)out % 8 == 0 && o_stride_t % 4 == 0 && o_stride_h % 4 == 0;
+  if (wide)
+    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false>::ROWS - 1) / verify::WideCfg<false>::ROWS;
   if (window_left > 0) {  // query s sees keys (s + nk - nq - window_left, s + nk - nq]: window_left keys
     a.window = window_left - 1;  // the kernel's band: keys >= s + nk - nq - window
+    if (wide) return verify::launch_wide<false, true, true>(a, s);
     switch (head_dim) {
       case 64: return verify::launch<64, false, true, true>(a, s);
       case 128: return verify::launch<128, false, true, true>(a, s);
@@ -1815,13 +1830,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
     }
     return S8KV_ERR_UNSUPPORTED;
   }
-  // head_dim 128: the wide kernel (32 query rows per wave) when its vector
-  // q loads (16 bytes) and output stores (8 bytes) are aligned
-  if (head_dim == 128 && (uintptr_t)q % 16 == 0 && q_stride_t % 8 == 0 && q_stride_h % 8 == 0 &&
-      (uintptr_t)out % 8 == 0 && o_stride_t % 4 == 0 && o_stride_h % 4 == 0) {
-    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false>::ROWS - 1) / verify::WideCfg<false>::ROWS;
-    return verify::launch_wide<false, true>(a, s);
-  }
+  if (wide) return verify::launch_wide<false, true>(a, s);
   switch (head_dim) {
     case 64: return verify::launch<64, false, false, true>(a, s);
     case 128: return verify::launch<128, false, false, true>(a, s);

@@ -103,6 +103,35 @@ def test_attn_varlen_window_left(d, qlens, klens, w):
     _close(out.float().cpu().numpy(), ref, f"window_left {w}")
 
 
+def test_attn_varlen_band_long_sequence_g16():
+    """head_dim 128 with a band inside a long sequence and 16 q heads per KV
+    head (128-row workgroups of 8 positions): the band's lower edge moves
+    across the tiles of every block."""
+    q, k, v, cu_q, cu_k = _case(771, 32, 2, 128, [1000, 70], [1000, 300])
+    scale = 1.0 / np.sqrt(128)
+    out = ops.attn_varlen(_t(q), _t(k), _t(v), _t(cu_q), _t(cu_k), 1000, 1000, causal=True, scale=scale,
+                          window_left=100)
+    torch.cuda.synchronize()
+    ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, scale, True, window_left=100)
+    _close(out.float().cpu().numpy(), ref, "band, G = 16")
+
+
+@pytest.mark.parametrize("window_left", [None, 50])
+def test_attn_varlen_unaligned_q(window_left):
+    """q rows that are not 16-byte aligned (a view 4 elements into each row)
+    take the 16-row kernel; the result is the same attention."""
+    q, k, v, cu_q, cu_k = _case(781, 8, 2, 128, [120, 9], [200, 9])
+    qbig = np.zeros((q.shape[0], q.shape[1], 136), np.float16)
+    qbig[:, :, 4:132] = q
+    qv = _t(qbig)[:, :, 4:132]
+    assert qv.data_ptr() % 16 != 0
+    out = ops.attn_varlen(qv, _t(k), _t(v), _t(cu_q), _t(cu_k), 120, 200, causal=True, scale=0.1,
+                          window_left=window_left)
+    torch.cuda.synchronize()
+    ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, 0.1, True, window_left=window_left)
+    _close(out.float().cpu().numpy(), ref, f"unaligned q, window {window_left}")
+
+
 def test_attn_varlen_wide_window_equals_plain_causal():
     q, k, v, cu_q, cu_k = _case(761, 8, 2, 128, [200, 50], [200, 90])
     args = (_t(q), _t(k), _t(v), _t(cu_q), _t(cu_k), 200, 200)
