@@ -858,11 +858,12 @@ struct WideCfg {
 // DENSE: fresh fp16 K / V (attn_varlen), token-major with cu_seqlens, not
 // rotated: q is the exact fp16 input (one QK MFMA per fragment) and the
 // softmax scale multiplies the fp32 score through the staged K scales.
-// WIN (dense only): a band -- query s sees keys j >= prefix + s - window.
+// WIN, dense: a band -- query s sees keys j >= prefix + s - window; paged
+// (no fresh drafts: they are in the cache): every row sees the last `window`
+// prefix keys and the drafts, keys j >= prefix - window.
 template <bool K8V3, bool DENSE = false, bool WIN = false>
 __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
-  static_assert(!WIN || DENSE, "the paged window verify runs the 16-row kernel");
   using C = WideCfg<K8V3>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -908,10 +909,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   kv_end = min(kv_end, DENSE ? nk : a.max_context_len);
   if (row0 / G >= nq) kv_end = 0;
   const int vis_all = tree ? prefix : prefix + row0 / G + 1;
-  // band: keys below lo_key are hidden from every row of the block (the key
+  // window: keys below lo_key are hidden from every row of the block (the key
   // loop starts at the tile holding it), keys from lo_all on from none
-  const int lo_key = WIN ? max(0, prefix + row0 / G - a.window) : 0;
-  const int lo_all = WIN ? prefix + min(nq - 1, (row0 + C::ROWS - 1) / G) - a.window : 0;
+  const int lo_key = WIN ? max(0, prefix + (DENSE ? row0 / G : 0) - a.window) : 0;
+  const int lo_all = WIN && DENSE ? prefix + min(nq - 1, (row0 + C::ROWS - 1) / G) - a.window : lo_key;
 
   const int r = row0 + wave * 32 + j;
   const int pos = r / G;
@@ -989,10 +990,11 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   const uint32_t hkv = (uint32_t)a.num_kv_heads;
   const int32_t* bt_row = a.block_table + (int64_t)b * a.bt_stride;
 
+  // this workgroup's keys: split sp of the block's tile-aligned key range
   int k_lo = lo_key & ~(kTile - 1), k_hi = kv_end;
   if (a.splits > 1) {
-    const int chunk = ((max(0, kv_end) + a.splits - 1) / a.splits + kTile - 1) & ~(kTile - 1);
-    k_lo = sp * chunk;
+    const int chunk = ((max(0, kv_end - k_lo) + a.splits - 1) / a.splits + kTile - 1) & ~(kTile - 1);
+    k_lo += sp * chunk;
     k_hi = min(kv_end, k_lo + chunk);
   }
   // A wave whose 32 rows are all past the query count (a short draft tree,
@@ -1133,7 +1135,8 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
           const int kk = base + 8 * (rr >> 2) + 4 * hf + (rr & 3);
           const int di = kk - prefix;
           const bool dvis = tree ? ((uint32_t)di < 64u && ((tmask >> (di & 63)) & 1ull)) : di <= pos;
-          const bool vis = kk < kv_end && row_live && (di < 0 || dvis) && (!WIN || kk >= prefix + pos - a.window);
+          const bool vis = kk < kv_end && row_live && (di < 0 || dvis) &&
+                           (!WIN || kk >= (DENSE ? prefix + pos - a.window : lo_key));
           const float v = __builtin_fmaf(sc[rr], kscale(rr), -m_ref);
           y[rr] = vis ? v : kNegInf;
         }
@@ -1145,8 +1148,10 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 #pragma unroll
       for (int rr = 1; rr < 16; ++rr) my = fmaxf(my, y[rr]);
       my = max_x32(my);
-      // V-scale bound test: lane l checks the V scale of key l % 32
-      const float vp = sb[kTile + j];
+      // V-scale bound test: lane l checks the V scale of key l % 32 (paged
+      // window: not of the keys below it, which may hold anything)
+      float vp = sb[kTile + j];
+      if constexpr (WIN && !DENSE) vp = base + j >= lo_key ? vp : 0.0f;
       if (__builtin_amdgcn_ballot_w64(my > ws.thr() || vp > ws.vbound()) != 0) {
         // rare: a V scale above the bound lowers the weight shift (by d, a
         // power of two folded into alpha), or a score passes the lazy slack:
@@ -1289,7 +1294,9 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 // or WideCfg::ROWS for the wide kernel), and the workgroups a CU keeps
 // resident (the kernels' launch bounds).  The wide kernel serves the paged
 // head_dim-128 calls without a window whose tensors fit 32-bit offsets.
-static bool use_wide(int head_dim, bool windowed, bool big) { return head_dim == 128 && !windowed && !big; }
+// the wide kernel: head_dim 128, no per-tile descriptor rebasing (a cache
+// under 4 GiB), and no fresh drafts (their rows are read by the 16-row kernel)
+static bool use_wide(int head_dim, bool fresh_drafts, bool big) { return head_dim == 128 && !fresh_drafts && !big; }
 static int rows_per_wg(int head_dim, bool k8v3, bool wide = false) {
   if (wide) return WideCfg<false>::ROWS;
   return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1);
@@ -1540,7 +1547,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
                         const int8_t* k_cache, const float* k_scale, int64_t num_blocks, int block_size,
                         const int32_t* block_table, int64_t block_table_stride, const int32_t* prefix_lens,
                         const int32_t* query_lens, const int64_t* tree_mask, int max_context_len, float scale,
-                        void* out, bool k8v3, bool windowed) {
+                        void* out, bool k8v3, bool fresh_drafts) {
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
@@ -1580,7 +1587,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, windowed, a.big));
+  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, fresh_drafts, a.big));
   a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
@@ -1597,16 +1604,17 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
                                 const FreshDrafts* fresh) {
   S8KV_REQUIRE(batch >= 0 && max_queries >= 0, S8KV_ERR_INVALID, "verify: negative batch or query count");
   if (batch == 0 || max_queries == 0) return S8KV_OK;
+  const bool fresh_k = fresh != nullptr && fresh->k != nullptr;
   verify::VerifyArgs a{};
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false, window > 0);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false, fresh_k);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  const bool wide = verify::use_wide(head_dim, window > 0, a.big);
+  const bool wide = verify::use_wide(head_dim, fresh_k, a.big);
   if (const int rc = verify_use_workspace(a, head_dim, false, wide, workspace, workspace_bytes)) return rc;
-  if (fresh != nullptr && fresh->k != nullptr) {
+  if (fresh_k) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
                      fresh->k_stride[1] % 4 == 0 && fresh->k_stride[2] % 4 == 0 && fresh->v_stride[0] % 8 == 0 &&
@@ -1629,6 +1637,7 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   a.vc_bytes = a.kc_bytes;
   a.vs_bytes = a.ks_bytes;
   hipStream_t s = (hipStream_t)stream;
+  if (wide) return a.window > 0 ? verify::launch_wide<false, false, true>(a, s) : verify::launch_wide<false>(a, s);
   if (a.window > 0) {
     switch (head_dim) {
       case 64: return verify::launch<64, false, true>(a, s);
@@ -1637,7 +1646,6 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
     }
     return S8KV_ERR_UNSUPPORTED;
   }
-  if (wide) return verify::launch_wide<false>(a, s);
   switch (head_dim) {
     case 64: return verify::launch<64, false>(a, s);
     case 128: return verify::launch<128, false>(a, s);
@@ -1691,16 +1699,17 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   S8KV_REQUIRE(head_dim == 128 || head_dim == 256, S8KV_ERR_UNSUPPORTED,
                "verify k8v3: head_dim %d not in {128, 256}", head_dim);
   S8KV_REQUIRE(lloyd_block == 128, S8KV_ERR_UNSUPPORTED, "verify k8v3: lloyd_block %d != 128", lloyd_block);
+  const bool fresh_k = fresh != nullptr && fresh->k != nullptr;
   verify::VerifyArgs a{};
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true, window > 0);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true, fresh_k);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  const bool wide = verify::use_wide(head_dim, window > 0, a.big);
+  const bool wide = verify::use_wide(head_dim, fresh_k, a.big);
   if (const int rc = verify_use_workspace(a, head_dim, true, wide, workspace, workspace_bytes)) return rc;
-  if (fresh != nullptr && fresh->k != nullptr) {
+  if (fresh_k) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
     S8KV_REQUIRE((uintptr_t)fresh->k % 16 == 0 && (uintptr_t)fresh->v % 16 == 0 && fresh->k_stride[0] % 4 == 0 &&
                      fresh->k_stride[1] % 4 == 0 && fresh->k_stride[2] % 4 == 0 && fresh->v_stride[0] % 8 == 0 &&
@@ -1725,9 +1734,9 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.vc_bytes = cap_u32(a.vc_total);
   a.vs_bytes = cap_u32(a.vs_total);
   hipStream_t s = (hipStream_t)stream;
+  if (wide) return a.window > 0 ? verify::launch_wide<true, false, true>(a, s) : verify::launch_wide<true>(a, s);
   if (a.window > 0)
     return head_dim == 128 ? verify::launch<128, true, true>(a, s) : verify::launch<256, true, true>(a, s);
-  if (wide) return verify::launch_wide<true>(a, s);
   return head_dim == 128 ? verify::launch<128, true>(a, s) : verify::launch<256, true>(a, s);
 }
 

@@ -208,11 +208,11 @@ def test_window_tree_verify():
 
 
 def test_window_verify_covering_the_prefix_equals_verify():
-    """A window covering every row's prefix masks nothing.  The windowed call
-    runs the 16-row verify kernel and the unwindowed head_dim-128 paged call
-    the 32-row one, whose sums round differently: equal within the attention
-    tolerance (a masking error would be far outside it), and both match the
-    oracle."""
+    """A window covering every row's prefix masks nothing.  Both calls run the
+    32-row kernel, but the windowed one plans its key split over the window
+    and the drafts, not the whole context, so its partial sums may round
+    differently: equal within the attention tolerance (a masking error would
+    be far outside it), and both match the oracle."""
     from tests.kvgpu import assert_close
 
     case, cache, q, pre = _verify_case(621, 3, 8, 2, 128, 16, [300, 37, 256], 7)
@@ -223,19 +223,22 @@ def test_window_verify_covering_the_prefix_equals_verify():
     assert_close(plain, ref, "unwindowed vs oracle")
 
 
-def test_window_verify_ignores_keys_before_the_window():
-    case, cache, q, pre = _verify_case(631, 2, 8, 2, 128, 16, [400, 150], 5)
+@pytest.mark.parametrize("k8v3", [False, True])
+def test_window_verify_ignores_keys_before_the_window(k8v3):
+    """Cache rows below the window (its first tile holds some) may hold any
+    bytes and scales, inf and NaN included: the result is bit-identical."""
+    case, cache, q, pre = _verify_case(631, 2, 8, 2, 128, 16, [400, 150], 5, k8v3)
     window = 61
-    before = _verify(case, cache, q, pre, window)
+    before = _verify(case, cache, q, pre, window, k8v3)
     kc, ks, vc, vs = (x.copy() for x in cache)
     for b, p in enumerate(pre):
         for pos in range(max(0, int(p) - window)):
             blk, off = case.block_table[b, pos // case.block_size], pos % case.block_size
             kc[blk, :, off] = 127
             ks[blk, :, off] = np.inf if pos % 2 else np.nan  # non-finite scales must not reach the output
-            vc[blk, :, off] = -127
+            vc[blk, :, off] = -1 if k8v3 else -127
             vs[blk, :, off] = np.nan if pos % 2 else np.inf
-    assert np.array_equal(_verify(case, (kc, ks, vc, vs), q, pre, window), before)
+    assert np.array_equal(_verify(case, (kc, ks, vc, vs), q, pre, window, k8v3), before)
 
 
 def _drafts(case, pre, nq):
