@@ -853,17 +853,22 @@ struct WideCfg {
   static constexpr int VJOBS = 2 * kTile * NG;  // K8V3: two threads per code group (16 values each)
   static_assert(VJOBS == THREADS, "one K8V3 expansion job per thread");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
+  // window verify with fresh drafts: the low fp16 part of the drafts' K per buffer
+  static constexpr int KLO_OFF = (SMEM + 15) / 16 * 16;
+  static constexpr int SMEM_WIN = KLO_OFF + 2 * KBYTES;
 };
 
 // DENSE: fresh fp16 K / V (attn_varlen), token-major with cu_seqlens, not
 // rotated: q is the exact fp16 input (one QK MFMA per fragment) and the
 // softmax scale multiplies the fp32 score through the staged K scales.
-// WIN, dense: a band -- query s sees keys j >= prefix + s - window; paged
-// (no fresh drafts: they are in the cache): every row sees the last `window`
-// prefix keys and the drafts, keys j >= prefix - window.
-template <bool K8V3, bool DENSE = false, bool WIN = false>
+// WIN, dense: a band -- query s sees keys j >= prefix + s - window; paged:
+// every row sees the last `window` prefix keys and the drafts, keys j >=
+// prefix - window, the drafts' K / V from the cache or (FRESH, a.kd set) from
+// the fresh fp32 K (rotated) and fp16 V rows of the drafts.
+template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
 __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
+  static_assert(!FRESH || (WIN && !DENSE), "fresh drafts: a paged window verify");
   using C = WideCfg<K8V3>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1019,6 +1024,20 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       return ((blk * hkv + (uint32_t)h) << bs_log2) + ((uint32_t)kk & bsm);
     };
 
+    // window verify with fresh drafts: whether the tile at `base` holds draft
+    // keys (wave-uniform), whose K then has a low fp16 part, and the draft
+    // index of its key tt (-1: a prefix key, or no fresh drafts)
+    auto fresh_tile = [&](int base) -> bool {
+      if constexpr (FRESH) return base + kTile > prefix && base < prefix + nq;
+      return false;
+    };
+    auto fresh_draft = [&](int base, int tt) -> int {
+      if constexpr (FRESH) {
+        const int di = base + tt - prefix;
+        return (di >= 0 && di < nq) ? di : -1;
+      }
+      return -1;
+    };
     // dense: two 16-byte fp16 K chunks and two V chunks per thread
     constexpr int NCH = DENSE ? 2 : 1;
     struct TileRegs {
@@ -1027,6 +1046,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
     };
     // one 16-byte K chunk and one V chunk (K8V3: a half code group's three
     // words) per thread, and the tile's 2 x 32 scales in threads 0..63
+    // (the cache rows of fresh drafts are loaded too, and not used)
     auto load_tile = [&](TileRegs& R, int base) {
       if constexpr (DENSE) {  // fp16 rows of keys base .. base + 31 (clamped to the last key)
 #pragma unroll
@@ -1058,7 +1078,7 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       if (tid < kTile) R.s = __builtin_bit_cast(float, bload32(ks, row_of(base + tid) * 4u));
       else if (tid < 2 * kTile) R.s = __builtin_bit_cast(float, bload32(vs, row_of(base + tid - kTile) * 4u));
     };
-    auto store_tile = [&](const TileRegs& R, int buf) {
+    auto store_tile = [&](const TileRegs& R, int buf, int base) {
       char* kb = smem + buf * C::BUF;
       char* vb = kb + C::KBYTES;
       float* sb = reinterpret_cast<float*>(vb + C::VBYTES);
@@ -1073,11 +1093,45 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         return;
       }
       const int tt = tid >> 3, part = tid & 7;
-      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k[0].x, R.k[0].y});
-      *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k[0].z, R.k[0].w});
-      if constexpr (K8V3) {  // 16 codes of one group -> fp16 codebook entries
+      const int di = fresh_draft(base, tt);
+      if (di >= 0) {  // the draft's fresh values, dims part*16 .. +16: K as fp16 hi + lo, V as it is
+        const float* kp = a.kd + (int64_t)b * a.kd_stride_b + (int64_t)di * a.kd_stride_s +
+                          (int64_t)h * a.kd_stride_h + part * 16;
+        const _Float16* vp = a.vd + (int64_t)b * a.vd_stride_b + (int64_t)di * a.vd_stride_s +
+                             (int64_t)h * a.vd_stride_h + part * 16;
+        half8_t k0, k1, l0, l1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x0 = kp[e], x1 = kp[8 + e];
+          k0[e] = (_Float16)x0;
+          k1[e] = (_Float16)x1;
+          l0[e] = (_Float16)(x0 - (float)k0[e]);
+          l1[e] = (_Float16)(x1 - (float)k1[e]);
+        }
+        char* klo = smem + C::KLO_OFF + buf * C::KBYTES + tt * C::KROW + part * 32;
+        *reinterpret_cast<half8_t*>(klo) = l0;
+        *reinterpret_cast<half8_t*>(klo + 16) = l1;
+        *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = k0;
+        *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = k1;
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = *reinterpret_cast<const half8_t*>(vp);
+        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = *reinterpret_cast<const half8_t*>(vp + 8);
+      } else {
+        if (fresh_tile(base)) {  // a prefix key in a tile holding drafts: no low part
+          char* klo = smem + C::KLO_OFF + buf * C::KBYTES + tt * C::KROW + part * 32;
+          *reinterpret_cast<half8_t*>(klo) = half8_t{};
+          *reinterpret_cast<half8_t*>(klo + 16) = half8_t{};
+        }
+        *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k[0].x, R.k[0].y});
+        *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k[0].z, R.k[0].w});
+        if constexpr (!K8V3) {
+          *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v[0].x, R.v[0].y});
+          *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v[0].z, R.v[0].w});
+        }
+      }
+      if constexpr (K8V3) {  // 16 codes of one group -> fp16 codebook entries (prefix keys)
         const int grp = tid >> 1, half = tid & 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
+        if (fresh_draft(base, gt) < 0) {
         const int sh = half * 16;
         const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
         char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
@@ -1093,14 +1147,14 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
           o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
           *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
         }
-      } else {
-        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v[0].x, R.v[0].y});
-        *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v[0].z, R.v[0].w});
+        }
       }
       // a V scale is staged finite (NaN and inf -> 2^100): the weight of a
       // hidden key, exp2(-inf) * scale, is then 0 whatever was stored there
-      // (clamped here, where the load is consumed, not where it is issued)
-      if (tid < 2 * kTile) sb[tid] = tid < kTile ? R.s : fminf(R.s, 0x1p100f);
+      // (clamped here, where the load is consumed, not where it is issued);
+      // a fresh draft's K and V scales are 1
+      if (tid < 2 * kTile)
+        sb[tid] = fresh_draft(base, tid & (kTile - 1)) >= 0 ? 1.0f : tid < kTile ? R.s : fminf(R.s, 0x1p100f);
     };
 
     // ---- one 32-key tile from LDS buffer `buf` ----
@@ -1121,6 +1175,13 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         for (int m = 0; m < 8; ++m) {
           sc = mfma32x32x16(ka[m], qhi[m], sc);
           if constexpr (!DENSE) sc = mfma32x32x16(ka[m], qlo[m], sc);
+        }
+      }
+      if constexpr (FRESH) {  // fresh draft keys: K = hi + lo
+        if (fresh_tile(base)) {
+          const char* lrow = smem + C::KLO_OFF + buf * C::KBYTES + j * C::KROW + hf * 128;
+#pragma unroll
+          for (int m = 0; m < 8; ++m) sc = mfma32x32x16(*reinterpret_cast<const half8_t*>(lrow + 16 * m), qhi[m], sc);
         }
       }
       // this lane's keys: register r is key 8 (r / 4) + 4 hf + r % 4
@@ -1231,18 +1292,18 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
     TileRegs ra, rb;
     load_tile(ra, u0);
     if (ntiles > 1) load_tile(rb, u0 + kTile);
-    store_tile(ra, 0);
+    store_tile(ra, 0, u0);
     __syncthreads();
     for (int t = 0; t < ntiles; t += 2) {  // (one exit: the accumulators keep their registers)
       const int base = u0 + t * kTile;
       if (t + 2 < ntiles) load_tile(ra, base + 2 * kTile);
       compute(0, base);
-      if (t + 1 < ntiles) store_tile(rb, 1);
+      if (t + 1 < ntiles) store_tile(rb, 1, base + kTile);
       __syncthreads();
       if (t + 1 < ntiles) {
         if (t + 3 < ntiles) load_tile(rb, base + 3 * kTile);
         compute(1, base + kTile);
-        if (t + 2 < ntiles) store_tile(ra, 0);
+        if (t + 2 < ntiles) store_tile(ra, 0, base + 2 * kTile);
         __syncthreads();
       }
     }
@@ -1290,13 +1351,12 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
   }
 }
 
+// The wide kernel serves the paged head_dim-128 calls whose tensors fit
+// 32-bit offsets (no per-tile descriptor rebasing), with or without a window.
 // Query rows per workgroup at this head_dim and layout (Cfg<D, K8V3>::ROWS,
 // or WideCfg::ROWS for the wide kernel), and the workgroups a CU keeps
-// resident (the kernels' launch bounds).  The wide kernel serves the paged
-// head_dim-128 calls without a window whose tensors fit 32-bit offsets.
-// the wide kernel: head_dim 128, no per-tile descriptor rebasing (a cache
-// under 4 GiB), and no fresh drafts (their rows are read by the 16-row kernel)
-static bool use_wide(int head_dim, bool fresh_drafts, bool big) { return head_dim == 128 && !fresh_drafts && !big; }
+// resident (the kernels' launch bounds).
+static bool use_wide(int head_dim, bool big) { return head_dim == 128 && !big; }
 static int rows_per_wg(int head_dim, bool k8v3, bool wide = false) {
   if (wide) return WideCfg<false>::ROWS;
   return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1);
@@ -1414,13 +1474,14 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
                  : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
-template <bool K8V3, bool DENSE = false, bool WIN = false>
+template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
 static int launch_wide(VerifyArgs& a, hipStream_t stream) {
   using C = WideCfg<K8V3>;
+  constexpr int smem = FRESH ? C::SMEM_WIN : C::SMEM;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE, WIN>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM) != hipSuccess) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE, WIN, FRESH>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
     }
@@ -1432,7 +1493,7 @@ static int launch_wide(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE, WIN>), dim3((unsigned)grid), dim3(C::THREADS), C::SMEM, stream,
+  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE, WIN, FRESH>), dim3((unsigned)grid), dim3(C::THREADS), smem, stream,
                      a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
@@ -1547,7 +1608,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
                         const int8_t* k_cache, const float* k_scale, int64_t num_blocks, int block_size,
                         const int32_t* block_table, int64_t block_table_stride, const int32_t* prefix_lens,
                         const int32_t* query_lens, const int64_t* tree_mask, int max_context_len, float scale,
-                        void* out, bool k8v3, bool fresh_drafts) {
+                        void* out, bool k8v3) {
   S8KV_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0, S8KV_ERR_INVALID,
                "verify: num_q_heads %d not a multiple of num_kv_heads %d", num_q_heads, num_kv_heads);
   S8KV_REQUIRE(num_q_heads / num_kv_heads <= 16, S8KV_ERR_UNSUPPORTED, "verify: more than 16 q heads per kv head");
@@ -1587,7 +1648,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, fresh_drafts, a.big));
+  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, a.big));
   a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
@@ -1609,10 +1670,10 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false, fresh_k);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, false);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  const bool wide = verify::use_wide(head_dim, fresh_k, a.big);
+  const bool wide = verify::use_wide(head_dim, a.big);
   if (const int rc = verify_use_workspace(a, head_dim, false, wide, workspace, workspace_bytes)) return rc;
   if (fresh_k) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
@@ -1637,7 +1698,10 @@ static int verify_int8_impl(const void* q, int batch, int num_q_heads, int num_k
   a.vc_bytes = a.kc_bytes;
   a.vs_bytes = a.ks_bytes;
   hipStream_t s = (hipStream_t)stream;
-  if (wide) return a.window > 0 ? verify::launch_wide<false, false, true>(a, s) : verify::launch_wide<false>(a, s);
+  if (wide) {
+    if (a.kd != nullptr) return verify::launch_wide<false, false, true, true>(a, s);
+    return a.window > 0 ? verify::launch_wide<false, false, true>(a, s) : verify::launch_wide<false>(a, s);
+  }
   if (a.window > 0) {
     switch (head_dim) {
       case 64: return verify::launch<64, false, true>(a, s);
@@ -1704,10 +1768,10 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.splits = 1;
   const int rc = verify_setup(a, q, batch, num_q_heads, num_kv_heads, head_dim, max_queries, q_stride_b, q_stride_h,
                               q_stride_s, k_cache, k_scale, num_blocks, block_size, block_table, block_table_stride,
-                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true, fresh_k);
+                              prefix_lens, query_lens, tree_mask, max_context_len, scale, out, true);
   if (rc != S8KV_OK) return rc;
   a.window = window;
-  const bool wide = verify::use_wide(head_dim, fresh_k, a.big);
+  const bool wide = verify::use_wide(head_dim, a.big);
   if (const int rc = verify_use_workspace(a, head_dim, true, wide, workspace, workspace_bytes)) return rc;
   if (fresh_k) {
     S8KV_REQUIRE(fresh->v != nullptr && window > 0, S8KV_ERR_INVALID, "verify: fresh drafts need V and a window");
@@ -1734,7 +1798,10 @@ static int verify_k8v3_impl(const void* q, int batch, int num_q_heads, int num_k
   a.vc_bytes = cap_u32(a.vc_total);
   a.vs_bytes = cap_u32(a.vs_total);
   hipStream_t s = (hipStream_t)stream;
-  if (wide) return a.window > 0 ? verify::launch_wide<true, false, true>(a, s) : verify::launch_wide<true>(a, s);
+  if (wide) {
+    if (a.kd != nullptr) return verify::launch_wide<true, false, true, true>(a, s);
+    return a.window > 0 ? verify::launch_wide<true, false, true>(a, s) : verify::launch_wide<true>(a, s);
+  }
   if (a.window > 0)
     return head_dim == 128 ? verify::launch<128, true, true>(a, s) : verify::launch<256, true, true>(a, s);
   return head_dim == 128 ? verify::launch<128, true>(a, s) : verify::launch<256, true>(a, s);

@@ -255,6 +255,9 @@ def _drafts(case, pre, nq):
     (False, 8, 2, 256, 256, [777, 64], 40, 100),
     (True, 8, 2, 128, 16, [1000, 130], 9, 129),
     (True, 4, 2, 256, 16, [700, 260], 4, 70),
+    (False, 32, 8, 128, 16, [3000, 500, 45], 40, 1024),  # drafts across tiles, two 128-row blocks
+    (True, 32, 8, 128, 256, [2100, 64], 33, 512),
+    (False, 64, 4, 128, 32, [2500, 31], 12, 700),        # G = 16, a prefix shorter than a tile
 ])
 def test_window_verify_with_fresh_drafts(k8v3, hq, hkv, d, bs, prefix, nq, window):
     """The reference's window verify attends the prefix window read back from
@@ -278,6 +281,33 @@ def test_window_verify_with_fresh_drafts(k8v3, hq, hkv, d, bs, prefix, nq, windo
     ref = O.paged_verify(q, layer, case.block_table, pre, case.scale, window=window, fresh_drafts=(kd, vd))
     _close(got, ref, f"verify window {window} with fresh drafts")
     assert not np.array_equal(got, _verify(case, cache, q, pre, window, k8v3))
+
+
+@pytest.mark.parametrize("k8v3", [False, True])
+def test_window_tree_verify_with_fresh_drafts(k8v3):
+    """Tree masks over fresh drafts (ancestor bits select the visible drafts)."""
+    nq = 24
+    case, cache, q, pre = _verify_case(731, 3, 16, 4, 128, 16, [1500, 600, 90], nq, k8v3)
+    rng = np.random.default_rng(732)
+    masks = np.zeros((3, nq), np.int64)
+    for b in range(3):
+        for i in range(nq):
+            par = int(rng.integers(-1, i)) if i else -1
+            masks[b, i] = (masks[b, par] if par >= 0 else 0) | (1 << i)
+    kd, vd = _drafts(case, pre, nq)
+    c = [_t(x) for x in cache]
+    kw = dict(max_context_len=int(case.block_table.shape[1] * case.block_size), scale=case.scale, window=400,
+              tree_mask=_t(masks), k_draft=_t(kd), v_draft=_t(vd))
+    bt, pl = _t(case.block_table), _t(pre.astype(np.int32))
+    if k8v3:
+        out = ops.attn_paged_verify_k8v3(_t(q), *c, _t(CODEBOOK), bt, pl, case.block_size, **kw)
+    else:
+        out = ops.attn_paged_verify(_t(q), *c, bt, pl, case.block_size, **kw)
+    layer = O.LayerCache(cache[0], cache[1], v_packed=cache[2], v_norm=cache[3], v_codebook=CODEBOOK) if k8v3 \
+        else O.LayerCache(*cache)
+    ref = O.paged_verify(q, layer, case.block_table, pre, case.scale, tree_mask=masks, window=400,
+                         fresh_drafts=(kd, vd))
+    _close(out.float().cpu().numpy(), ref, "tree verify window 400 with fresh drafts")
 
 
 def test_fresh_drafts_need_a_window():
