@@ -115,6 +115,27 @@ def test_split_window_verify(kind, force_splits):
 
 
 @pytest.mark.parametrize("kind", ["int8", "k8v3"])
+def test_split_window_verify_with_fresh_drafts(kind, force_splits):
+    """A window verify whose drafts come fresh (fp16 K / V rows, not the
+    cache's) split into 5 key ranges: the drafts' tiles sit in the last
+    ranges, and the result matches the oracle in that mode."""
+    nq = 37
+    case, cache, host, qv, prefix = _case(965, kind, 16, 4, 128, 16, [4000, 700], nq)
+    starts = np.concatenate([[0], np.cumsum(case.lens)])
+    idx = np.stack([starts[b] + prefix[b] + np.arange(nq) for b in range(len(prefix))])
+    kd, vd = case.k[idx], case.v[idx]
+    force_splits("5")
+    fn = ops.attn_paged_verify if kind == "int8" else ops.attn_paged_verify_k8v3
+    extra = () if kind == "int8" else (t(CODEBOOK),)
+    out = fn(t(qv), *cache, *extra, t(case.block_table), t(prefix.astype(np.int32)), case.block_size,
+             max_context_len=int(case.lens.max()), scale=case.scale, window=900, k_draft=t(kd), v_draft=t(vd))
+    torch.cuda.synchronize()
+    ref = O.paged_verify(qv, layer(kind, host), case.block_table, prefix, case.scale, window=900,
+                         fresh_drafts=(kd, vd))
+    assert_close(to_np(out.float()), ref, f"{kind} window verify with fresh drafts, 5 splits")
+
+
+@pytest.mark.parametrize("kind", ["int8", "k8v3"])
 def test_batch_one_long_context_plans_a_split(kind):
     """Batch 1 with a 32K prefix and a 32-node tree at Qwen3-8B heads has 16
     units (8 for K8V3, whose workgroups hold 128 query rows): the default
