@@ -1132,21 +1132,21 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         const int grp = tid >> 1, half = tid & 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
         if (fresh_draft(base, gt) < 0) {
-        const int sh = half * 16;
-        const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
-        char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
+          const int sh = half * 16;
+          const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
+          char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; q4 += 2) {
-          u32x4_t o;
-          const uint32_t sel0 =
-              spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
-          const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
-                                (spread4(w2 >> (4 * q4 + 4)) << 2);
-          const u32x2_t r0 = codebook_lookup4(sel0, tlo03, tlo47, thi03, thi47);
-          const u32x2_t r1 = codebook_lookup4(sel1, tlo03, tlo47, thi03, thi47);
-          o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
-          *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
-        }
+          for (int q4 = 0; q4 < 4; q4 += 2) {
+            u32x4_t o;
+            const uint32_t sel0 =
+                spread4(w0 >> (4 * q4)) | (spread4(w1 >> (4 * q4)) << 1) | (spread4(w2 >> (4 * q4)) << 2);
+            const uint32_t sel1 = spread4(w0 >> (4 * q4 + 4)) | (spread4(w1 >> (4 * q4 + 4)) << 1) |
+                                  (spread4(w2 >> (4 * q4 + 4)) << 2);
+            const u32x2_t r0 = codebook_lookup4(sel0, tlo03, tlo47, thi03, thi47);
+            const u32x2_t r1 = codebook_lookup4(sel1, tlo03, tlo47, thi03, thi47);
+            o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+            *reinterpret_cast<u32x4_t*>(dst + q4 * 8) = o;
+          }
         }
       }
       // a V scale is staged finite (NaN and inf -> 2^100): the weight of a
