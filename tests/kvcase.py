@@ -167,16 +167,17 @@ def needle_fill(nc: NeedleCase):
     return kc, ks, vc, vs
 
 
-def needle_reference(nc: NeedleCase, limit: int) -> np.ndarray:
+def needle_reference(nc: NeedleCase, limit: int, start: int = 0) -> np.ndarray:
     """Closed-form float64 attention ``[Hq, D]`` of ``nc.q`` over positions
-    ``[0, limit)``: each background token weighs ``e^0`` with V ``u``, each
-    visible needle ``e^s`` with its own V."""
+    ``[start, limit)``: each background token weighs ``e^0`` with V ``u``,
+    each visible needle ``e^s`` with its own V."""
     h = O.hadamard_matrix(nc.head_dim)
     k = (nc.k_i8.astype(np.float64) * nc.k_scale.astype(np.float64)[:, None]) @ h
     v = nc.v_i8.astype(np.float64) * nc.v_scale.astype(np.float64)[:, None]
     s = nc.scale * nc.q.astype(np.float64) @ k.T
-    s = np.where(nc.pos[None, :] < limit, s, -np.inf)
-    n_bg = limit - int((nc.pos < limit).sum())
+    seen = (nc.pos >= start) & (nc.pos < limit)
+    s = np.where(seen[None, :], s, -np.inf)
+    n_bg = (limit - start) - int(seen.sum())
     mx = np.maximum(s.max(axis=1, keepdims=True), 0.0)
     w = np.exp(s - mx)
     wb = n_bg * np.exp(-mx)

@@ -326,6 +326,30 @@ def test_decode_through_a_whole_pool(pool):
 
 
 @pytest.mark.parametrize("pool", sorted(WHOLE_POOLS))
+def test_window_verify_through_a_whole_pool(pool):
+    """The same chain verify with a window of a third of the sequence: query
+    s sees positions [n - 4 - window, n - 4 + s], with needles on both sides
+    of the window start (the 32-row kernel under 4 GiB, the 16-row kernel
+    with descriptors rebased per tile at 6 GiB)."""
+    nc, cache = _whole_pool(WHOLE_POOLS[pool])
+    try:
+        kc, ks, vc, vs = cache
+        n, d, bs, hq, nq = nc.n, nc.head_dim, nc.block_size, len(nc.pos), 4
+        window = n // 3
+        lo = n - nq - window
+        assert (nc.pos < lo).any() and (nc.pos >= lo).any(), "needles on both sides of the window start"
+        qv = np.ascontiguousarray(np.broadcast_to(nc.q[:, None, :], (hq, nq, d)))
+        got = to_np(ops.attn_paged_verify(t(qv[None]), kc, ks, vc, vs, t(nc.block_table[None]),
+                                          t(np.array([n - nq], np.int32)), bs, max_context_len=n,
+                                          scale=nc.scale, window=window).float())[0]
+        for s in range(nq):
+            assert_close(got[:, s], needle_reference(nc, n - nq + s + 1, start=lo), f"whole-pool window verify {s}")
+    finally:
+        cache.clear()
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("pool", sorted(WHOLE_POOLS))
 def test_chain_verify_through_a_whole_pool(pool):
     """A 4-query chain verify of the whole-pool sequence's last positions:
     query s sees positions [0, n - 4 + s].  The single query block's 33.5M

@@ -32,6 +32,13 @@ def test_needle_closed_form_matches_oracle(nblk, bs, d, hq):
     ver = O.paged_verify(qv, layer, bt, np.array([n - nq]), nc.scale)[0]
     for s in range(nq):
         np.testing.assert_allclose(needle_reference(nc, n - nq + s + 1), ver[:, s], rtol=1e-10, atol=1e-12)
+    # a window verify: positions [n - nq - window, n - nq + s] (some needles outside the window)
+    window = n // 3
+    wver = O.paged_verify(qv, layer, bt, np.array([n - nq]), nc.scale, window=window)[0]
+    for s in range(nq):
+        np.testing.assert_allclose(needle_reference(nc, n - nq + s + 1, start=n - nq - window), wver[:, s],
+                                   rtol=1e-10, atol=1e-12)
+    assert ((nc.pos < n - nq - window).any() and (nc.pos >= n - nq - window).any()), "needles on both sides"
 
 
 def test_needle_reference_detects_a_missing_needle():
