@@ -310,6 +310,38 @@ def test_window_tree_verify_with_fresh_drafts(k8v3):
     _close(out.float().cpu().numpy(), ref, "tree verify window 400 with fresh drafts")
 
 
+@pytest.mark.parametrize("k8v3", [False, True])
+def test_window_verify_fresh_drafts_query_lens(k8v3):
+    """Rows with fewer drafts than the call's S (query_lens, one row with
+    none): their queries past the count are zeros and the drafts past it are
+    never read (NaN there changes nothing); the live rows match the oracle."""
+    nq = 20
+    ql = np.array([20, 7, 0, 13], np.int32)
+    case, cache, q, pre = _verify_case(741, 4, 16, 4, 128, 16, [900, 2500, 300, 64], nq, k8v3)
+    kd, vd = _drafts(case, pre, nq)
+    kd, vd = kd.copy(), vd.copy()
+    for b, n in enumerate(ql):
+        kd[b, n:] = np.nan
+        vd[b, n:] = np.nan
+    c = [_t(x) for x in cache]
+    kw = dict(max_context_len=int(case.block_table.shape[1] * case.block_size), scale=case.scale, window=600,
+              query_lens=_t(ql), k_draft=_t(kd), v_draft=_t(vd))
+    bt, pl = _t(case.block_table), _t(pre.astype(np.int32))
+    if k8v3:
+        out = ops.attn_paged_verify_k8v3(_t(q), *c, _t(CODEBOOK), bt, pl, case.block_size, **kw)
+    else:
+        out = ops.attn_paged_verify(_t(q), *c, bt, pl, case.block_size, **kw)
+    got = out.float().cpu().numpy()
+    for b, n in enumerate(ql):
+        assert not got[b, :, n:].any(), f"row {b}: outputs past its {n} queries"
+    layer = O.LayerCache(cache[0], cache[1], v_packed=cache[2], v_norm=cache[3], v_codebook=CODEBOOK) if k8v3 \
+        else O.LayerCache(*cache)
+    clean_k, clean_v = _drafts(case, pre, nq)
+    ref = O.paged_verify(q, layer, case.block_table, pre, case.scale, query_lens=ql, window=600,
+                         fresh_drafts=(clean_k, clean_v))
+    _close(got, ref, "window verify with fresh drafts and query_lens")
+
+
 def test_fresh_drafts_need_a_window():
     case, cache, q, pre = _verify_case(711, 1, 8, 2, 128, 16, [100], 4)
     kd, vd = _drafts(case, pre, 4)
