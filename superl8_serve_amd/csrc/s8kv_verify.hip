@@ -1365,10 +1365,10 @@ static int wg_per_cu(bool k8v3, bool wide = false) { return wide ? 2 : (k8v3 ? 1
 
 // Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
 // KV head, query block) merges the row's `splits` partials -- each relative to
-// its own running max, so weighted by 2^(m_s - max_s m_s) -- and writes the
+// its own running max, so weighted by 2^(m_s - max m) -- and writes the
 // normalized fp16 dims.  Workgroup x covers items kCombineThreads * (x %
 // blocks_per_unit) .. of unit x / blocks_per_unit.
-constexpr int kCombineThreads = 256;
+constexpr int kCombineThreads = 64;  // one wave: a batch-1 combine spreads over every CU
 template <int D, int ROWS>
 __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyArgs a) {
   constexpr int V4 = D / 4;
@@ -1398,15 +1398,10 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
   const int S = a.splits;
   const int64_t stride = (int64_t)ROWS * (D + 4);  // between splits of one row
   const float* row = a.part + ((int64_t)pq * S * ROWS + rl) * (D + 4);
-  constexpr int U = 8;  // partials in flight
+  // one pass, 32 partials in flight: the running max rises batch by batch and
+  // rescales what is summed so far (a split count of 64 reads in 2 rounds)
+  constexpr int U = 32;
   float M = -__builtin_inff();
-  for (int s0 = 0; s0 < S; s0 += U) {
-    float m[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) m[u] = s0 + u < S ? row[(s0 + u) * stride + D] : -__builtin_inff();
-#pragma unroll
-    for (int u = 0; u < U; ++u) M = fmaxf(M, m[u]);
-  }
   float4_t num = float4_t{0.f, 0.f, 0.f, 0.f};
   float den = 0.0f;
   for (int s0 = 0; s0 < S; s0 += U) {
@@ -1420,12 +1415,19 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
       l[u] = pr[D + 1];
       x[u] = *reinterpret_cast<const float4_t*>(pr + 4 * c4);
     }
+    float mb = M;  // (partial maxima are finite: a split without keys keeps its initial max)
+#pragma unroll
+    for (int u = 0; u < U; ++u) mb = s0 + u < S ? fmaxf(mb, m[u]) : mb;
+    const float c = __builtin_amdgcn_exp2f(M - mb);  // 0 on the first batch
+    num *= c;
+    den *= c;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float f = s0 + u < S ? __builtin_amdgcn_exp2f(m[u] - M) : 0.0f;
+      const float f = s0 + u < S ? __builtin_amdgcn_exp2f(m[u] - mb) : 0.0f;
       num += f * x[u];
       den += f * l[u];
     }
+    M = mb;
   }
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
   half4_t o;
@@ -1525,10 +1527,12 @@ struct FreshDrafts {
 // the GPU keeps resident (two per CU) leaves CUs idle for the whole call --
 // batch-1 speculative decoding with a long context is the common case -- so
 // each (sequence, KV head, query block) is split until about that many
-// exist, down to kMinSplitKeys keys per split; and one workgroup never
-// accumulates more than kMaxSplitKeys keys, which bounds the rounding of its
-// fp32 sums.  s8kv_verify_set_splits overrides the count (diagnostics).
-constexpr int kMinSplitKeys = 1024;
+// exist, down to kMinSplitKeys keys per split (512: a 32K-key batch-1 tree
+// verify at 8 KV heads fills all 512 slots, 4-5 % faster than 32 splits of
+// 1024 keys; a second round of splits is slower again); and one workgroup
+// never accumulates more than kMaxSplitKeys keys, which bounds the rounding
+// of its fp32 sums.  s8kv_verify_set_splits overrides the count (diagnostics).
+constexpr int kMinSplitKeys = 512;
 constexpr int kMaxSplitKeys = 1 << 20;
 constexpr int kMaxSplits = 1024;
 static std::atomic<int> g_verify_splits{0};  // 0: planned per call
