@@ -137,10 +137,10 @@ def test_split_window_verify_with_fresh_drafts(kind, force_splits):
 
 @pytest.mark.parametrize("kind", ["int8", "k8v3"])
 def test_batch_one_long_context_plans_a_split(kind):
-    """Batch 1 with a 32K prefix and a 32-node tree at Qwen3-8B heads has 16
-    units (8 for K8V3, whose workgroups hold 128 query rows): the default
-    plan splits them within the workspace the size query gives for either
-    layout, and the result matches the oracle."""
+    """Batch 1 with a 32K prefix and a 32-node tree at Qwen3-8B heads has 8
+    units (one 128-row query block per KV head): the default plan splits
+    each into 64 key ranges of 512 keys within the workspace the size query
+    gives, and the combined result matches the oracle."""
     nq = 32
     ws = _lib.load().s8kv_verify_workspace_size(1, 32, 8, 128, nq, 32768 + nq)
     assert ws > 0
