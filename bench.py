@@ -285,14 +285,34 @@ def _time_graph(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e-3 / max(steps, 1)
 
 
-def _spin_ahead() -> None:
+def _spin_ahead(warm=None, per_call_s: float = 0.0, warm_s: float = 0.03) -> None:
     """Keep the GPU ahead of the host for an eager timed loop: a ~0.1 s spin
     kernel runs while the host enqueues the timed calls, so host launch
     overhead never opens a gap between them (the start event, recorded
-    after the spin, is stamped when the spin ends)."""
+    after the spin, is stamped when the spin ends).  The spin is one wave,
+    so the engine clock may fall while it runs: with `warm` (a call of the
+    timed workload, ~per_call_s of GPU time) about warm_s of untimed calls
+    follow it, so the timed calls start at the clock a busy GPU holds."""
     import torch
 
     torch.cuda._sleep(int(2e8))
+    if warm is not None and per_call_s > 0:
+        for i in range(min(4000, max(1, math.ceil(warm_s / per_call_s)))):
+            warm(i)
+
+
+def _timed_warmup(fn, calls: int) -> float:
+    """Run `calls` untimed calls fn(i) and return their GPU seconds per call
+    (HIP events; the first timing pass of a process warms the clocks too)."""
+    import torch
+
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(calls):
+        fn(i)
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) * 1e-3 / max(calls, 1)
 
 
 def read_ceiling(w, steps: int) -> dict:
@@ -621,19 +641,18 @@ def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
         return ops.attn_paged_verify(w["q"][layer], w["kc"][layer], w["ks"][layer], w["vc"][layer], w["vs"][layer],
                                      w["bt"], w["prefix"], BS, **kw)
 
-    for i in range(warmup * VERIFY_LAYERS):
-        layer_ops(i % VERIFY_LAYERS)
-    torch.cuda.synchronize()
+    per_call = _timed_warmup(lambda i: layer_ops(i % VERIFY_LAYERS), max(warmup, 1) * VERIFY_LAYERS)
+    warm = lambda i: layer_ops(i % VERIFY_LAYERS, append=False)  # noqa: E731
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # attention alone
-    _spin_ahead()
+    _spin_ahead(warm, per_call)
     st.record()
     for i in range(steps * VERIFY_LAYERS):
         layer_ops(i % VERIFY_LAYERS, append=False)
     en.record()
     torch.cuda.synchronize()
     t_attn = st.elapsed_time(en) * 1e-3 / (steps * VERIFY_LAYERS)
-    _spin_ahead()
+    _spin_ahead(warm, per_call)
     st.record()
     for i in range(steps * VERIFY_LAYERS):
         layer_ops(i % VERIFY_LAYERS)
@@ -649,7 +668,7 @@ def run_verify(kind: str, steps: int, warmup: int, k8v3: bool = False) -> None:
         from superl8_serve_amd import _lib
 
         _lib.check(_lib.load().s8kv_verify_set_splits(1), "s8kv_verify_set_splits")
-        _spin_ahead()
+        _spin_ahead(warm, _timed_warmup(warm, 2))
         st.record()
         for i in range(steps * VERIFY_LAYERS):
             layer_ops(i % VERIFY_LAYERS, append=False)
@@ -910,11 +929,9 @@ def run_prefill(steps: int, warmup: int) -> None:
         q, k, v = layers[i % 4]
         return ops.attn_varlen(q, k, v, cu, cu, PREFILL_LEN, PREFILL_LEN, causal=True, scale=scale)
 
-    for i in range(warmup * 4):
-        attend(i)
-    torch.cuda.synchronize()
+    per_call = _timed_warmup(attend, max(warmup, 1) * 4)
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _spin_ahead()
+    _spin_ahead(attend, per_call)
     st.record()
     for i in range(steps * 4):
         attend(i)
