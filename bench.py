@@ -1071,7 +1071,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed steps first (50 graph replays of the decode step take ~0.12 s; with 5 the "
+                         "timed steps start before the engine clock settles and read ~1 %% lower)")
     ap.add_argument("--cpu-layers", type=int, default=NUM_LAYERS, help="layers in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per decode launch (from the PMC runs) to report as roofline.traffic")
