@@ -1010,11 +1010,9 @@ def run_window(steps: int, warmup: int) -> None:
         return ops.attn_paged_decode_window(q, kc, ks, vc, vs, btd, cl, BS, max_context_len=width * BS,
                                             window=WINDOW, scale=scale)
 
-    for i in range(warmup * WINDOW_LAYERS):
-        attend(i)
-    torch.cuda.synchronize()
+    per_call = _timed_warmup(attend, max(warmup, 1) * WINDOW_LAYERS)
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _spin_ahead()
+    _spin_ahead(attend, per_call)
     st.record()
     for i in range(steps * WINDOW_LAYERS):
         attend(i)
