@@ -1095,14 +1095,15 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
       const int tt = tid >> 3, part = tid & 7;
       const int di = fresh_draft(base, tt);
       if (di >= 0) {  // the draft's fresh values, dims part*16 .. +16: K as fp16 hi + lo, V as it is
-        const float* kp = a.kd + (int64_t)b * a.kd_stride_b + (int64_t)di * a.kd_stride_s +
-                          (int64_t)h * a.kd_stride_h + part * 16;
+        const float4_t* kp = reinterpret_cast<const float4_t*>(
+            a.kd + (int64_t)b * a.kd_stride_b + (int64_t)di * a.kd_stride_s + (int64_t)h * a.kd_stride_h + part * 16);
         const _Float16* vp = a.vd + (int64_t)b * a.vd_stride_b + (int64_t)di * a.vd_stride_s +
                              (int64_t)h * a.vd_stride_h + part * 16;
+        const float4_t kx[4] = {kp[0], kp[1], kp[2], kp[3]};  // (rows 16-byte aligned: checked on the host)
         half8_t k0, k1, l0, l1;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float x0 = kp[e], x1 = kp[8 + e];
+          const float x0 = kx[e >> 2][e & 3], x1 = kx[2 + (e >> 2)][e & 3];
           k0[e] = (_Float16)x0;
           k1[e] = (_Float16)x1;
           l0[e] = (_Float16)(x0 - (float)k0[e]);
@@ -1436,6 +1437,19 @@ __global__ __launch_bounds__(kCombineThreads) void verify_combine_kernel(VerifyA
   *op = o;
 }
 
+// The combine of a split call: one single-wave workgroup per 64 (row, 4 dims)
+// items of every unit.
+template <int D, int ROWS>
+static int launch_combine(VerifyArgs& a, int64_t units, hipStream_t stream) {
+  const int64_t grid = units * (ROWS * (D / 4) / kCombineThreads);
+  if (grid > INT32_MAX) {
+    set_error("s8kv_verify: combine grid too large");
+    return S8KV_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((verify_combine_kernel<D, ROWS>), dim3((unsigned)grid), dim3(kCombineThreads), 0, stream, a);
+  return check_launch("s8kv_verify_combine");
+}
+
 template <int D, bool K8V3, bool WIN, bool DENSE, bool BIG>
 static int launch_impl(VerifyArgs& a, hipStream_t stream) {
   static_assert(Cfg<D, K8V3>::ROWS == 16 * kWavesOf<K8V3> * (D <= 64 ? 2 : 1), "rows_per_wg");
@@ -1460,10 +1474,7 @@ static int launch_impl(VerifyArgs& a, hipStream_t stream) {
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
-    const int64_t units = (int64_t)P * a.n_qblocks;
-    hipLaunchKernelGGL((verify_combine_kernel<D, C::ROWS>), dim3((unsigned)(units * (C::ROWS * (D / 4) / kCombineThreads))),
-                       dim3(kCombineThreads), 0, stream, a);
-    return check_launch("s8kv_verify_combine");
+    return launch_combine<D, C::ROWS>(a, (int64_t)P * a.n_qblocks, stream);
   }
   return check_launch("s8kv_verify");
 }
@@ -1500,11 +1511,7 @@ static int launch_wide(VerifyArgs& a, hipStream_t stream) {
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
-    const int64_t units = (int64_t)P * a.n_qblocks;
-    hipLaunchKernelGGL((verify_combine_kernel<C::D, C::ROWS>),
-                       dim3((unsigned)(units * (C::ROWS * (C::D / 4) / kCombineThreads))), dim3(kCombineThreads), 0,
-                       stream, a);
-    return check_launch("s8kv_verify_combine");
+    return launch_combine<C::D, C::ROWS>(a, (int64_t)P * a.n_qblocks, stream);
   }
   return check_launch("s8kv_verify");
 }
