@@ -837,7 +837,10 @@ __device__ __forceinline__ void split_pair(float w0, float w1, uint32_t& hi, uin
 template <bool K8V3>
 struct WideCfg {
   static constexpr int D = 128;
-  static constexpr int WAVES = 4;
+  // K8V3: 8 waves (256 query rows) per workgroup, one workgroup per CU, so
+  // twice the rows share each tile's code expansion; int8: 4 waves, two per CU
+  static constexpr int WAVES = K8V3 ? 8 : 4;
+  static constexpr int WG_PER_CU = 8 / WAVES;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int ROWS = 32 * WAVES;  // query rows per workgroup
   static constexpr int KROW = 2 * D + 16;  // LDS pitch of an fp16 K row (8 consecutive rows: distinct 16-byte slots)
@@ -847,11 +850,11 @@ struct WideCfg {
   static constexpr int SBYTES = 2 * kTile * 4;  // k_scale, then the V scale (int8) or block norm (K8V3) per key
   static constexpr int BUF = KBYTES + VBYTES + SBYTES;
   static constexpr int CHUNKS = kTile * D / 16;  // 16-byte int8 chunks per K (or V) tile: one per thread
-  static_assert(CHUNKS == THREADS, "one K chunk and one V chunk per thread");
+  static_assert(CHUNKS == 256, "one K chunk per thread of the first 256 (and one V chunk per thread of the last)");
   static constexpr int NG = D / 32;      // K8V3: 32-value code groups per key
   static constexpr int WORDS = 3 * NG;   // K8V3: packed words per key
   static constexpr int VJOBS = 2 * kTile * NG;  // K8V3: two threads per code group (16 values each)
-  static_assert(VJOBS == THREADS, "one K8V3 expansion job per thread");
+  static_assert(VJOBS == 256, "one K8V3 expansion job per thread of the last 256");
   static constexpr int SMEM = 2 * BUF + kMaxSubBlocks * 4;
   // window verify with fresh drafts: the low fp16 part of the drafts' K per buffer
   static constexpr int KLO_OFF = (SMEM + 15) / 16 * 16;
@@ -866,7 +869,7 @@ struct WideCfg {
 // prefix - window, the drafts' K / V from the cache or (FRESH, a.kd set) from
 // the fresh fp32 K (rotated) and fp16 V rows of the drafts.
 template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
-__global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
+__global__ __launch_bounds__(WideCfg<K8V3>::THREADS, WideCfg<K8V3>::WG_PER_CU) void verify_wide_kernel(VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
   static_assert(!FRESH || (WIN && !DENSE), "fresh drafts: a paged window verify");
   using C = WideCfg<K8V3>;
@@ -1059,11 +1062,17 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         R.s = 1.0f;
         return;
       }
-      const int tt = tid >> 3, part = tid & 7;
+      // 4 waves: every thread one K and one V chunk; 8 waves: threads 0..255
+      // the K chunks, 256..511 the V chunks (vt: the V job index)
+      constexpr bool SPLITKV = C::WAVES == 8;
+      const bool kthr = !SPLITKV || tid < 256, vthr = !SPLITKV || tid >= 256;
+      const int vt = tid & 255;
+      const int tt = tid >> 3 & 31, part = tid & 7;
       const uint32_t row = row_of(base + tt);
-      R.k[0] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
-      if constexpr (K8V3) {
-        const int grp = tid >> 1;
+      if (kthr) R.k[0] = bload128(kc, row * (uint32_t)D + (uint32_t)part * 16u);
+      if (!vthr) {
+      } else if constexpr (K8V3) {
+        const int grp = vt >> 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
         const uint32_t off = row_of(base + gt) * (uint32_t)(C::WORDS * 4) + (uint32_t)gi * 12u;
         const u32x3_t w = bload96(vc, off);
@@ -1092,9 +1101,13 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         if (tid < 2 * kTile) sb[tid] = tid < kTile ? a.qscale : 1.0f;
         return;
       }
-      const int tt = tid >> 3, part = tid & 7;
-      const int di = fresh_draft(base, tt);
-      if (di >= 0) {  // the draft's fresh values, dims part*16 .. +16: K as fp16 hi + lo, V as it is
+      constexpr bool SPLITKV = C::WAVES == 8;
+      const bool kthr = !SPLITKV || tid < 256, vthr = !SPLITKV || tid >= 256;
+      const int vt = tid & 255;
+      const int tt = tid >> 3 & 31, part = tid & 7;
+      const int di = kthr ? fresh_draft(base, tt) : -1;
+      if (!kthr) {
+      } else if (di >= 0) {  // the draft's fresh values, dims part*16 .. +16: K as fp16 hi + lo, V as it is
         const float4_t* kp = reinterpret_cast<const float4_t*>(
             a.kd + (int64_t)b * a.kd_stride_b + (int64_t)di * a.kd_stride_s + (int64_t)h * a.kd_stride_h + part * 16);
         const _Float16* vp = a.vd + (int64_t)b * a.vd_stride_b + (int64_t)di * a.vd_stride_s +
@@ -1130,9 +1143,9 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
         }
       }
       if constexpr (K8V3) {  // 16 codes of one group -> fp16 codebook entries (prefix keys)
-        const int grp = tid >> 1, half = tid & 1;
+        const int grp = vt >> 1, half = vt & 1;
         const int gt = grp / C::NG, gi = grp % C::NG;
-        if (fresh_draft(base, gt) < 0) {
+        if (vthr && fresh_draft(base, gt) < 0) {
           const int sh = half * 16;
           const uint32_t w0 = R.v[0].x >> sh, w1 = R.v[0].y >> sh, w2 = R.v[0].z >> sh;
           char* dst = vb + gt * C::VROW + gi * 64 + sh * 2;
@@ -1359,10 +1372,12 @@ __global__ __launch_bounds__(256, 2) void verify_wide_kernel(VerifyArgs a) {
 // resident (the kernels' launch bounds).
 static bool use_wide(int head_dim, bool big) { return head_dim == 128 && !big; }
 static int rows_per_wg(int head_dim, bool k8v3, bool wide = false) {
-  if (wide) return WideCfg<false>::ROWS;
+  if (wide) return k8v3 ? WideCfg<true>::ROWS : WideCfg<false>::ROWS;
   return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1);
 }
-static int wg_per_cu(bool k8v3, bool wide = false) { return wide ? 2 : (k8v3 ? 1 : 2); }
+static int wg_per_cu(bool k8v3, bool wide = false) {
+  return wide ? (k8v3 ? WideCfg<true>::WG_PER_CU : WideCfg<false>::WG_PER_CU) : (k8v3 ? 1 : 2);
+}
 
 // Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
 // KV head, query block) merges the row's `splits` partials -- each relative to
