@@ -834,12 +834,14 @@ __device__ __forceinline__ void split_pair(float w0, float w1, uint32_t& hi, uin
   lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(l0, l1));
 }
 
-template <bool K8V3>
+template <bool K8V3, bool EIGHT>
 struct WideCfg {
   static constexpr int D = 128;
-  // K8V3: 8 waves (256 query rows) per workgroup, one workgroup per CU, so
-  // twice the rows share each tile's code expansion; int8: 4 waves, two per CU
-  static constexpr int WAVES = K8V3 ? 8 : 4;
+  // EIGHT (paged calls with more than 128 query rows per sequence and KV
+  // head): 8 waves (256 rows) per workgroup, one workgroup per CU, so twice
+  // the rows share each tile's conversion (K8V3: code expansion); else (and
+  // dense inputs) 4 waves, two per CU
+  static constexpr int WAVES = EIGHT ? 8 : 4;
   static constexpr int WG_PER_CU = 8 / WAVES;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int ROWS = 32 * WAVES;  // query rows per workgroup
@@ -868,11 +870,13 @@ struct WideCfg {
 // every row sees the last `window` prefix keys and the drafts, keys j >=
 // prefix - window, the drafts' K / V from the cache or (FRESH, a.kd set) from
 // the fresh fp32 K (rotated) and fp16 V rows of the drafts.
-template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
-__global__ __launch_bounds__(WideCfg<K8V3>::THREADS, WideCfg<K8V3>::WG_PER_CU) void verify_wide_kernel(VerifyArgs a) {
+template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false, bool EIGHT = false>
+__global__ __launch_bounds__((WideCfg<K8V3, EIGHT>::THREADS), (WideCfg<K8V3, EIGHT>::WG_PER_CU)) void verify_wide_kernel(
+    VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
   static_assert(!FRESH || (WIN && !DENSE), "fresh drafts: a paged window verify");
-  using C = WideCfg<K8V3>;
+  static_assert(!(EIGHT && DENSE), "dense inputs: 4-wave workgroups");
+  using C = WideCfg<K8V3, EIGHT>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* bt_lds = reinterpret_cast<int*>(smem + 2 * C::BUF);
@@ -1137,7 +1141,11 @@ __global__ __launch_bounds__(WideCfg<K8V3>::THREADS, WideCfg<K8V3>::WG_PER_CU) v
         }
         *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32) = i8x8_to_f16(u32x2_t{R.k[0].x, R.k[0].y});
         *reinterpret_cast<half8_t*>(kb + tt * C::KROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.k[0].z, R.k[0].w});
-        if constexpr (!K8V3) {
+      }
+      // int8 V rows: by the V threads (the same key and part as a K thread's
+      // tt, part; a fresh draft's V is written above with its K)
+      if constexpr (!K8V3) {
+        if (vthr && fresh_draft(base, tt) < 0) {
           *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32) = i8x8_to_f16(u32x2_t{R.v[0].x, R.v[0].y});
           *reinterpret_cast<half8_t*>(vb + tt * C::VROW + part * 32 + 16) = i8x8_to_f16(u32x2_t{R.v[0].z, R.v[0].w});
         }
@@ -1371,12 +1379,16 @@ __global__ __launch_bounds__(WideCfg<K8V3>::THREADS, WideCfg<K8V3>::WG_PER_CU) v
 // or WideCfg::ROWS for the wide kernel), and the workgroups a CU keeps
 // resident (the kernels' launch bounds).
 static bool use_wide(int head_dim, bool big) { return head_dim == 128 && !big; }
-static int rows_per_wg(int head_dim, bool k8v3, bool wide = false) {
-  if (wide) return k8v3 ? WideCfg<true>::ROWS : WideCfg<false>::ROWS;
+// rows: query rows per (sequence, KV head) -- group x max_queries; the wide
+// kernel takes 8-wave workgroups when they exceed one 4-wave block
+static bool wide_eight(int rows) { return rows > WideCfg<false, false>::ROWS; }
+static int rows_per_wg(int head_dim, bool k8v3, bool wide, int rows) {
+  if (wide) return wide_eight(rows) ? WideCfg<false, true>::ROWS : WideCfg<false, false>::ROWS;
   return 16 * (k8v3 ? 8 : 4) * (head_dim <= 64 ? 2 : 1);
 }
-static int wg_per_cu(bool k8v3, bool wide = false) {
-  return wide ? (k8v3 ? WideCfg<true>::WG_PER_CU : WideCfg<false>::WG_PER_CU) : (k8v3 ? 1 : 2);
+static int wg_per_cu(bool k8v3, bool wide, int rows) {
+  return wide ? (wide_eight(rows) ? WideCfg<false, true>::WG_PER_CU : WideCfg<false, false>::WG_PER_CU)
+              : (k8v3 ? 1 : 2);
 }
 
 // Combine of a split verify: one thread per (row, 4 dims) of a (sequence,
@@ -1502,13 +1514,13 @@ static int launch(VerifyArgs& a, hipStream_t stream) {
                  : launch_impl<D, K8V3, WIN, DENSE, false>(a, stream);
 }
 
-template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
-static int launch_wide(VerifyArgs& a, hipStream_t stream) {
-  using C = WideCfg<K8V3>;
+template <bool K8V3, bool DENSE, bool WIN, bool FRESH, bool EIGHT>
+static int launch_wide_impl(VerifyArgs& a, hipStream_t stream) {
+  using C = WideCfg<K8V3, EIGHT>;
   constexpr int smem = FRESH ? C::SMEM_WIN : C::SMEM;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE, WIN, FRESH>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_wide_kernel<K8V3, DENSE, WIN, FRESH, EIGHT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess) {
       set_error("s8kv_verify: cannot set the dynamic LDS size");
       return S8KV_ERR_LAUNCH;
@@ -1521,14 +1533,25 @@ static int launch_wide(VerifyArgs& a, hipStream_t stream) {
     set_error("s8kv_verify: grid too large");
     return S8KV_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE, WIN, FRESH>), dim3((unsigned)grid), dim3(C::THREADS), smem, stream,
-                     a);
+  hipLaunchKernelGGL((verify_wide_kernel<K8V3, DENSE, WIN, FRESH, EIGHT>), dim3((unsigned)grid), dim3(C::THREADS), smem,
+                     stream, a);
   if (a.splits > 1) {
     const int rc = check_launch("s8kv_verify");
     if (rc != S8KV_OK) return rc;
     return launch_combine<C::D, C::ROWS>(a, (int64_t)P * a.n_qblocks, stream);
   }
   return check_launch("s8kv_verify");
+}
+
+// 8-wave workgroups for paged calls with more than 128 query rows per
+// (sequence, KV head) (a batch-1 32-node tree at G 4 would leave half of
+// their waves idle: 13 % slower); the host sized n_qblocks and the split by
+// the same rule (rows_per_wg, wg_per_cu)
+template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
+static int launch_wide(VerifyArgs& a, hipStream_t stream) {
+  if constexpr (!DENSE)
+    if (wide_eight(a.group * a.max_queries)) return launch_wide_impl<K8V3, DENSE, WIN, FRESH, true>(a, stream);
+  return launch_wide_impl<K8V3, DENSE, WIN, FRESH, false>(a, stream);
 }
 
 }  // namespace verify
@@ -1558,9 +1581,9 @@ constexpr int kMinSplitKeys = 512;
 constexpr int kMaxSplitKeys = 1 << 20;
 constexpr int kMaxSplits = 1024;
 static std::atomic<int> g_verify_splits{0};  // 0: planned per call
-static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3, bool wide) {
+static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int keys, bool k8v3, bool wide, int rows) {
   const int64_t natural = (int64_t)batch * num_kv_heads * n_qblocks;
-  const int64_t resident = (int64_t)verify::wg_per_cu(k8v3, wide) * device_cus();
+  const int64_t resident = (int64_t)verify::wg_per_cu(k8v3, wide, rows) * device_cus();
   int64_t s = natural < resident ? (resident + natural - 1) / natural : 1;
   s = std::min<int64_t>(s, std::max(1, keys / kMinSplitKeys));
   s = std::max<int64_t>(s, ((int64_t)keys + kMaxSplitKeys - 1) / kMaxSplitKeys);
@@ -1569,9 +1592,9 @@ static int verify_plan_splits(int batch, int num_kv_heads, int n_qblocks, int ke
   return (int)std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
 }
 static int64_t verify_part_bytes(int batch, int num_kv_heads, int n_qblocks, int head_dim, int splits, bool k8v3,
-                                 bool wide) {
+                                 bool wide, int rows) {
   if (splits <= 1) return 0;
-  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim, k8v3, wide) *
+  return (int64_t)batch * num_kv_heads * n_qblocks * splits * verify::rows_per_wg(head_dim, k8v3, wide, rows) *
          (head_dim + 4) * 4;
 }
 
@@ -1585,12 +1608,13 @@ extern "C" int64_t s8kv_verify_workspace_size(int batch, int num_q_heads, int nu
   for (const bool k8v3 : {false, true}) {
     for (const bool wide : {false, true}) {
       if (wide && head_dim != 128) continue;
-      const int rows_wg = verify::rows_per_wg(head_dim, k8v3, wide);
-      const int n_qblocks = (num_q_heads / num_kv_heads * max_queries + rows_wg - 1) / rows_wg;
+      const int rows = num_q_heads / num_kv_heads * max_queries;
+      const int rows_wg = verify::rows_per_wg(head_dim, k8v3, wide, rows);
+      const int n_qblocks = (rows + rows_wg - 1) / rows_wg;
       need = std::max(need, verify_part_bytes(batch, num_kv_heads, n_qblocks, head_dim,
                                               verify_plan_splits(batch, num_kv_heads, n_qblocks, max_context_len,
-                                                                 k8v3, wide),
-                                              k8v3, wide));
+                                                                 k8v3, wide, rows),
+                                              k8v3, wide, rows));
     }
   }
   return need;
@@ -1607,8 +1631,9 @@ static int verify_use_workspace(verify::VerifyArgs& a, int head_dim, bool k8v3, 
                                 int64_t workspace_bytes) {
   const int keys = a.window > 0 ? (int)std::min<int64_t>(a.max_context_len, (int64_t)a.window + a.max_queries)
                                 : a.max_context_len;
-  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3, wide);
-  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3, wide);
+  const int rows = a.group * a.max_queries;
+  const int s = verify_plan_splits(a.batch, a.num_kv_heads, a.n_qblocks, keys, k8v3, wide, rows);
+  const int64_t need = verify_part_bytes(a.batch, a.num_kv_heads, a.n_qblocks, head_dim, s, k8v3, wide, rows);
   const bool fits = workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0;
   if (s > 1 && fits) {
     a.splits = s;
@@ -1674,7 +1699,7 @@ static int verify_setup(verify::VerifyArgs& a, const void* q, int batch, int num
   a.tree_mask = tree_mask;
   a.bs_log2 = log2i(block_size);
   a.max_context_len = max_context_len;
-  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, a.big));
+  const int rows_wg = verify::rows_per_wg(head_dim, k8v3, verify::use_wide(head_dim, a.big), a.group * max_queries);
   a.n_qblocks = (a.group * max_queries + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634 / __builtin_sqrt((double)head_dim));
   a.out = (_Float16*)out;
@@ -1900,7 +1925,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   a.max_queries = max_seqlen_q;
   a.max_context_len = max_seqlen_k;
   a.bs_log2 = 5;
-  const int rows_wg = verify::rows_per_wg(head_dim, false);
+  const int rows_wg = verify::rows_per_wg(head_dim, false, false, 0);
   a.n_qblocks = (a.group * max_seqlen_q + rows_wg - 1) / rows_wg;
   a.qscale = (float)((double)scale * 1.4426950408889634);  // K is not rotated: no 1/sqrt(D)
   a.cu_q = cu_seqlens_q;
@@ -1921,7 +1946,7 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   const bool wide = head_dim == 128 && (uintptr_t)q % 16 == 0 && q_stride_t % 8 == 0 && q_stride_h % 8 == 0 &&
                     (uintptr_t)out % 8 == 0 && o_stride_t % 4 == 0 && o_stride_h % 4 == 0;
   if (wide)
-    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false>::ROWS - 1) / verify::WideCfg<false>::ROWS;
+    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false, false>::ROWS - 1) / verify::WideCfg<false, false>::ROWS;
   if (window_left > 0) {  // query s sees keys (s + nk - nq - window_left, s + nk - nq]: window_left keys
     a.window = window_left - 1;  // the kernel's band: keys >= s + nk - nq - window
     if (wide) return verify::launch_wide<false, true, true>(a, s);
