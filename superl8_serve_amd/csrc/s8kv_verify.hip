@@ -837,10 +837,9 @@ __device__ __forceinline__ void split_pair(float w0, float w1, uint32_t& hi, uin
 template <bool K8V3, bool EIGHT>
 struct WideCfg {
   static constexpr int D = 128;
-  // EIGHT (paged calls with more than 128 query rows per sequence and KV
-  // head): 8 waves (256 rows) per workgroup, one workgroup per CU, so twice
-  // the rows share each tile's conversion (K8V3: code expansion); else (and
-  // dense inputs) 4 waves, two per CU
+  // EIGHT (calls with more than 128 query rows per sequence and KV head):
+  // 8 waves (256 rows) per workgroup, one workgroup per CU, so twice the rows
+  // share each tile's staging (K8V3: code expansion); else 4 waves, two per CU
   static constexpr int WAVES = EIGHT ? 8 : 4;
   static constexpr int WG_PER_CU = 8 / WAVES;
   static constexpr int THREADS = 64 * WAVES;
@@ -875,7 +874,6 @@ __global__ __launch_bounds__((WideCfg<K8V3, EIGHT>::THREADS), (WideCfg<K8V3, EIG
     VerifyArgs a) {
   static_assert(!(DENSE && K8V3), "dense inputs: fp16 K / V");
   static_assert(!FRESH || (WIN && !DENSE), "fresh drafts: a paged window verify");
-  static_assert(!(EIGHT && DENSE), "dense inputs: 4-wave workgroups");
   using C = WideCfg<K8V3, EIGHT>;
   constexpr int D = C::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1045,8 +1043,9 @@ __global__ __launch_bounds__((WideCfg<K8V3, EIGHT>::THREADS), (WideCfg<K8V3, EIG
       }
       return -1;
     };
-    // dense: two 16-byte fp16 K chunks and two V chunks per thread
-    constexpr int NCH = DENSE ? 2 : 1;
+    // dense: 512 16-byte fp16 K chunks and as many V chunks per tile, two
+    // each per thread of a 4-wave workgroup, one of an 8-wave one
+    constexpr int NCH = DENSE ? 512 / C::THREADS : 1;
     struct TileRegs {
       u32x4_t k[NCH], v[NCH];
       float s;
@@ -1543,14 +1542,13 @@ static int launch_wide_impl(VerifyArgs& a, hipStream_t stream) {
   return check_launch("s8kv_verify");
 }
 
-// 8-wave workgroups for paged calls with more than 128 query rows per
-// (sequence, KV head) (a batch-1 32-node tree at G 4 would leave half of
-// their waves idle: 13 % slower); the host sized n_qblocks and the split by
-// the same rule (rows_per_wg, wg_per_cu)
+// 8-wave workgroups for calls with more than 128 query rows per (sequence,
+// KV head) (a batch-1 32-node tree at G 4 would leave half of their waves
+// idle: 13 % slower); the host sized n_qblocks and the split by the same
+// rule (rows_per_wg, wg_per_cu)
 template <bool K8V3, bool DENSE = false, bool WIN = false, bool FRESH = false>
 static int launch_wide(VerifyArgs& a, hipStream_t stream) {
-  if constexpr (!DENSE)
-    if (wide_eight(a.group * a.max_queries)) return launch_wide_impl<K8V3, DENSE, WIN, FRESH, true>(a, stream);
+  if (wide_eight(a.group * a.max_queries)) return launch_wide_impl<K8V3, DENSE, WIN, FRESH, true>(a, stream);
   return launch_wide_impl<K8V3, DENSE, WIN, FRESH, false>(a, stream);
 }
 
@@ -1946,7 +1944,8 @@ extern "C" int s8kv_attn_varlen_f16(const void* q, const void* k, const void* v,
   const bool wide = head_dim == 128 && (uintptr_t)q % 16 == 0 && q_stride_t % 8 == 0 && q_stride_h % 8 == 0 &&
                     (uintptr_t)out % 8 == 0 && o_stride_t % 4 == 0 && o_stride_h % 4 == 0;
   if (wide)
-    a.n_qblocks = (a.group * max_seqlen_q + verify::WideCfg<false, false>::ROWS - 1) / verify::WideCfg<false, false>::ROWS;
+    a.n_qblocks = (a.group * max_seqlen_q + verify::rows_per_wg(128, false, true, a.group * max_seqlen_q) - 1) /
+                  verify::rows_per_wg(128, false, true, a.group * max_seqlen_q);
   if (window_left > 0) {  // query s sees keys (s + nk - nq - window_left, s + nk - nq]: window_left keys
     a.window = window_left - 1;  // the kernel's band: keys >= s + nk - nq - window
     if (wide) return verify::launch_wide<false, true, true>(a, s);
